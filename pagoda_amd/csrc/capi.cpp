@@ -1,0 +1,242 @@
+// capi.cpp — extern "C" surface: devices, matrices and the error channel.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/pagoda_hip.h"
+#include "common.h"
+#include "device.h"
+#include "quant.h"
+
+namespace pgd {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+const std::string& last_error() { return g_last_error; }
+
+}  // namespace pgd
+
+using namespace pgd;
+
+struct pgd_matrix {
+  pgd_dev* dev;
+  QMat m;
+};
+
+extern "C" {
+
+int pgd_last_error(char* buf, size_t len) {
+  const std::string& e = last_error();
+  if (buf && len) {
+    size_t n = e.size() < len - 1 ? e.size() : len - 1;
+    memcpy(buf, e.data(), n);
+    buf[n] = 0;
+  }
+  return (int)e.size();
+}
+
+int pgd_version(void) { return 100; }
+
+int pgd_device_open(const char* spec, pgd_dev** out) {
+  return guard([&] {
+    PGD_CHECK(spec && out, kErrArg, "pgd_device_open: null argument");
+    std::string s(spec);
+    int ordinal = 0;
+    if (s == "hip") {
+      ordinal = 0;
+    } else if (s.rfind("hip:", 0) == 0 && s.size() > 4) {
+      char* end = nullptr;
+      long v = strtol(s.c_str() + 4, &end, 10);
+      PGD_CHECK(end && *end == 0 && v >= 0, kErrArg, "bad PAGODA_DEVICE index in \"" + s + "\"");
+      ordinal = (int)v;
+    } else {
+      throw Error{kErrArg, "unknown device spec \"" + s + "\" (want hip or hip:N)"};
+    }
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    PGD_CHECK(e == hipSuccess && count > 0, kErrDevice, "no HIP device available");
+    PGD_CHECK(ordinal < count, kErrDevice, "no HIP device " + std::to_string(ordinal));
+    *out = new pgd_dev(ordinal);
+  });
+}
+
+int pgd_device_close(pgd_dev* dev) {
+  return guard([&] {
+    if (!dev) return;
+    delete dev;
+  });
+}
+
+int pgd_device_sync(pgd_dev* dev) {
+  return guard([&] {
+    PGD_CHECK(dev, kErrArg, "null device");
+    DeviceScope scope(dev);
+    PGD_HIP(hipStreamSynchronize(dev->stream));
+  });
+}
+
+void* pgd_device_stream(pgd_dev* dev) { return dev ? (void*)dev->stream : nullptr; }
+
+int pgd_device_malloc(pgd_dev* dev, size_t bytes, void** out) {
+  return guard([&] {
+    PGD_CHECK(dev && out, kErrArg, "null argument");
+    DeviceScope scope(dev);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    PGD_CHECK(e == hipSuccess, kErrAlloc, std::string("hipMalloc: ") + hipGetErrorString(e));
+    *out = p;
+  });
+}
+
+int pgd_device_free(pgd_dev* dev, void* ptr) {
+  return guard([&] {
+    PGD_CHECK(dev, kErrArg, "null device");
+    DeviceScope scope(dev);
+    if (ptr) PGD_HIP(hipFree(ptr));
+  });
+}
+
+int pgd_device_memcpy(pgd_dev* dev, void* dst, const void* src, size_t bytes, int kind) {
+  return guard([&] {
+    PGD_CHECK(dev, kErrArg, "null device");
+    PGD_CHECK(kind >= 0 && kind <= 2, kErrArg, "memcpy kind");
+    DeviceScope scope(dev);
+    hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    if (bytes) PGD_HIP(hipMemcpyAsync(dst, src, bytes, k, dev->stream));
+    PGD_HIP(hipStreamSynchronize(dev->stream));
+  });
+}
+
+static int new_matrix(pgd_dev* dev, int fmt, int n_out, int n_in, pgd_matrix** out, pgd_matrix** held) {
+  PGD_CHECK(dev && out, kErrArg, "null argument");
+  auto* m = new pgd_matrix{dev, QMat{}};
+  *held = m;
+  qmat_alloc(m->m, fmt, n_out, n_in);
+  return 0;
+}
+
+int pgd_matrix_upload_a8(pgd_dev* dev, const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
+                         int n_out, int n_in, pgd_matrix** out) {
+  pgd_matrix* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(packed && scales && biases, kErrArg, "null argument");
+    DeviceScope scope(dev);
+    new_matrix(dev, FMT_A8, n_out, n_in, out, &held);
+    qmat_upload_a8(held->m, packed, scales, biases, dev->stream);
+    *out = held;
+  });
+  if (rc && held) pgd_matrix_free(held);
+  return rc;
+}
+
+static int upload_kq(pgd_dev* dev, int fmt, const void* blocks, int n_out, int n_in, pgd_matrix** out) {
+  pgd_matrix* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(blocks, kErrArg, "null argument");
+    DeviceScope scope(dev);
+    new_matrix(dev, fmt, n_out, n_in, out, &held);
+    qmat_upload_kq(held->m, (const uint8_t*)blocks, dev->stream);
+    *out = held;
+  });
+  if (rc && held) pgd_matrix_free(held);
+  return rc;
+}
+
+int pgd_matrix_upload_q4k(pgd_dev* dev, const void* blocks, int n_out, int n_in, pgd_matrix** out) {
+  return upload_kq(dev, FMT_Q4K, blocks, n_out, n_in, out);
+}
+
+int pgd_matrix_upload_q6k(pgd_dev* dev, const void* blocks, int n_out, int n_in, pgd_matrix** out) {
+  return upload_kq(dev, FMT_Q6K, blocks, n_out, n_in, out);
+}
+
+int pgd_matrix_synth(pgd_dev* dev, int fmt, int n_out, int n_in, uint64_t seed, uint64_t key, float std,
+                     pgd_matrix** out) {
+  pgd_matrix* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(fmt >= 0 && fmt <= 2, kErrFormat, "unknown matrix format");
+    DeviceScope scope(dev);
+    new_matrix(dev, fmt, n_out, n_in, out, &held);
+    qmat_synth(held->m, seed, key, std, dev->stream);
+    PGD_HIP(hipStreamSynchronize(dev->stream));
+    *out = held;
+  });
+  if (rc && held) pgd_matrix_free(held);
+  return rc;
+}
+
+int pgd_matrix_free(pgd_matrix* m) {
+  return guard([&] {
+    if (!m) return;
+    DeviceScope scope(m->dev);
+    (void)hipStreamSynchronize(m->dev->stream);
+    qmat_free(m->m);
+    delete m;
+  });
+}
+
+int pgd_matrix_info(const pgd_matrix* m, int* fmt, int* n_out, int* n_in, size_t* dev_bytes, double* algo) {
+  return guard([&] {
+    PGD_CHECK(m, kErrArg, "null matrix");
+    if (fmt) *fmt = m->m.fmt;
+    if (n_out) *n_out = m->m.n_out;
+    if (n_in) *n_in = m->m.n_in;
+    if (dev_bytes) *dev_bytes = m->m.bytes;
+    if (algo) *algo = qmat_algo_bytes(m->m);
+  });
+}
+
+int pgd_matrix_dequant(const pgd_matrix* m, int row0, int rows, float* out) {
+  return guard([&] {
+    PGD_CHECK(m && out, kErrArg, "null argument");
+    PGD_CHECK(row0 >= 0 && rows >= 0 && row0 + rows <= m->m.n_out, kErrShape, "dequant row range");
+    if (!rows) return;
+    DeviceScope scope(m->dev);
+    DevBuf buf((size_t)rows * m->m.n_in * 4);
+    qmat_dequant(m->m, row0, rows, (float*)buf.p, m->dev->stream);
+    PGD_HIP(hipMemcpyAsync(out, buf.p, buf.bytes, hipMemcpyDeviceToHost, m->dev->stream));
+    PGD_HIP(hipStreamSynchronize(m->dev->stream));
+  });
+}
+
+int pgd_matrix_gemv(const pgd_matrix* m, const float* x, int nrows, float* y) {
+  return guard([&] {
+    PGD_CHECK(m && x && y, kErrArg, "null argument");
+    PGD_CHECK(nrows >= 1 && nrows <= 64, kErrShape, "gemv rows must be in 1..64");
+    DeviceScope scope(m->dev);
+    int ldx = (m->m.n_in + 7) & ~7;
+    DevBuf xb((size_t)nrows * ldx * 4), yb((size_t)nrows * m->m.n_out * 4);
+    hipStream_t s = m->dev->stream;
+    PGD_HIP(hipMemcpy2DAsync(xb.p, (size_t)ldx * 4, x, (size_t)m->m.n_in * 4, (size_t)m->m.n_in * 4, nrows,
+                             hipMemcpyHostToDevice, s));
+    qmat_gemv(m->m, xb.p, 0, ldx, nrows, (float*)yb.p, m->m.n_out, nullptr, 0, s);
+    PGD_HIP(hipMemcpyAsync(y, yb.p, yb.bytes, hipMemcpyDeviceToHost, s));
+    PGD_HIP(hipStreamSynchronize(s));
+  });
+}
+
+int pgd_matrix_gemv_dev(const pgd_matrix* m, const void* x, int x_f16, int ldx, int nrows, float* y, int ldy,
+                        const float* res, int ldres) {
+  return guard([&] {
+    PGD_CHECK(m && x && y, kErrArg, "null argument");
+    PGD_CHECK(ldy >= m->m.n_out && (!res || ldres >= m->m.n_out), kErrShape, "gemv output stride");
+    DeviceScope scope(m->dev);
+    qmat_gemv(m->m, x, x_f16, ldx, nrows, y, ldy, res, ldres, m->dev->stream);
+  });
+}
+
+int pgd_matrix_gemv_swiglu_dev(const pgd_matrix* gate, const pgd_matrix* up, const float* x, int ldx, int nrows,
+                               float* mid, int ldm) {
+  return guard([&] {
+    PGD_CHECK(gate && up && x && mid, kErrArg, "null argument");
+    PGD_CHECK(gate->dev == up->dev, kErrArg, "gate and up live on different devices");
+    PGD_CHECK(ldm >= gate->m.n_out, kErrShape, "swiglu output stride");
+    DeviceScope scope(gate->dev);
+    qmat_gemv_swiglu(gate->m, up->m, x, ldx, nrows, mid, ldm, gate->dev->stream);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// quant.h — device layout of quantized matrices and the GEMV launchers.
+//
+// Every matrix is [n_out, n_in] with n_in contiguous. One device allocation
+// per matrix holds structure-of-arrays planes so each wave streams one plane
+// with 128-bit loads:
+//
+//   A8  (MLX affine, group 64):  codes u8 [n_out][n_in]        (the packed u32 words, same bytes)
+//                                sb    u32 [n_out][n_in/64]     bf16 scale | bf16 bias << 16
+//   Q4K (GGML block_q4_K):       qs    u8 [n_out][nsb*128]      the 128 nibble bytes of each block
+//                                hdr   16B [n_out][nsb]         d, dmin (f16) + 12 packed scale bytes
+//   Q6K (GGML block_q6_K):       ql    u8 [n_out][nsb*128]
+//                                qh    u8 [n_out][nsb*64]
+//                                sc    i8 [n_out][nsb*16]
+//                                d     f16 [n_out][nsb]
+//
+// The planes hold exactly the bytes of the source blocks (144 B / 210 B per
+// 256 weights; 1.0625 B per A8 weight), only regrouped.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pgd {
+
+enum Fmt : int { FMT_A8 = 0, FMT_Q4K = 1, FMT_Q6K = 2 };
+
+struct QMat {
+  int fmt = FMT_A8;
+  int n_out = 0, n_in = 0, nsb = 0;
+  uint8_t* base = nullptr;  // owning device allocation
+  size_t bytes = 0;
+  // plane pointers (into base)
+  uint8_t* p0 = nullptr;  // A8 codes | Q4K qs | Q6K ql
+  uint8_t* p1 = nullptr;  // A8 sb    | Q4K hdr | Q6K qh
+  uint8_t* p2 = nullptr;  //                      Q6K sc
+  uint8_t* p3 = nullptr;  //                      Q6K d
+};
+
+// algorithmic bytes of the weights (what a GEMV must stream at least once;
+// unpadded n_in as the measurement plan defines it)
+double qmat_algo_bytes(const QMat& m);
+
+// allocate planes for a matrix (device memory, uninitialised)
+void qmat_alloc(QMat& m, int fmt, int n_out, int n_in);
+void qmat_free(QMat& m);
+
+// host source blocks -> device planes
+void qmat_upload_a8(QMat& m, const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
+                    hipStream_t s);
+void qmat_upload_kq(QMat& m, const uint8_t* blocks, hipStream_t s);
+
+// dequantize rows [row0, row0+rows) to f32 [rows, n_in]; bit-exact to the
+// host formulas (A8: bias + scale*code; Q4K: d1*q - m1; Q6K: d*sc*q).
+void qmat_dequant(const QMat& m, int row0, int rows, float* out, hipStream_t s);
+
+// GEMV / skinny GEMM: y[r, n] = sum_k W[n, k] * x[r, k] for r < nrows.
+// x is f32 (x_f16 == 0) or IEEE f16 (x_f16 == 1), row stride ldx elements.
+// res (nullable): y = res + W.x (res may alias y).
+void qmat_gemv(const QMat& m, const void* x, int x_f16, int ldx, int nrows, float* y, int ldy,
+               const float* res, int ldres, hipStream_t s);
+
+// fused SwiGLU: mid[r, n] = silu(gate.x) * (up.x)
+void qmat_gemv_swiglu(const QMat& gate, const QMat& up, const float* x, int ldx, int nrows, float* mid,
+                      int ldm, hipStream_t s);
+
+// embedding rows: out[r, :] = dequant(W[ids[r], :]) (ids on device)
+void qmat_embed(const QMat& m, const uint32_t* ids, int nrows, float* out, int ldo, hipStream_t s);
+
+// synthetic init: fill the planes with the quantized form of seeded
+// N(0, std) weights (counter-based generator, reproduced bit for bit by the
+// CPU checker).
+void qmat_synth(QMat& m, uint64_t seed, uint64_t key, float std, hipStream_t s);
+
+// seeded f32 vectors
+void synth_normal_f32(float* out, size_t n, uint64_t seed, uint64_t key, float scale, hipStream_t s);
+void synth_uniform_f32(float* out, size_t n, uint64_t seed, uint64_t key, float scale, hipStream_t s);
+void fill_f32(float* out, size_t n, float v, hipStream_t s);
+
+}  // namespace pgd

@@ -1,0 +1,179 @@
+"""GPU parity of the quantized formats and GEMVs, through the C ABI.
+
+Bars: dequantized weights bit-exact to the oracle; GEMV within 1e-3 of an
+fp64 dot over the oracle-dequantized weights (max error relative to max
+|y|), batched rows bitwise equal to single-row calls.
+"""
+import numpy as np
+import pytest
+
+from oracle import pyoracle as ora
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3
+
+
+def rel_err(y, ref):
+    return float(np.abs(y.astype(np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def make(dev, fmt, w):
+    from pagoda_amd import Matrix
+    from pagoda_amd.matrix import FMT_A8, FMT_Q4K
+
+    n_out, n_in = w.shape
+    if fmt == FMT_A8:
+        p, s, b = ora.a8_quantize(w)
+        return Matrix.upload_a8(dev, p, s, b, n_out, n_in), ora.a8_dequant(p, s, b, n_out, n_in)
+    if fmt == FMT_Q4K:
+        blk = ora.q4k_quantize(w)
+        return Matrix.upload_kq(dev, fmt, blk, n_out, n_in), ora.q4k_dequant(blk, n_out, n_in)
+    blk = ora.q6k_quantize(w)
+    return Matrix.upload_kq(dev, fmt, blk, n_out, n_in), ora.q6k_dequant(blk, n_out, n_in)
+
+
+FMTS = [0, 1, 2]
+SHAPES = [(64, 256), (37, 896), (130, 4864 // 4), (96, 1152)]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("shape", SHAPES)
+def test_dequant_bit_exact(dev, fmt, shape):
+    n_out, n_in = shape
+    if fmt == 0 and n_in % 64:
+        pytest.skip("A8 needs n_in % 64 == 0")
+    rng = np.random.default_rng(n_out * 7 + n_in + fmt)
+    w = rng.normal(0, 0.02, shape).astype(np.float32)
+    m, ref = make(dev, fmt, w)
+    got = m.dequant()
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # row window
+    np.testing.assert_array_equal(m.dequant(3, 5), ref[3:8])
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("shape", [(64, 256), (300, 896), (129, 1216), (64, 4864)])
+def test_synth_on_device_matches_cpu_quantizer(dev, fmt, shape):
+    """The device generator reproduces the CPU generator + quantizer bit for
+    bit (same seeded weights on both sides of every parity test)."""
+    from pagoda_amd import Matrix
+
+    n_out, n_in = shape
+    if fmt == 0 and n_in % 64:
+        pytest.skip("A8 needs n_in % 64 == 0")
+    seed, key = 1234, (5 << 8) | 12
+    m = Matrix.synth(dev, fmt, n_out, n_in, seed, key, 0.02)
+    w = ora.synth_normal(seed, key, n_out * n_in, 0.02).reshape(n_out, n_in)
+    _, ref = make(dev, fmt, w)
+    np.testing.assert_array_equal(m.dequant().view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("shape", [(64, 256), (333, 896), (77, 4864), (1152, 896)])
+@pytest.mark.parametrize("rows", [1, 3, 8, 13])
+def test_gemv_matches_fp64(dev, fmt, shape, rows):
+    n_out, n_in = shape
+    if fmt == 0 and n_in % 64:
+        pytest.skip("A8 needs n_in % 64 == 0")
+    rng = np.random.default_rng(fmt * 1000 + rows)
+    w = rng.normal(0, 0.02, shape).astype(np.float32)
+    m, deq = make(dev, fmt, w)
+    x = rng.normal(0, 1, (rows, n_in)).astype(np.float32)
+    y = m.gemv(x)
+    ref = x.astype(np.float64) @ deq.astype(np.float64).T
+    assert rel_err(y, ref) < GEMV_TOL
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_batched_rows_bitwise_equal_serial(dev, fmt):
+    """qwen3_gemv.rs:1115-1167: a batched step equals per-row GEMVs exactly."""
+    rng = np.random.default_rng(9)
+    w = rng.normal(0, 0.02, (200, 1024)).astype(np.float32)
+    m, _ = make(dev, fmt, w)
+    x = rng.normal(0, 1, (21, 1024)).astype(np.float32)
+    serial = np.stack([m.gemv(x[i]) for i in range(21)])
+    for rows in (2, 4, 8, 13, 21):
+        got = m.gemv(x[:rows])
+        np.testing.assert_array_equal(got.view(np.uint32), serial[:rows].view(np.uint32))
+
+
+def test_reference_gemv_patterns(dev):
+    """qwen3_gemv.rs:1038-1112: closed-form A8 GEMVs."""
+    from pagoda_amd import Matrix
+
+    n_in = 256
+    # code = i % 256, scale .5, bias -1, x = 1  (tol 1e-4)
+    codes = (np.arange(n_in) % 256).astype(np.uint8)
+    s = np.full(4, ora.f32_to_bf16(0.5), np.uint16)
+    b = np.full(4, ora.f32_to_bf16(-1.0), np.uint16)
+    m = Matrix.upload_a8(dev, codes.view(np.uint32), s, b, 1, n_in)
+    y = m.gemv(np.ones(n_in, np.float32))
+    expect = sum(-1.0 + 0.5 * (i % 256) for i in range(n_in))
+    assert abs(y[0] - expect) < 1e-4
+    # multi-row: code = (r*3+i) % 256, scale .25, bias 1, x = i*0.01 (tol 1e-1)
+    n_out = 8
+    codes = np.array([[(r * 3 + i) % 256 for i in range(n_in)] for r in range(n_out)], np.uint8)
+    s = np.full(n_out * 4, ora.f32_to_bf16(0.25), np.uint16)
+    b = np.full(n_out * 4, ora.f32_to_bf16(1.0), np.uint16)
+    m = Matrix.upload_a8(dev, codes.reshape(-1).view(np.uint32), s, b, n_out, n_in)
+    x = (np.arange(n_in) * 0.01).astype(np.float32)
+    y = m.gemv(x)
+    for r in range(n_out):
+        e = sum((1.0 + 0.25 * ((r * 3 + i) % 256)) * x[i] for i in range(n_in))
+        assert abs(y[r] - e) < 1e-1
+
+
+def test_shared_x_two_matrices_and_residual(dev):
+    """qwen3_gemv.rs:1061-1085 and 1964-2055: same x through two matrices,
+    SwiGLU epilogue and residual epilogue."""
+    from pagoda_amd import Matrix
+
+    n_out, n_in = 128, 256
+    a_pk = np.full(n_out * n_in // 4, 0x01020304, np.uint32)
+    b_pk = np.full(n_out * n_in // 4, 0x04030201, np.uint32)
+    s = np.full(n_out * 4, ora.f32_to_bf16(0.01), np.uint16)
+    bb = np.full(n_out * 4, ora.f32_to_bf16(0.1), np.uint16)
+    A = Matrix.upload_a8(dev, a_pk, s, bb, n_out, n_in)
+    B = Matrix.upload_a8(dev, b_pk, s, bb, n_out, n_in)
+    x = np.full(n_in, 0.5, np.float32)
+    ya, yb = A.gemv(x), B.gemv(x)
+    deq_a = ora.a8_dequant(a_pk, s, bb, n_out, n_in)
+    np.testing.assert_allclose(ya, deq_a.astype(np.float64) @ x, atol=1e-4)
+    # device-side swiglu and residual
+    xd = dev.upload(np.pad(x, (0, 0)))
+    mid = dev.alloc(n_out * 4)
+    Matrix.gemv_swiglu_dev(A, B, xd, n_in, 1, mid, n_out)
+    got = dev.download(mid, (n_out,), np.float32)
+    np.testing.assert_allclose(got, ya / (1 + np.exp(-ya)) * yb, rtol=1e-5, atol=1e-5)
+    res = np.arange(n_out, dtype=np.float32)
+    rd = dev.upload(res)
+    A.gemv_dev(xd, n_in, 1, rd, n_out, res_ptr=rd, ldres=n_out)  # aliasing residual
+    got = dev.download(rd, (n_out,), np.float32)
+    np.testing.assert_allclose(got, res + ya, rtol=1e-6, atol=1e-5)
+    for p in (xd, mid, rd):
+        dev.free(p)
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("shape", [(4864, 896), (896, 4864), (1152, 896)])
+@pytest.mark.parametrize("rows", [1, 4, 8, 16, 32, 64])
+def test_config2_sweep_f16_activations(dev, fmt, shape, rows):
+    """Config 2: Q4K/Q6K, x fp16 N(0,1), ragged rows, vs CPU-dequant fp32 GEMV
+    (evaluated in fp64). shape is (N, K)."""
+    from pagoda_amd import Matrix
+
+    n_out, n_in = shape
+    seed = 77
+    m = Matrix.synth(dev, fmt, n_out, n_in, seed, fmt, 0.02)
+    deq = m.dequant()
+    rng = np.random.default_rng(rows)
+    x16 = rng.normal(0, 1, (rows, n_in)).astype(np.float16)
+    xd = dev.upload(x16)
+    yd = dev.alloc(rows * n_out * 4)
+    m.gemv_dev(xd, n_in, rows, yd, n_out, x_f16=True)
+    y = dev.download(yd, (rows, n_out), np.float32)
+    ref = x16.astype(np.float64) @ deq.astype(np.float64).T
+    assert rel_err(y, ref) < GEMV_TOL
+    dev.free(xd)
+    dev.free(yd)
