@@ -56,6 +56,14 @@ int pgd_device_free(pgd_dev* dev, void* ptr);
 /* kind: 0 host->device, 1 device->host, 2 device->device (synchronous) */
 int pgd_device_memcpy(pgd_dev* dev, void* dst, const void* src, size_t bytes, int kind);
 
+/* ---- timing: HIP events recorded on the device handle's stream --------- */
+typedef struct pgd_event pgd_event;
+int pgd_event_new(pgd_dev* dev, pgd_event** out);
+int pgd_event_record(pgd_event* ev);
+/* Waits for `end`, then writes the elapsed milliseconds between the two. */
+int pgd_event_elapsed_ms(pgd_event* start, pgd_event* end, float* ms);
+int pgd_event_free(pgd_event* ev);
+
 /* ---- quantized matrices ---------------------------------------------------
  * Replaces QuantMatrix::upload (pagoda-hf/src/qwen3_gemv.rs:658-705):
  * MLX affine 8-bit group 64, packed u32 [n_out, n_in/4] (codes little

@@ -7,7 +7,7 @@ and the model/session surface of the reference's ModelEngine/ModelSession
 (pagoda/src/model.rs:66-195).
 """
 from ._lib import LIB_PATH, PagodaError, lib  # noqa: F401
-from .device import Device, device_from_env  # noqa: F401
+from .device import Device, Event, device_from_env  # noqa: F401
 from .matrix import Matrix  # noqa: F401
 
 __all__ = ["LIB_PATH", "PagodaError", "lib", "Device", "device_from_env", "Matrix"]

@@ -26,6 +26,11 @@ struct pgd_matrix {
   QMat m;
 };
 
+struct pgd_event {
+  pgd_dev* dev;
+  hipEvent_t ev;
+};
+
 extern "C" {
 
 int pgd_last_error(char* buf, size_t len) {
@@ -107,6 +112,42 @@ int pgd_device_memcpy(pgd_dev* dev, void* dst, const void* src, size_t bytes, in
     hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
     if (bytes) PGD_HIP(hipMemcpyAsync(dst, src, bytes, k, dev->stream));
     PGD_HIP(hipStreamSynchronize(dev->stream));
+  });
+}
+
+int pgd_event_new(pgd_dev* dev, pgd_event** out) {
+  return guard([&] {
+    PGD_CHECK(dev && out, kErrArg, "null argument");
+    DeviceScope scope(dev);
+    hipEvent_t e;
+    PGD_HIP(hipEventCreate(&e));
+    *out = new pgd_event{dev, e};
+  });
+}
+
+int pgd_event_record(pgd_event* ev) {
+  return guard([&] {
+    PGD_CHECK(ev, kErrArg, "null event");
+    DeviceScope scope(ev->dev);
+    PGD_HIP(hipEventRecord(ev->ev, ev->dev->stream));
+  });
+}
+
+int pgd_event_elapsed_ms(pgd_event* start, pgd_event* end, float* ms) {
+  return guard([&] {
+    PGD_CHECK(start && end && ms, kErrArg, "null argument");
+    DeviceScope scope(end->dev);
+    PGD_HIP(hipEventSynchronize(end->ev));
+    PGD_HIP(hipEventElapsedTime(ms, start->ev, end->ev));
+  });
+}
+
+int pgd_event_free(pgd_event* ev) {
+  return guard([&] {
+    if (!ev) return;
+    DeviceScope scope(ev->dev);
+    (void)hipEventDestroy(ev->ev);
+    delete ev;
   });
 }
 

@@ -1,0 +1,350 @@
+// gemv_impl.h — GEMV kernel templates shared by the per-format
+// instantiation files (gemv_a8.hip, gemv_q4k.hip, gemv_q6k.hip).
+//
+// Dequant-in-register GEMV / skinny GEMM for MLX affine-8 (group 64) and
+// GGML Q4_K / Q6_K matrices.
+//
+// GEMV mapping (wave64): a wave owns ROWS consecutive output rows. A row is
+// cut into 16-byte chunks of its main plane (A8 codes / Q4K qs / Q6K ql);
+// lane l takes chunks l, l+64, ... so every load instruction of the wave
+// reads 1 KiB of one row contiguously (128-bit per lane). The activation
+// values a chunk needs are loaded once per chunk and reused for the ROWS
+// rows; the per-row partials are folded with a fixed wave butterfly, so the
+// result is deterministic and the same for every batch size (each batch row
+// runs the identical instruction sequence).
+//
+// Reference kernels whose results this reproduces: affine_gemv / gemm4 /
+// gemv2_silu / gemv_res (pagoda-hf/src/qwen3_gemv.rs:54-306, 414-567);
+// Q4K/Q6K have no reference GPU kernel (candle QMatMul on CPU,
+// pagoda-hf/src/qwen2_gguf.rs:271-289).
+#pragma once
+#include <algorithm>
+
+#include "common.h"
+#include "quant.h"
+
+namespace pgd {
+namespace gemv {
+
+
+struct GemvArgs {
+  const uint8_t* p0;
+  const uint8_t* p1;
+  const uint8_t* p2;
+  const uint8_t* p3;
+  const uint8_t* u0;  // second matrix (SwiGLU up)
+  const uint8_t* u1;
+  const uint8_t* u2;
+  const uint8_t* u3;
+  int n_out, n_in, nsb;
+  const void* x;
+  int ldx;
+  float* y;
+  int ldy;
+  const float* res;
+  int ldres;
+};
+
+enum { EPI_STORE = 0, EPI_RES = 1, EPI_SWIGLU = 2 };
+
+// ---- activation loads ------------------------------------------------------
+template <bool XF16>
+__device__ inline void load_x16(const void* x, size_t off, float* v) {
+  if constexpr (XF16) {
+    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + off);
+    uint4 a = p[0], b = p[1];
+    uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = f16_to_f32(w[i] & 0xffffu);
+      v[2 * i + 1] = f16_to_f32(w[i] >> 16);
+    }
+  } else {
+    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float4 f = p[i];
+      v[4 * i] = f.x;
+      v[4 * i + 1] = f.y;
+      v[4 * i + 2] = f.z;
+      v[4 * i + 3] = f.w;
+    }
+  }
+}
+
+__device__ inline float sum16(const float* v) {
+  float s = v[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) s += v[i];
+  return s;
+}
+
+__device__ inline uint32_t byte_of(uint4 q, int i) {
+  uint32_t w = i < 4 ? q.x : (i < 8 ? q.y : (i < 12 ? q.z : q.w));
+  return (w >> (8 * (i & 3))) & 255u;
+}
+
+// ---- per-format chunk logic ------------------------------------------------
+// A8: chunk p = codes [16p, 16p+16) of a row; group p/4.
+struct A8 {
+  struct W {
+    uint4 q;
+    uint32_t sb;
+  };
+  static __device__ inline int chunks(const GemvArgs& a) { return a.n_in >> 4; }
+  static __device__ inline bool pos(const GemvArgs& a, int p, int& lo, int& hi) {
+    lo = p << 4;
+    hi = -1;
+    return true;
+  }
+  static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t*, const uint8_t*,
+                                  const GemvArgs& a, int row, int p) {
+    W w;
+    w.q = *reinterpret_cast<const uint4*>(c0 + (size_t)row * a.n_in + ((size_t)p << 4));
+    w.sb = reinterpret_cast<const uint32_t*>(c1)[(size_t)row * (a.n_in >> 6) + (p >> 2)];
+    return w;
+  }
+  // pagoda-hf/src/qwen3_gemv.rs:96-99: r = fma(scale, sum(code*x), fma(sum(x), bias, r))
+  static __device__ inline float acc(float r, const W& w, const float* xl, const float*, float sl, float) {
+    float d = (float)byte_of(w.q, 0) * xl[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) d = fmaf((float)byte_of(w.q, i), xl[i], d);
+    float s = bf16_to_f32(w.sb & 0xffffu), b = bf16_to_f32(w.sb >> 16);
+    return fmaf(s, d, fmaf(sl, b, r));
+  }
+};
+
+// Q4K: chunk p = qs bytes [16p, 16p+16): block p/8, part p%8 -> 64-group
+// j = part/2, half h = part%2. Low nibbles are elements 64j+16h+i of
+// sub-block 2j, high nibbles 64j+32+16h+i of sub-block 2j+1.
+struct Q4K {
+  struct W {
+    uint4 q;
+    uint4 hdr;
+  };
+  static __device__ inline int chunks(const GemvArgs& a) { return a.nsb << 3; }
+  static __device__ inline bool pos(const GemvArgs& a, int p, int& lo, int& hi) {
+    int sb = p >> 3, part = p & 7;
+    lo = (sb << 8) + ((part >> 1) << 6) + ((part & 1) << 4);
+    hi = lo + 32;
+    if (hi >= a.n_in) hi = -1;
+    return lo < a.n_in;
+  }
+  static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t*, const uint8_t*,
+                                  const GemvArgs& a, int row, int p) {
+    W w;
+    w.q = *reinterpret_cast<const uint4*>(c0 + (size_t)row * a.nsb * 128 + ((size_t)p << 4));
+    w.hdr = reinterpret_cast<const uint4*>(c1)[(size_t)row * a.nsb + (p >> 3)];
+    return w;
+  }
+  static __device__ inline void scale_min(const uint4& hdr, int is, float& sc, float& m) {
+    // 12 scale bytes are hdr bytes 4..15 (hdr.y, hdr.z, hdr.w)
+    uint4 s = make_uint4(hdr.y, hdr.z, hdr.w, 0u);
+    uint32_t a, b;
+    if (is < 4) {
+      a = byte_of(s, is) & 63u;
+      b = byte_of(s, is + 4) & 63u;
+    } else {
+      a = (byte_of(s, is + 4) & 0xFu) | ((byte_of(s, is - 4) >> 6) << 4);
+      b = (byte_of(s, is + 4) >> 4) | ((byte_of(s, is) >> 6) << 4);
+    }
+    sc = (float)a;
+    m = (float)b;
+  }
+  static __device__ inline float acc(float r, const W& w, const float* xl, const float* xh, float sl, float sh,
+                                     int p, bool has_hi) {
+    int j = (p & 7) >> 1;
+    float d = f16_to_f32(w.hdr.x & 0xffffu), dmin = f16_to_f32(w.hdr.x >> 16);
+    float sc0, m0, sc1, m1;
+    scale_min(w.hdr, 2 * j, sc0, m0);
+    scale_min(w.hdr, 2 * j + 1, sc1, m1);
+    float dl = 0.0f, dh = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      uint32_t b = byte_of(w.q, i);
+      dl = fmaf((float)(b & 15u), xl[i], dl);
+      dh = fmaf((float)(b >> 4), xh[i], dh);
+    }
+    r = fmaf(d * sc0, dl, r);
+    r = fmaf(-(dmin * m0), sl, r);
+    if (has_hi) {
+      r = fmaf(d * sc1, dh, r);
+      r = fmaf(-(dmin * m1), sh, r);
+    }
+    return r;
+  }
+};
+
+// Q6K: chunk p = ql bytes [16p, 16p+16): block p/8, part p%8 -> half
+// n = part/4, c = part%4. Low nibbles: elements 128n+16c+i, high nibbles
+// 128n+64+16c+i; the two high bits come from qh byte 32n+16(c&1)+i at shift
+// 2(c>>1) (low) and 4+2(c>>1) (high); scales sc[8n+c] and sc[8n+4+c].
+struct Q6K {
+  struct W {
+    uint4 ql;
+    uint4 qh;
+    float s_lo, s_hi;
+  };
+  static __device__ inline int chunks(const GemvArgs& a) { return a.nsb << 3; }
+  static __device__ inline bool pos(const GemvArgs& a, int p, int& lo, int& hi) {
+    int sb = p >> 3, part = p & 7;
+    lo = (sb << 8) + ((part >> 2) << 7) + ((part & 3) << 4);
+    hi = lo + 64;
+    if (hi >= a.n_in) hi = -1;
+    return lo < a.n_in;
+  }
+  static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t* c2, const uint8_t* c3,
+                                  const GemvArgs& a, int row, int p) {
+    int sb = p >> 3, part = p & 7, n = part >> 2, c = part & 3;
+    W w;
+    w.ql = *reinterpret_cast<const uint4*>(c0 + (size_t)row * a.nsb * 128 + ((size_t)p << 4));
+    w.qh = *reinterpret_cast<const uint4*>(c1 + (size_t)row * a.nsb * 64 + sb * 64 + 32 * n + 16 * (c & 1));
+    const int8_t* sc = reinterpret_cast<const int8_t*>(c2) + (size_t)row * a.nsb * 16 + sb * 16 + 8 * n + c;
+    float d = f16_to_f32(reinterpret_cast<const uint16_t*>(c3)[(size_t)row * a.nsb + sb]);
+    w.s_lo = d * (float)sc[0];
+    w.s_hi = d * (float)sc[4];
+    return w;
+  }
+  static __device__ inline float acc(float r, const W& w, const float* xl, const float* xh, float sl, float sh,
+                                     int p, bool has_hi) {
+    int c = p & 3;
+    int shl = 2 * (c >> 1), shh = 4 + 2 * (c >> 1);
+    float dl = 0.0f, dh = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      uint32_t l = byte_of(w.ql, i), h = byte_of(w.qh, i);
+      uint32_t ql = (l & 15u) | (((h >> shl) & 3u) << 4);
+      uint32_t qh = (l >> 4) | (((h >> shh) & 3u) << 4);
+      dl = fmaf((float)ql, xl[i], dl);
+      dh = fmaf((float)qh, xh[i], dh);
+    }
+    // sum (q-32) x = sum q x - 32 sum x
+    r = fmaf(w.s_lo, fmaf(-32.0f, sl, dl), r);
+    if (has_hi) r = fmaf(w.s_hi, fmaf(-32.0f, sh, dh), r);
+    return r;
+  }
+};
+
+template <class F>
+struct Acc {
+  template <class W>
+  static __device__ inline float run(float r, const W& w, const float* xl, const float* xh, float sl, float sh,
+                                     int p, bool has_hi) {
+    return F::acc(r, w, xl, xh, sl, sh, p, has_hi);
+  }
+};
+template <>
+struct Acc<A8> {
+  template <class W>
+  static __device__ inline float run(float r, const W& w, const float* xl, const float* xh, float sl, float sh,
+                                     int, bool) {
+    return A8::acc(r, w, xl, xh, sl, sh);
+  }
+};
+
+template <class F, int ROWS, int NB, bool XF16, int EPI>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row0 = wave * ROWS;
+  if (row0 >= a.n_out) return;
+  int rows[ROWS];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) rows[r] = min(row0 + r, a.n_out - 1);
+  constexpr bool DUAL = EPI == EPI_SWIGLU;
+  float acc[ROWS][NB];
+  float acc2[DUAL ? ROWS : 1][DUAL ? NB : 1];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      acc[r][b] = 0.0f;
+      if constexpr (DUAL) acc2[r][b] = 0.0f;
+    }
+  const int nch = F::chunks(a);
+  for (int p = lane; p < nch; p += 64) {
+    int lo, hi;
+    if (!F::pos(a, p, lo, hi)) continue;
+    const bool has_hi = hi >= 0;
+    typename F::W w[ROWS];
+    typename F::W w2[DUAL ? ROWS : 1];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      w[r] = F::load(a.p0, a.p1, a.p2, a.p3, a, rows[r], p);
+      if constexpr (DUAL) w2[r] = F::load(a.u0, a.u1, a.u2, a.u3, a, rows[r], p);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float xl[16], xh[16];
+      load_x16<XF16>(a.x, (size_t)b * a.ldx + lo, xl);
+      float sl = sum16(xl), sh = 0.0f;
+      if (has_hi) {
+        load_x16<XF16>(a.x, (size_t)b * a.ldx + hi, xh);
+        sh = sum16(xh);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xh[i] = 0.0f;
+      }
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r) {
+        acc[r][b] = Acc<F>::run(acc[r][b], w[r], xl, xh, sl, sh, p, has_hi);
+        if constexpr (DUAL) acc2[r][b] = Acc<F>::run(acc2[r][b], w2[r], xl, xh, sl, sh, p, has_hi);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float v = wave_sum(acc[r][b]);
+      float v2 = 0.0f;
+      if constexpr (DUAL) v2 = wave_sum(acc2[r][b]);
+      if (lane == 0 && row0 + r < a.n_out) {
+        size_t o = (size_t)b * a.ldy + row0 + r;
+        if constexpr (EPI == EPI_STORE) a.y[o] = v;
+        if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + row0 + r] + v;
+        if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(v) * v2;
+      }
+    }
+}
+
+constexpr int kRows = 4;
+
+template <class F, int NB, bool XF16, int EPI>
+void launch_nb(const GemvArgs& a, hipStream_t s) {
+  int waves = (a.n_out + kRows - 1) / kRows;
+  int blocks = (waves + 3) / 4;
+  hipLaunchKernelGGL((gemv_kernel<F, kRows, NB, XF16, EPI>), dim3(blocks), dim3(256), 0, s, a);
+}
+
+template <class F, bool XF16, int EPI>
+void launch_rows(GemvArgs a, int nrows, hipStream_t s) {
+  const size_t xel = XF16 ? 2 : 4;
+  while (nrows > 0) {
+    int nb = std::min(nrows, 8);
+    switch (nb) {
+      case 1: launch_nb<F, 1, XF16, EPI>(a, s); break;
+      case 2: launch_nb<F, 2, XF16, EPI>(a, s); break;
+      case 3: launch_nb<F, 3, XF16, EPI>(a, s); break;
+      case 4: launch_nb<F, 4, XF16, EPI>(a, s); break;
+      case 5: launch_nb<F, 5, XF16, EPI>(a, s); break;
+      case 6: launch_nb<F, 6, XF16, EPI>(a, s); break;
+      case 7: launch_nb<F, 7, XF16, EPI>(a, s); break;
+      default: launch_nb<F, 8, XF16, EPI>(a, s); break;
+    }
+    PGD_HIP(hipGetLastError());
+    nrows -= nb;
+    a.x = reinterpret_cast<const uint8_t*>(a.x) + (size_t)nb * a.ldx * xel;
+    a.y += (size_t)nb * a.ldy;
+    if (a.res) a.res += (size_t)nb * a.ldres;
+  }
+}
+
+
+// entry points of the instantiation files
+void run_a8(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
+void run_q4k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
+void run_q6k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
+
+}  // namespace gemv
+}  // namespace pgd

@@ -58,6 +58,31 @@ class Device:
         return out
 
 
+class Event:
+    """HIP event recorded on the device handle's stream."""
+
+    def __init__(self, dev: Device):
+        self.dev = dev
+        h = C.c_void_p()
+        call("pgd_event_new", dev.handle, C.byref(h))
+        self.handle = h
+
+    def record(self) -> "Event":
+        call("pgd_event_record", self.handle)
+        return self
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        call("pgd_event_elapsed_ms", self.handle, end.handle, C.byref(ms))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            call("pgd_event_free", self.handle)
+        except Exception:
+            pass
+
+
 def device_from_env() -> Device:
     """PAGODA_DEVICE must be `hip` or `hip:N`; anything else is an error (no
     silent CPU fallback, as in the reference's device_from_env)."""
