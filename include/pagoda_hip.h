@@ -99,6 +99,68 @@ int pgd_matrix_gemv_dev(const pgd_matrix* m, const void* x, int x_f16, int ldx, 
 int pgd_matrix_gemv_swiglu_dev(const pgd_matrix* gate, const pgd_matrix* up, const float* x, int ldx,
                                int nrows, float* mid, int ldm);
 
+/* ---- models and sessions ---------------------------------------------------
+ * Architecture of a model handle. arch 0 is the hybrid Qwen3.5 tower
+ * (Gated-DeltaNet + gated full attention, MLX affine-8 weights; Qwen35::load
+ * pagoda-hf/src/qwen3_5.rs:338-452); arch 1 is Qwen2 with GGUF Q4_K/Q6_K
+ * weights and tied embeddings (Qwen2Gguf::load pagoda-hf/src/qwen2_gguf.rs:65-140). */
+enum { PGD_ARCH_QWEN35 = 0, PGD_ARCH_QWEN2 = 1 };
+
+typedef struct pgd_model_config {
+  int arch;
+  int n_layers, hidden, intermediate, vocab;
+  int heads, kv_heads, head_dim, rotary_dim;
+  float rope_theta, eps;
+  int k_heads, v_heads, k_dim, v_dim, conv_kernel; /* gated-delta layers (arch 0) */
+  int full_every; /* arch 0: layer i is full attention iff i % full_every == full_every - 1 */
+  int max_pos;    /* context limit (qwen2_gguf.rs:146-150) */
+  int kv_block;   /* tokens per KV page (16) */
+  int kv_blocks;  /* KV pages per full-attention layer */
+} pgd_model_config;
+
+typedef struct pgd_model pgd_model;
+typedef struct pgd_session pgd_session;
+
+/* Build a model with seeded synthetic weights generated on the device (the
+ * configs use random-init weights; no reference counterpart). */
+int pgd_model_synth(pgd_dev* dev, const pgd_model_config* cfg, uint64_t seed, pgd_model** out);
+int pgd_model_free(pgd_model* m);
+/* weight bytes on the device, algorithmic weight bytes per decode step, KV pages free */
+int pgd_model_info(const pgd_model* m, size_t* weight_bytes, double* algo_bytes_per_token, int* kv_free);
+
+/* ModelEngine::begin_session (pagoda/src/model.rs:78-80). */
+int pgd_session_new(pgd_model* m, pgd_session** out);
+/* ModelSession::fork (pagoda/src/model.rs:185-187): KV pages are shared
+ * copy-on-write, the recurrent state is copied. */
+int pgd_session_fork(const pgd_session* s, pgd_session** out);
+int pgd_session_free(pgd_session* s);
+/* ModelSession::context_len (pagoda/src/model.rs:165). */
+int pgd_session_len(const pgd_session* s, int* len);
+/* ModelSession::forward (pagoda/src/model.rs:167): feed n >= 0 tokens, write
+ * the last position's logits [vocab] (n == 0 repeats the cached logits). */
+int pgd_forward(pgd_session* s, const uint32_t* toks, int n, float* logits);
+/* Qwen35::forward_greedy (pagoda-hf/src/qwen3_5.rs:511-530): one token in,
+ * greedy id and its logit out (device argmax; ties keep the last max). */
+int pgd_forward_greedy(pgd_session* s, uint32_t tok, uint32_t* id, float* logit);
+/* Qwen35::forward_verify (pagoda-hf/src/qwen3_5.rs:663-755): n in 1..4
+ * teacher-forced tokens, greedy id and logit per position. */
+int pgd_forward_verify(pgd_session* s, const uint32_t* toks, int n, uint32_t* ids, float* logits_max);
+/* Ragged batched step (ModelEngine::session_forward_batch,
+ * pagoda/src/model.rs:88-94, widened to multi-token rows): session i feeds
+ * n_per_seq[i] >= 1 tokens from toks (concatenated). ids receive the greedy
+ * id (first max, pagoda/src/sampler.rs:59-69) of each session's last position
+ * (all_rows = 0) or of every fed position (all_rows = 1); 0xFFFFFFFF marks a
+ * row whose logits are all non-finite. logits (nullable) receive the
+ * matching rows [rows][vocab]. Atomic: on an argument error no session
+ * advances. */
+int pgd_step_ragged(pgd_model* m, pgd_session* const* sessions, const uint32_t* toks, const int* n_per_seq,
+                    int nseq, int all_rows, uint32_t* ids, float* logits);
+/* Qwen35Cache::to_bytes / from_bytes, format v1 (pagoda-hf/src/qwen3_5.rs:
+ * 177-255). Arch 0 only. export writes *len bytes when buf is large enough
+ * (pass buf = NULL to query). */
+int pgd_session_export(const pgd_session* s, uint8_t* buf, size_t cap, size_t* len);
+int pgd_session_import(pgd_model* m, const uint8_t* buf, size_t len, pgd_session** out);
+
 #ifdef __cplusplus
 }
 #endif

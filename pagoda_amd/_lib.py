@@ -40,6 +40,19 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_matrix_gemv": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "pgd_matrix_gemv_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int]),
     "pgd_matrix_gemv_swiglu_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int]),
+    "pgd_model_synth": (c_int, [c_void_p, c_void_p, c_uint64, P(c_void_p)]),
+    "pgd_model_free": (c_int, [c_void_p]),
+    "pgd_model_info": (c_int, [c_void_p, P(c_size_t), P(c_double), P(c_int)]),
+    "pgd_session_new": (c_int, [c_void_p, P(c_void_p)]),
+    "pgd_session_fork": (c_int, [c_void_p, P(c_void_p)]),
+    "pgd_session_free": (c_int, [c_void_p]),
+    "pgd_session_len": (c_int, [c_void_p, P(c_int)]),
+    "pgd_forward": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
+    "pgd_forward_greedy": (c_int, [c_void_p, c_uint32, P(c_uint32), P(c_float)]),
+    "pgd_forward_verify": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "pgd_step_ragged": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "pgd_session_export": (c_int, [c_void_p, c_void_p, c_size_t, P(c_size_t)]),
+    "pgd_session_import": (c_int, [c_void_p, c_void_p, c_size_t, P(c_void_p)]),
 }
 
 _lib: C.CDLL | None = None

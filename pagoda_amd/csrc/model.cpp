@@ -1,0 +1,884 @@
+// model.cpp — decode runtime behind the pgd_model / pgd_session C ABI.
+//
+// One HIP stream per device handle; every call is serialized by the caller
+// (the reference engine is single-threaded per instance, engine.rs:1404).
+// A forward is one ragged step: token rows of all sequences go through the
+// projections together; the causal conv, Gated-DeltaNet recurrence and
+// attention run per sequence in token order (qwen3_5.rs:1193-1479,
+// qwen2_gguf.rs:142-266, llama.rs:734-886).
+#include "model.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <unordered_set>
+
+#include "common.h"
+
+struct pgd_model {
+  pgd::Model m;
+};
+
+struct pgd_session {
+  pgd::Session s;
+};
+
+namespace pgd {
+
+namespace {
+
+// Tensor keys of the synthetic generator: (layer << 8) | kind, layer 0xFFFF
+// for model-global tensors.
+enum {
+  K_EMBED = 1, K_HEAD = 2, K_FINAL_NORM = 3,
+  K_IN_NORM = 10, K_POST_NORM = 11, K_GATE = 12, K_UP = 13, K_DOWN = 14,
+  K_QKV = 20, K_Z = 21, K_A = 22, K_B = 23, K_OUT = 24, K_CONV = 25, K_ALOG = 26, K_DTB = 27, K_GNORM = 28,
+  K_Q = 30, K_K = 31, K_V = 32, K_O = 33, K_QNORM = 34, K_KNORM = 35, K_QB = 36, K_KB = 37, K_VB = 38
+};
+
+uint64_t tkey(int layer, int kind) { return ((uint64_t)(layer < 0 ? 0xFFFF : layer) << 8) | (uint64_t)kind; }
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+float* dev_floats(Model& m, size_t n) {
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(float));
+  if (e != hipSuccess) throw Error{kErrAlloc, std::string("hipMalloc: ") + hipGetErrorString(e)};
+  m.allocs.push_back(p);
+  return (float*)p;
+}
+
+float* dev_const(Model& m, size_t n, float v, hipStream_t s) {
+  float* p = dev_floats(m, n);
+  fill_f32(p, n, v, s);
+  return p;
+}
+
+void validate(const pgd_model_config& c) {
+  PGD_CHECK(c.arch == PGD_ARCH_QWEN35 || c.arch == PGD_ARCH_QWEN2, kErrArg, "unknown arch");
+  PGD_CHECK(c.n_layers > 0 && c.hidden > 0 && c.intermediate > 0 && c.vocab > 0, kErrShape, "model dims");
+  PGD_CHECK(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0, kErrShape, "heads / kv_heads");
+  PGD_CHECK(c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256, kErrShape, "head_dim must be 64/128/256");
+  PGD_CHECK(c.rotary_dim > 0 && c.rotary_dim % 2 == 0 && c.rotary_dim <= c.head_dim, kErrShape, "rotary_dim");
+  PGD_CHECK(c.kv_block > 0 && c.kv_blocks > 0, kErrShape, "kv pool");
+  PGD_CHECK(c.max_pos > 0, kErrShape, "max_pos");
+  int kmul = c.arch == PGD_ARCH_QWEN35 ? 64 : 32;
+  PGD_CHECK(c.hidden % kmul == 0 && c.intermediate % kmul == 0 && (c.heads * c.head_dim) % kmul == 0, kErrShape,
+            "GEMV input widths must be multiples of the quant group");
+  if (c.arch == PGD_ARCH_QWEN35) {
+    PGD_CHECK(c.full_every >= 1, kErrShape, "full_every");
+    PGD_CHECK(c.k_dim == 128 && c.v_dim == 128, kErrShape, "gated delta needs k_dim == v_dim == 128");
+    PGD_CHECK(c.k_heads > 0 && c.v_heads % c.k_heads == 0, kErrShape, "v_heads % k_heads");
+    PGD_CHECK(c.conv_kernel >= 2 && c.conv_kernel <= 8, kErrShape, "conv kernel");
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+Model::~Model() {
+  if (dev) {
+    DeviceScope scope(dev);
+    (void)hipStreamSynchronize(dev->stream);
+    qmat_free(embed);
+    if (!tied) qmat_free(head);
+    for (auto& L : layers) {
+      for (QMat* q : {&L.gate, &L.up, &L.down, &L.qkv, &L.z, &L.a, &L.b, &L.out, &L.q, &L.k, &L.v, &L.o}) qmat_free(*q);
+    }
+    for (void* p : allocs) (void)hipFree(p);
+    if (meta_host) (void)hipHostFree(meta_host);
+    if (out_host) (void)hipHostFree(out_host);
+    ws.reset();
+    meta_dev.reset();
+    out_dev.reset();
+  }
+}
+
+void Model::ensure_rope(int pos) {
+  // pagoda-hf/src/qwen3_5.rs:1855-1870 (rope_cos_sin); equal to the Qwen2
+  // tables of qwen2_gguf.rs:327-344 when rotary_dim == head_dim.
+  const int rd = cfg.rotary_dim, half = rd / 2;
+  if (pos < rope_rows) return;
+  int rows = std::max(pos + 1, std::max(2 * rope_rows, 256));
+  rows = std::min(rows, std::max(cfg.max_pos, pos + 1));
+  cos_tab.resize((size_t)rows * rd);
+  sin_tab.resize((size_t)rows * rd);
+  std::vector<float> freq(half);
+  for (int i = 0; i < half; ++i) freq[i] = 1.0f / powf(cfg.rope_theta, (float)(2 * i) / (float)rd);
+  for (int p = rope_rows; p < rows; ++p) {
+    for (int i = 0; i < half; ++i) {
+      float ang = (float)p * freq[i];
+      float c = cosf(ang), s = sinf(ang);
+      cos_tab[(size_t)p * rd + i] = c;
+      cos_tab[(size_t)p * rd + half + i] = c;
+      sin_tab[(size_t)p * rd + i] = s;
+      sin_tab[(size_t)p * rd + half + i] = s;
+    }
+  }
+  rope_rows = rows;
+}
+
+int Model::alloc_block() {
+  PGD_CHECK(!free_blocks.empty(), kErrAlloc, "KV page pool exhausted");
+  int b = free_blocks.back();
+  free_blocks.pop_back();
+  refcount[b] = 1;
+  return b;
+}
+
+void Model::release_block(int b) {
+  if (--refcount[b] == 0) free_blocks.push_back(b);
+}
+
+void Model::copy_block(int dst, int src) {
+  size_t per = (size_t)cfg.kv_heads * cfg.kv_block * cfg.head_dim;
+  for (auto& L : layers) {
+    if (!L.full) continue;
+    PGD_HIP(hipMemcpyAsync(L.k_pool + (size_t)dst * per, L.k_pool + (size_t)src * per, per * 4,
+                           hipMemcpyDeviceToDevice, dev->stream));
+    PGD_HIP(hipMemcpyAsync(L.v_pool + (size_t)dst * per, L.v_pool + (size_t)src * per, per * 4,
+                           hipMemcpyDeviceToDevice, dev->stream));
+  }
+}
+
+Session::~Session() {
+  if (!model) return;
+  for (int b : blocks) model->release_block(b);
+  if (rec) {
+    DeviceScope scope(model->dev);
+    (void)hipStreamSynchronize(model->dev->stream);
+    (void)hipFree(rec);
+  }
+  model->live_sessions--;
+}
+
+// ---------------------------------------------------------------------------
+// synthetic model
+// ---------------------------------------------------------------------------
+static void build_synth(Model& m, uint64_t seed) {
+  const pgd_model_config& c = m.cfg;
+  hipStream_t s = m.dev->stream;
+  const int H = c.hidden;
+  m.kv_width = c.kv_heads * c.head_dim;
+  if (c.arch == PGD_ARCH_QWEN35) {
+    m.key_dim = c.k_heads * c.k_dim;
+    m.value_dim = c.v_heads * c.v_dim;
+    m.conv_dim = 2 * m.key_dim + m.value_dim;
+    m.q_out = c.heads * c.head_dim * 2;
+    qmat_alloc(m.embed, FMT_A8, c.vocab, H);
+    qmat_synth(m.embed, seed, tkey(-1, K_EMBED), 0.02f, s);
+    qmat_alloc(m.head, FMT_A8, c.vocab, H);
+    qmat_synth(m.head, seed, tkey(-1, K_HEAD), 0.02f, s);
+  } else {
+    m.q_out = c.heads * c.head_dim;
+    qmat_alloc(m.embed, FMT_Q6K, c.vocab, H);
+    qmat_synth(m.embed, seed, tkey(-1, K_EMBED), 0.02f, s);
+    m.head = m.embed;  // tied lm_head (qwen2_gguf.rs:96-99)
+    m.tied = true;
+  }
+  m.final_norm = dev_const(m, H, 1.0f, s);
+  m.layers.resize(c.n_layers);
+  size_t kv_per_layer = (size_t)c.kv_blocks * c.kv_heads * c.kv_block * c.head_dim;
+  auto mat = [&](QMat& q, int fmt, int n_out, int n_in, int li, int kind) {
+    qmat_alloc(q, fmt, n_out, n_in);
+    qmat_synth(q, seed, tkey(li, kind), 0.02f, s);
+  };
+  for (int i = 0; i < c.n_layers; ++i) {
+    Layer& L = m.layers[i];
+    L.in_norm = dev_const(m, H, 1.0f, s);
+    L.post_norm = dev_const(m, H, 1.0f, s);
+    if (c.arch == PGD_ARCH_QWEN35) {
+      L.full = (i % c.full_every) == c.full_every - 1;
+      mat(L.gate, FMT_A8, c.intermediate, H, i, K_GATE);
+      mat(L.up, FMT_A8, c.intermediate, H, i, K_UP);
+      mat(L.down, FMT_A8, H, c.intermediate, i, K_DOWN);
+      if (!L.full) {
+        L.lin_index = m.n_lin++;
+        mat(L.qkv, FMT_A8, m.conv_dim, H, i, K_QKV);
+        mat(L.z, FMT_A8, m.value_dim, H, i, K_Z);
+        mat(L.a, FMT_A8, c.v_heads, H, i, K_A);
+        mat(L.b, FMT_A8, c.v_heads, H, i, K_B);
+        mat(L.out, FMT_A8, H, m.value_dim, i, K_OUT);
+        L.conv = dev_floats(m, (size_t)m.conv_dim * c.conv_kernel);
+        synth_normal_f32(L.conv, (size_t)m.conv_dim * c.conv_kernel, seed, tkey(i, K_CONV), 0.2f, s);
+        L.a_log = dev_floats(m, c.v_heads);
+        synth_uniform_f32(L.a_log, c.v_heads, seed, tkey(i, K_ALOG), 2.7725887f, s);
+        L.dt_bias = dev_floats(m, c.v_heads);
+        synth_normal_f32(L.dt_bias, c.v_heads, seed, tkey(i, K_DTB), 0.1f, s);
+        L.gnorm = dev_const(m, c.v_dim, 1.0f, s);
+      } else {
+        L.full_index = m.n_full++;
+        mat(L.q, FMT_A8, m.q_out, H, i, K_Q);
+        mat(L.k, FMT_A8, m.kv_width, H, i, K_K);
+        mat(L.v, FMT_A8, m.kv_width, H, i, K_V);
+        mat(L.o, FMT_A8, H, c.heads * c.head_dim, i, K_O);
+        L.q_norm = dev_const(m, c.head_dim, 1.0f, s);
+        L.k_norm = dev_const(m, c.head_dim, 1.0f, s);
+      }
+    } else {
+      L.full = true;
+      L.full_index = m.n_full++;
+      mat(L.q, FMT_Q4K, m.q_out, H, i, K_Q);
+      mat(L.k, FMT_Q4K, m.kv_width, H, i, K_K);
+      mat(L.v, FMT_Q6K, m.kv_width, H, i, K_V);
+      mat(L.o, FMT_Q4K, H, c.heads * c.head_dim, i, K_O);
+      mat(L.gate, FMT_Q4K, c.intermediate, H, i, K_GATE);
+      mat(L.up, FMT_Q4K, c.intermediate, H, i, K_UP);
+      mat(L.down, i % 2 == 0 ? FMT_Q6K : FMT_Q4K, H, c.intermediate, i, K_DOWN);
+      L.qb = dev_floats(m, m.q_out);
+      synth_normal_f32(L.qb, m.q_out, seed, tkey(i, K_QB), 0.02f, s);
+      L.kb = dev_floats(m, m.kv_width);
+      synth_normal_f32(L.kb, m.kv_width, seed, tkey(i, K_KB), 0.02f, s);
+      L.vb = dev_floats(m, m.kv_width);
+      synth_normal_f32(L.vb, m.kv_width, seed, tkey(i, K_VB), 0.02f, s);
+    }
+    if (L.full) {
+      L.k_pool = dev_floats(m, kv_per_layer);
+      L.v_pool = dev_floats(m, kv_per_layer);
+    }
+  }
+  if (c.arch == PGD_ARCH_QWEN35) {
+    m.conv_floats = (size_t)m.conv_dim * (c.conv_kernel - 1);
+    m.conv_floats = align_up(m.conv_floats, 64);
+    m.state_floats = (size_t)c.v_heads * c.k_dim * c.v_dim;
+    m.rec_floats = (size_t)m.n_lin * (m.conv_floats + m.state_floats);
+  }
+  m.refcount.assign(c.kv_blocks, 0);
+  m.free_blocks.resize(c.kv_blocks);
+  for (int b = 0; b < c.kv_blocks; ++b) m.free_blocks[b] = c.kv_blocks - 1 - b;
+  PGD_HIP(hipStreamSynchronize(s));
+}
+
+// ---------------------------------------------------------------------------
+// ragged step
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Ws {
+  float *x, *xn, *A, *B, *C0, *C1, *D, *E, *F, *G, *logits;
+  size_t lda, ldb, ldd, lde;
+};
+
+Ws carve_ws(Model& m, int rows, int lrows) {
+  const pgd_model_config& c = m.cfg;
+  size_t H = c.hidden;
+  size_t lda = std::max<size_t>(m.conv_dim, m.q_out);
+  size_t ldb = std::max<size_t>(m.value_dim, m.kv_width);
+  size_t ldc = std::max<size_t>(align_up(std::max(c.v_heads, 1), 8), m.kv_width);
+  size_t ldd = std::max<size_t>(m.conv_dim, (size_t)c.heads * c.head_dim);
+  size_t lde = std::max<size_t>(m.value_dim, (size_t)c.heads * c.head_dim);
+  size_t sizes[] = {rows * H, rows * H, rows * lda, rows * ldb, rows * ldc, rows * ldc, rows * ldd, rows * lde,
+                    rows * (size_t)c.heads * c.head_dim, rows * (size_t)c.intermediate, (size_t)lrows * c.vocab};
+  size_t total = 0;
+  for (size_t v : sizes) total += align_up(v, 64);
+  if (m.ws.bytes < total * 4) {
+    PGD_HIP(hipStreamSynchronize(m.dev->stream));
+    m.ws = DevBuf(total * 4);
+  }
+  float* p = m.ws.as<float>();
+  float* ptrs[11];
+  for (int i = 0; i < 11; ++i) {
+    ptrs[i] = p;
+    p += align_up(sizes[i], 64);
+  }
+  Ws w{ptrs[0], ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], ptrs[6], ptrs[7], ptrs[8], ptrs[9], ptrs[10],
+       lda, ldb, ldd, lde};
+  return w;
+}
+
+}  // namespace
+
+void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, int nseq, StepOut& out) {
+  const pgd_model_config& c = m.cfg;
+  hipStream_t st = m.dev->stream;
+  PGD_CHECK(nseq > 0 && sess && toks && n, kErrArg, "empty step");
+  // ---- validation (nothing is modified before this block passes) ----
+  int rows = 0;
+  {
+    std::unordered_set<const Session*> seen;
+    for (int i = 0; i < nseq; ++i) {
+      PGD_CHECK(sess[i] && sess[i]->model == &m, kErrArg, "session does not belong to this model");
+      PGD_CHECK(seen.insert(sess[i]).second, kErrArg, "a session appears twice in one step");
+      PGD_CHECK(n[i] >= 1, kErrArg, "every session must feed at least one token");
+      PGD_CHECK((long long)sess[i]->len + n[i] <= c.max_pos, kErrShape,
+                "context " + std::to_string(sess[i]->len) + " + " + std::to_string(n[i]) + " exceeds max_pos");
+      rows += n[i];
+    }
+    for (int r = 0; r < rows; ++r)
+      PGD_CHECK(toks[r] < (uint32_t)c.vocab, kErrArg, "token " + std::to_string(toks[r]) + " out of vocab");
+  }
+  const int lrows = out.all_rows ? rows : nseq;
+  // ---- KV pages: count, then allocate (copy-on-write for a shared tail) ----
+  if (m.n_full > 0) {
+    size_t need = 0;
+    for (int i = 0; i < nseq; ++i) {
+      const Session* s = sess[i];
+      size_t want = (size_t)(s->len + n[i] + c.kv_block - 1) / c.kv_block;
+      need += want - s->blocks.size();
+      if (s->len % c.kv_block && m.refcount[s->blocks.back()] > 1) need += 1;
+    }
+    PGD_CHECK(need <= m.free_blocks.size(), kErrAlloc, "KV page pool exhausted");
+    for (int i = 0; i < nseq; ++i) {
+      Session* s = sess[i];
+      if (s->len % c.kv_block && m.refcount[s->blocks.back()] > 1) {
+        int nb = m.alloc_block();
+        m.copy_block(nb, s->blocks.back());
+        m.release_block(s->blocks.back());
+        s->blocks.back() = nb;
+      }
+      size_t want = (size_t)(s->len + n[i] + c.kv_block - 1) / c.kv_block;
+      while (s->blocks.size() < want) s->blocks.push_back(m.alloc_block());
+    }
+  }
+  int max_pos = 0;
+  size_t max_blocks = 1;
+  for (int i = 0; i < nseq; ++i) {
+    max_pos = std::max(max_pos, sess[i]->len + n[i] - 1);
+    max_blocks = std::max(max_blocks, sess[i]->blocks.size());
+  }
+  m.ensure_rope(max_pos);
+  const int rd = c.rotary_dim;
+  // ---- host metadata, one upload ----
+  size_t off_seq = 0;
+  size_t off_pos = align_up(off_seq + rows * 4, 256);
+  size_t off_rs = align_up(off_pos + rows * 4, 256);
+  size_t off_rc = align_up(off_rs + nseq * 4, 256);
+  size_t off_bt = align_up(off_rc + nseq * 4, 256);
+  size_t off_lr = align_up(off_bt + nseq * max_blocks * 4, 256);
+  size_t off_tok = align_up(off_lr + lrows * 4, 256);
+  size_t off_sb = align_up(off_tok + rows * 4, 256);
+  size_t off_cos = align_up(off_sb + nseq * 8, 256);
+  size_t off_sin = align_up(off_cos + (size_t)rows * rd * 4, 256);
+  size_t meta_bytes = align_up(off_sin + (size_t)rows * rd * 4, 256);
+  if (m.meta_host_cap < meta_bytes) {
+    if (m.meta_host) {
+      PGD_HIP(hipStreamSynchronize(st));
+      PGD_HIP(hipHostFree(m.meta_host));
+      m.meta_host = nullptr;
+    }
+    PGD_HIP(hipHostMalloc(&m.meta_host, meta_bytes * 2));
+    m.meta_host_cap = meta_bytes * 2;
+  }
+  if (m.meta_dev.bytes < meta_bytes) {
+    PGD_HIP(hipStreamSynchronize(st));
+    m.meta_dev = DevBuf(meta_bytes * 2);
+  }
+  PGD_HIP(hipStreamSynchronize(st));  // host staging buffer reuse
+  uint8_t* hb = (uint8_t*)m.meta_host;
+  int* h_seq = (int*)(hb + off_seq);
+  int* h_pos = (int*)(hb + off_pos);
+  int* h_rs = (int*)(hb + off_rs);
+  int* h_rc = (int*)(hb + off_rc);
+  int* h_bt = (int*)(hb + off_bt);
+  int* h_lr = (int*)(hb + off_lr);
+  uint32_t* h_tok = (uint32_t*)(hb + off_tok);
+  float** h_sb = (float**)(hb + off_sb);
+  float* h_cos = (float*)(hb + off_cos);
+  float* h_sin = (float*)(hb + off_sin);
+  {
+    int r = 0, lr = 0;
+    for (int i = 0; i < nseq; ++i) {
+      Session* s = sess[i];
+      h_rs[i] = r;
+      h_rc[i] = n[i];
+      h_sb[i] = s->rec;
+      for (size_t b = 0; b < max_blocks; ++b) h_bt[i * max_blocks + b] = b < s->blocks.size() ? s->blocks[b] : 0;
+      for (int t = 0; t < n[i]; ++t, ++r) {
+        h_seq[r] = i;
+        h_pos[r] = s->len + t;
+        h_tok[r] = toks[r];
+        memcpy(h_cos + (size_t)r * rd, m.cos_tab.data() + (size_t)(s->len + t) * rd, rd * 4);
+        memcpy(h_sin + (size_t)r * rd, m.sin_tab.data() + (size_t)(s->len + t) * rd, rd * 4);
+        if (out.all_rows) h_lr[lr++] = r;
+      }
+      if (!out.all_rows) h_lr[lr++] = r - 1;
+    }
+  }
+  PGD_HIP(hipMemcpyAsync(m.meta_dev.p, m.meta_host, meta_bytes, hipMemcpyHostToDevice, st));
+  uint8_t* db = (uint8_t*)m.meta_dev.p;
+  const int* d_seq = (const int*)(db + off_seq);
+  const int* d_pos = (const int*)(db + off_pos);
+  SeqMeta sm{(const int*)(db + off_rs), (const int*)(db + off_rc)};
+  const int* d_lr = (const int*)(db + off_lr);
+  const uint32_t* d_tok = (const uint32_t*)(db + off_tok);
+  float* const* d_sb = (float* const*)(db + off_sb);
+  RowMeta rm{d_seq, d_pos, (const int*)(db + off_bt), (int)max_blocks, (const float*)(db + off_cos),
+             (const float*)(db + off_sin)};
+
+  // ---- forward ----
+  Ws w = carve_ws(m, rows, lrows);
+  const int H = c.hidden;
+  const int norm_mode = c.arch == PGD_ARCH_QWEN35 ? 0 : 1;
+  const float eps = c.arch == PGD_ARCH_QWEN35 ? 1e-6f : c.eps;
+  qmat_embed(m.embed, d_tok, rows, w.x, H, st);
+  const size_t per_lin = m.conv_floats + m.state_floats;
+  for (auto& L : m.layers) {
+    rmsnorm_rows(w.x, H, nullptr, rows, H, L.in_norm, eps, norm_mode, w.xn, H, st);
+    if (!L.full) {
+      qmat_gemv(L.qkv, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
+      qmat_gemv(L.z, w.xn, 0, H, rows, w.B, (int)w.ldb, nullptr, 0, st);
+      qmat_gemv(L.b, w.xn, 0, H, rows, w.C0, c.v_heads, nullptr, 0, st);
+      qmat_gemv(L.a, w.xn, 0, H, rows, w.C1, c.v_heads, nullptr, 0, st);
+      conv_step(w.A, (int)w.lda, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb,
+                (size_t)L.lin_index * per_lin, sm, nseq, st);
+      GdnParams gp{};
+      gp.k_heads = c.k_heads;
+      gp.v_heads = c.v_heads;
+      gp.k_dim = c.k_dim;
+      gp.v_dim = c.v_dim;
+      gp.conv_out = w.D;
+      gp.ld_conv = (int)w.ldd;
+      gp.a = w.C1;
+      gp.b = w.C0;
+      gp.ld_ab = c.v_heads;
+      gp.z = w.B;
+      gp.ld_z = (int)w.ldb;
+      gp.a_log = L.a_log;
+      gp.dt_bias = L.dt_bias;
+      gp.norm = L.gnorm;
+      gp.out = w.E;
+      gp.ld_out = (int)w.lde;
+      gp.state_base = d_sb;
+      gp.state_off = (size_t)L.lin_index * per_lin + m.conv_floats;
+      gdn_step(gp, sm, nseq, st);
+      qmat_gemv(L.out, w.E, 0, (int)w.lde, rows, w.x, H, w.x, H, st);
+    } else {
+      qmat_gemv(L.q, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
+      qmat_gemv(L.k, w.xn, 0, H, rows, w.B, (int)w.ldb, nullptr, 0, st);
+      qmat_gemv(L.v, w.xn, 0, H, rows, w.C0, (int)w.ldb, nullptr, 0, st);
+      AttnLayout al{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.kv_block, L.k_pool, L.v_pool};
+      QkvPrep qp{};
+      qp.variant = c.arch == PGD_ARCH_QWEN35 ? 0 : 1;
+      qp.q_raw = w.A;
+      qp.ld_q = (int)w.lda;
+      qp.k_raw = w.B;
+      qp.v_raw = w.C0;
+      qp.ld_kv = (int)w.ldb;
+      qp.q_norm = L.q_norm;
+      qp.k_norm = L.k_norm;
+      qp.q_bias = L.qb;
+      qp.k_bias = L.kb;
+      qp.v_bias = L.vb;
+      qp.q = w.D;
+      qp.gate = w.F;
+      qkv_prep(qp, al, rm, rows, st);
+      attn_decode(w.D, qp.variant == 0 ? w.F : nullptr, w.E, al, rm, rows, st);
+      qmat_gemv(L.o, w.E, 0, c.heads * c.head_dim, rows, w.x, H, w.x, H, st);
+    }
+    rmsnorm_rows(w.x, H, nullptr, rows, H, L.post_norm, eps, norm_mode, w.xn, H, st);
+    qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
+    qmat_gemv(L.down, w.G, 0, c.intermediate, rows, w.x, H, w.x, H, st);
+  }
+  // ---- head ----
+  rmsnorm_rows(w.x, H, d_lr, lrows, H, m.final_norm, eps, norm_mode, w.xn, H, st);
+  qmat_gemv(m.head, w.xn, 0, H, lrows, w.logits, c.vocab, nullptr, 0, st);
+  size_t out_bytes = (size_t)lrows * 12;
+  if (m.out_dev.bytes < out_bytes) m.out_dev = DevBuf(out_bytes * 2);
+  if (m.out_host_cap < out_bytes) {
+    if (m.out_host) PGD_HIP(hipHostFree(m.out_host));
+    PGD_HIP(hipHostMalloc(&m.out_host, out_bytes * 2));
+    m.out_host_cap = out_bytes * 2;
+  }
+  uint32_t* d_ids = m.out_dev.as<uint32_t>();
+  float* d_vals = (float*)(d_ids + lrows);
+  int* d_nf = (int*)(d_vals + lrows);
+  argmax_rows(w.logits, c.vocab, lrows, c.vocab, out.last_max, d_ids, d_vals, d_nf, st);
+  PGD_HIP(hipMemcpyAsync(m.out_host, m.out_dev.p, out_bytes, hipMemcpyDeviceToHost, st));
+  if (out.logits)
+    PGD_HIP(hipMemcpyAsync(out.logits, w.logits, (size_t)lrows * c.vocab * 4, hipMemcpyDeviceToHost, st));
+  PGD_HIP(hipStreamSynchronize(st));
+  const uint32_t* h_ids = (const uint32_t*)m.out_host;
+  const float* h_vals = (const float*)(h_ids + lrows);
+  if (out.ids) memcpy(out.ids, h_ids, (size_t)lrows * 4);
+  if (out.vals) memcpy(out.vals, h_vals, (size_t)lrows * 4);
+  for (int i = 0; i < nseq; ++i) sess[i]->len += n[i];
+}
+
+}  // namespace pgd
+
+using namespace pgd;
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int pgd_model_synth(pgd_dev* dev, const pgd_model_config* cfg, uint64_t seed, pgd_model** out) {
+  pgd_model* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(dev && cfg && out, kErrArg, "null argument");
+    validate(*cfg);
+    DeviceScope scope(dev);
+    held = new pgd_model();
+    held->m.dev = dev;
+    held->m.cfg = *cfg;
+    build_synth(held->m, seed);
+    *out = held;
+  });
+  if (rc && held) delete held;
+  return rc;
+}
+
+int pgd_model_free(pgd_model* m) {
+  return guard([&] {
+    if (!m) return;
+    PGD_CHECK(m->m.live_sessions == 0, kErrState, "free every session before its model");
+    delete m;
+  });
+}
+
+int pgd_model_info(const pgd_model* pm, size_t* weight_bytes, double* algo, int* kv_free) {
+  return guard([&] {
+    PGD_CHECK(pm, kErrArg, "null model");
+    const Model& m = pm->m;
+    size_t wb = m.embed.bytes + (m.tied ? 0 : m.head.bytes);
+    double ab = qmat_algo_bytes(m.head);  // one embedding row is negligible
+    for (auto& L : m.layers)
+      for (const QMat* q : {&L.gate, &L.up, &L.down, &L.qkv, &L.z, &L.a, &L.b, &L.out, &L.q, &L.k, &L.v, &L.o}) {
+        wb += q->bytes;
+        ab += q->base ? qmat_algo_bytes(*q) : 0.0;
+      }
+    if (weight_bytes) *weight_bytes = wb;
+    if (algo) *algo = ab;
+    if (kv_free) *kv_free = (int)m.free_blocks.size();
+  });
+}
+
+int pgd_session_new(pgd_model* pm, pgd_session** out) {
+  pgd_session* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(pm && out, kErrArg, "null argument");
+    Model& m = pm->m;
+    DeviceScope scope(m.dev);
+    held = new pgd_session();
+    held->s.model = &m;
+    m.live_sessions++;
+    if (m.rec_floats) {
+      void* p = nullptr;
+      hipError_t e = hipMalloc(&p, m.rec_floats * 4);
+      PGD_CHECK(e == hipSuccess, kErrAlloc, std::string("hipMalloc session state: ") + hipGetErrorString(e));
+      held->s.rec = (float*)p;
+      PGD_HIP(hipMemsetAsync(p, 0, m.rec_floats * 4, m.dev->stream));
+      PGD_HIP(hipStreamSynchronize(m.dev->stream));
+    }
+    *out = held;
+  });
+  if (rc && held) delete held;
+  return rc;
+}
+
+int pgd_session_fork(const pgd_session* ps, pgd_session** out) {
+  pgd_session* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(ps && out, kErrArg, "null argument");
+    const Session& s = ps->s;
+    Model& m = *s.model;
+    DeviceScope scope(m.dev);
+    held = new pgd_session();
+    held->s.model = &m;
+    m.live_sessions++;
+    held->s.len = s.len;
+    held->s.blocks = s.blocks;
+    for (int b : s.blocks) m.refcount[b]++;
+    held->s.last_logits = s.last_logits;
+    held->s.has_logits = s.has_logits;
+    if (m.rec_floats) {
+      void* p = nullptr;
+      hipError_t e = hipMalloc(&p, m.rec_floats * 4);
+      PGD_CHECK(e == hipSuccess, kErrAlloc, std::string("hipMalloc session state: ") + hipGetErrorString(e));
+      held->s.rec = (float*)p;
+      PGD_HIP(hipMemcpyAsync(p, s.rec, m.rec_floats * 4, hipMemcpyDeviceToDevice, m.dev->stream));
+      PGD_HIP(hipStreamSynchronize(m.dev->stream));
+    }
+    *out = held;
+  });
+  if (rc && held) delete held;
+  return rc;
+}
+
+int pgd_session_free(pgd_session* s) {
+  return guard([&] { delete s; });
+}
+
+int pgd_session_len(const pgd_session* s, int* len) {
+  return guard([&] {
+    PGD_CHECK(s && len, kErrArg, "null argument");
+    *len = s->s.len;
+  });
+}
+
+int pgd_forward(pgd_session* ps, const uint32_t* toks, int n, float* logits) {
+  return guard([&] {
+    PGD_CHECK(ps && logits && n >= 0, kErrArg, "bad argument");
+    Session& s = ps->s;
+    Model& m = *s.model;
+    if (n == 0) {
+      PGD_CHECK(s.has_logits, kErrState, "empty feed before any forward");
+      memcpy(logits, s.last_logits.data(), (size_t)m.cfg.vocab * 4);
+      return;
+    }
+    PGD_CHECK(toks, kErrArg, "null tokens");
+    DeviceScope scope(m.dev);
+    Session* sp = &s;
+    uint32_t id = 0;
+    StepOut o;
+    o.ids = &id;
+    o.logits = logits;
+    step(m, &sp, toks, &n, 1, o);
+    s.last_logits.assign(logits, logits + m.cfg.vocab);
+    s.has_logits = true;
+  });
+}
+
+int pgd_forward_greedy(pgd_session* ps, uint32_t tok, uint32_t* id, float* logit) {
+  return guard([&] {
+    PGD_CHECK(ps && id, kErrArg, "null argument");
+    Session& s = ps->s;
+    Model& m = *s.model;
+    DeviceScope scope(m.dev);
+    Session* sp = &s;
+    int n = 1;
+    float v = 0.0f;
+    StepOut o;
+    o.last_max = 1;
+    o.ids = id;
+    o.vals = &v;
+    step(m, &sp, &tok, &n, 1, o);
+    s.has_logits = false;
+    if (logit) *logit = v;
+  });
+}
+
+int pgd_forward_verify(pgd_session* ps, const uint32_t* toks, int n, uint32_t* ids, float* logits_max) {
+  return guard([&] {
+    PGD_CHECK(ps && toks && ids, kErrArg, "null argument");
+    PGD_CHECK(n >= 1 && n <= 4, kErrArg, "verify batch must be 1..4 tokens");
+    Session& s = ps->s;
+    Model& m = *s.model;
+    DeviceScope scope(m.dev);
+    Session* sp = &s;
+    StepOut o;
+    o.all_rows = 1;
+    o.last_max = 1;
+    o.ids = ids;
+    o.vals = logits_max;
+    step(m, &sp, toks, &n, 1, o);
+    s.has_logits = false;
+  });
+}
+
+int pgd_step_ragged(pgd_model* pm, pgd_session* const* sessions, const uint32_t* toks, const int* n_per_seq,
+                    int nseq, int all_rows, uint32_t* ids, float* logits) {
+  return guard([&] {
+    PGD_CHECK(pm && sessions && toks && n_per_seq && ids && nseq > 0, kErrArg, "null argument");
+    Model& m = pm->m;
+    DeviceScope scope(m.dev);
+    std::vector<Session*> ss(nseq);
+    for (int i = 0; i < nseq; ++i) {
+      PGD_CHECK(sessions[i], kErrArg, "null session");
+      ss[i] = &sessions[i]->s;
+    }
+    StepOut o;
+    o.all_rows = all_rows ? 1 : 0;
+    o.ids = ids;
+    o.logits = logits;
+    step(m, ss.data(), toks, n_per_seq, nseq, o);
+    for (int i = 0; i < nseq; ++i) {
+      if (logits && !all_rows) {
+        ss[i]->last_logits.assign(logits + (size_t)i * m.cfg.vocab, logits + (size_t)(i + 1) * m.cfg.vocab);
+        ss[i]->has_logits = true;
+      } else {
+        ss[i]->has_logits = false;
+      }
+    }
+  });
+}
+
+// ---- cache bytes v1 (pagoda-hf/src/qwen3_5.rs:177-255) ----
+namespace {
+void put(std::vector<uint8_t>& b, const void* p, size_t n) {
+  const uint8_t* c = (const uint8_t*)p;
+  b.insert(b.end(), c, c + n);
+}
+void put_u32(std::vector<uint8_t>& b, uint32_t v) { put(b, &v, 4); }
+void put_vec(std::vector<uint8_t>& b, const float* v, size_t n) {
+  put_u32(b, (uint32_t)n);
+  put(b, v, n * 4);
+}
+struct Reader {
+  const uint8_t* p;
+  size_t n, at = 0;
+  void need(size_t k) { PGD_CHECK(at + k <= n, kErrFormat, "kv truncated"); }
+  uint8_t u8() {
+    need(1);
+    return p[at++];
+  }
+  uint32_t u32() {
+    need(4);
+    uint32_t v;
+    memcpy(&v, p + at, 4);
+    at += 4;
+    return v;
+  }
+  uint64_t u64() {
+    need(8);
+    uint64_t v;
+    memcpy(&v, p + at, 8);
+    at += 8;
+    return v;
+  }
+  std::vector<float> vec() {
+    uint32_t k = u32();
+    need((size_t)k * 4);
+    std::vector<float> v(k);
+    memcpy(v.data(), p + at, (size_t)k * 4);
+    at += (size_t)k * 4;
+    return v;
+  }
+};
+}  // namespace
+
+int pgd_session_export(const pgd_session* ps, uint8_t* buf, size_t cap, size_t* len) {
+  return guard([&] {
+    PGD_CHECK(ps && len, kErrArg, "null argument");
+    const Session& s = ps->s;
+    const Model& m = *s.model;
+    const pgd_model_config& c = m.cfg;
+    PGD_CHECK(c.arch == PGD_ARCH_QWEN35, kErrArg, "cache bytes v1 are defined for the hybrid model only");
+    DeviceScope scope(m.dev);
+    PGD_HIP(hipStreamSynchronize(m.dev->stream));
+    std::vector<uint8_t> b;
+    put_u32(b, 1);
+    uint64_t L64 = (uint64_t)s.len;
+    put(b, &L64, 8);
+    put_u32(b, (uint32_t)c.n_layers);
+    const size_t per_blk = (size_t)c.kv_heads * c.kv_block * c.head_dim;
+    const size_t per_lin = m.conv_floats + m.state_floats;
+    std::vector<float> tmp;
+    for (const Layer& L : m.layers) {
+      if (L.full) {
+        b.push_back(2);
+        put_u32(b, (uint32_t)s.len);
+        put_u32(b, (uint32_t)c.kv_heads);
+        put_u32(b, (uint32_t)c.head_dim);
+        for (int which = 0; which < 2; ++which) {
+          const float* pool = which == 0 ? L.k_pool : L.v_pool;
+          std::vector<float> out((size_t)s.len * c.kv_heads * c.head_dim);
+          tmp.resize(per_blk);
+          for (size_t bi = 0; bi < s.blocks.size(); ++bi) {
+            PGD_HIP(hipMemcpy(tmp.data(), pool + (size_t)s.blocks[bi] * per_blk, per_blk * 4, hipMemcpyDeviceToHost));
+            for (int sl = 0; sl < c.kv_block; ++sl) {
+              size_t p = bi * c.kv_block + sl;
+              if (p >= (size_t)s.len) break;
+              for (int h = 0; h < c.kv_heads; ++h)
+                memcpy(&out[(p * c.kv_heads + h) * c.head_dim], &tmp[((size_t)h * c.kv_block + sl) * c.head_dim],
+                       (size_t)c.head_dim * 4);
+            }
+          }
+          put_vec(b, out.data(), out.size());
+        }
+      } else {
+        b.push_back(1);
+        size_t cf = (size_t)m.conv_dim * (c.conv_kernel - 1);
+        tmp.resize(std::max(cf, m.state_floats));
+        const float* base = s.rec + (size_t)L.lin_index * per_lin;
+        PGD_HIP(hipMemcpy(tmp.data(), base, cf * 4, hipMemcpyDeviceToHost));
+        put_vec(b, tmp.data(), cf);
+        PGD_HIP(hipMemcpy(tmp.data(), base + m.conv_floats, m.state_floats * 4, hipMemcpyDeviceToHost));
+        put_vec(b, tmp.data(), m.state_floats);
+      }
+    }
+    *len = b.size();
+    if (buf) {
+      PGD_CHECK(cap >= b.size(), kErrArg, "export buffer too small");
+      memcpy(buf, b.data(), b.size());
+    }
+  });
+}
+
+int pgd_session_import(pgd_model* pm, const uint8_t* buf, size_t len, pgd_session** out) {
+  pgd_session* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(pm && buf && out, kErrArg, "null argument");
+    Model& m = pm->m;
+    const pgd_model_config& c = m.cfg;
+    PGD_CHECK(c.arch == PGD_ARCH_QWEN35, kErrArg, "cache bytes v1 are defined for the hybrid model only");
+    Reader rd{buf, len};
+    PGD_CHECK(rd.u32() == 1, kErrFormat, "kv version");
+    uint64_t slen = rd.u64();
+    PGD_CHECK(rd.u32() == (uint32_t)c.n_layers, kErrFormat, "layer count mismatch");
+    PGD_CHECK(slen <= (uint64_t)c.max_pos, kErrFormat, "length exceeds max_pos");
+    size_t nblk = (slen + c.kv_block - 1) / c.kv_block;
+    PGD_CHECK(nblk <= m.free_blocks.size() || m.n_full == 0, kErrAlloc, "KV page pool exhausted");
+    const size_t per_blk = (size_t)c.kv_heads * c.kv_block * c.head_dim;
+    const size_t per_lin = m.conv_floats + m.state_floats;
+    // parse everything first
+    std::vector<std::vector<float>> conv(m.n_lin), state(m.n_lin), kk(m.n_full), vv(m.n_full);
+    for (const Layer& L : m.layers) {
+      uint8_t tag = rd.u8();
+      if (L.full) {
+        PGD_CHECK(tag == 2, kErrFormat, "layer kind mismatch");
+        uint32_t kv_len = rd.u32(), kvh = rd.u32(), hd = rd.u32();
+        PGD_CHECK(kv_len == slen && kvh == (uint32_t)c.kv_heads && hd == (uint32_t)c.head_dim, kErrFormat, "kv shape");
+        kk[L.full_index] = rd.vec();
+        vv[L.full_index] = rd.vec();
+        PGD_CHECK(kk[L.full_index].size() == (size_t)kv_len * kvh * hd && vv[L.full_index].size() == kk[L.full_index].size(),
+                  kErrFormat, "kv shape");
+      } else {
+        PGD_CHECK(tag == 1, kErrFormat, "layer kind mismatch");
+        conv[L.lin_index] = rd.vec();
+        state[L.lin_index] = rd.vec();
+        PGD_CHECK(conv[L.lin_index].size() == (size_t)m.conv_dim * (c.conv_kernel - 1) &&
+                      state[L.lin_index].size() == m.state_floats,
+                  kErrFormat, "recurrent state shape");
+      }
+    }
+    PGD_CHECK(rd.at == len, kErrFormat, "kv trailing bytes");
+    DeviceScope scope(m.dev);
+    held = new pgd_session();
+    Session& s = held->s;
+    s.model = &m;
+    m.live_sessions++;
+    if (m.rec_floats) {
+      void* p = nullptr;
+      hipError_t e = hipMalloc(&p, m.rec_floats * 4);
+      PGD_CHECK(e == hipSuccess, kErrAlloc, "hipMalloc session state");
+      s.rec = (float*)p;
+      PGD_HIP(hipMemset(p, 0, m.rec_floats * 4));
+    }
+    if (m.n_full) {
+      for (size_t i = 0; i < nblk; ++i) s.blocks.push_back(m.alloc_block());
+    }
+    std::vector<float> page(per_blk);
+    for (const Layer& L : m.layers) {
+      if (L.full) {
+        for (int which = 0; which < 2; ++which) {
+          const std::vector<float>& src = which == 0 ? kk[L.full_index] : vv[L.full_index];
+          float* pool = which == 0 ? L.k_pool : L.v_pool;
+          for (size_t bi = 0; bi < nblk; ++bi) {
+            std::fill(page.begin(), page.end(), 0.0f);
+            for (int sl = 0; sl < c.kv_block; ++sl) {
+              size_t p = bi * c.kv_block + sl;
+              if (p >= slen) break;
+              for (int h = 0; h < c.kv_heads; ++h)
+                memcpy(&page[((size_t)h * c.kv_block + sl) * c.head_dim], &src[(p * c.kv_heads + h) * c.head_dim],
+                       (size_t)c.head_dim * 4);
+            }
+            PGD_HIP(hipMemcpy(pool + (size_t)s.blocks[bi] * per_blk, page.data(), per_blk * 4, hipMemcpyHostToDevice));
+          }
+        }
+      } else {
+        float* base = s.rec + (size_t)L.lin_index * per_lin;
+        PGD_HIP(hipMemcpy(base, conv[L.lin_index].data(), conv[L.lin_index].size() * 4, hipMemcpyHostToDevice));
+        PGD_HIP(hipMemcpy(base + m.conv_floats, state[L.lin_index].data(), m.state_floats * 4, hipMemcpyHostToDevice));
+      }
+    }
+    s.len = (int)slen;
+    *out = held;
+  });
+  if (rc && held) delete held;
+  return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,108 @@
+// model.h — decode runtime: model weights on the device, paged KV pool,
+// per-session recurrent state and the ragged step that drives every forward.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "../../include/pagoda_hip.h"
+#include "device.h"
+#include "ops.h"
+#include "quant.h"
+
+namespace pgd {
+
+struct Layer {
+  bool full = false;
+  float* in_norm = nullptr;
+  float* post_norm = nullptr;
+  QMat gate, up, down;
+  // gated-delta (linear attention) layer
+  QMat qkv, z, a, b, out;
+  float* conv = nullptr;
+  float* a_log = nullptr;
+  float* dt_bias = nullptr;
+  float* gnorm = nullptr;
+  int lin_index = -1;
+  // full-attention layer
+  QMat q, k, v, o;
+  float* q_norm = nullptr;
+  float* k_norm = nullptr;
+  float* qb = nullptr;
+  float* kb = nullptr;
+  float* vb = nullptr;
+  int full_index = -1;
+  float* k_pool = nullptr;  // [kv_blocks][kv_heads][block][head_dim]
+  float* v_pool = nullptr;
+};
+
+struct Session;
+
+struct Model {
+  pgd_dev* dev = nullptr;
+  pgd_model_config cfg{};
+  int conv_dim = 0, key_dim = 0, value_dim = 0, q_out = 0, kv_width = 0;
+  QMat embed, head;
+  bool tied = false;
+  float* final_norm = nullptr;
+  std::vector<Layer> layers;
+  int n_lin = 0, n_full = 0;
+  size_t conv_floats = 0, state_floats = 0;  // per linear layer
+  size_t rec_floats = 0;                     // per session (all linear layers)
+  std::vector<void*> allocs;                 // small device vectors, KV pools
+
+  // KV page allocator (block ids shared by all full-attention layers)
+  std::vector<int> free_blocks;
+  std::vector<int> refcount;
+
+  // host rope tables, grown on demand
+  std::vector<float> cos_tab, sin_tab;
+  int rope_rows = 0;
+
+  // per-step workspace
+  DevBuf ws;
+  size_t ws_rows = 0;
+  DevBuf meta_dev;
+  size_t meta_cap = 0;
+  void* meta_host = nullptr;  // pinned
+  size_t meta_host_cap = 0;
+  DevBuf out_dev;  // ids / values / non-finite counts
+  size_t out_cap = 0;
+  void* out_host = nullptr;
+  size_t out_host_cap = 0;
+  int live_sessions = 0;
+
+  ~Model();
+  void ensure_rope(int pos);
+  int alloc_block();
+  void release_block(int b);
+  void copy_block(int dst, int src);
+};
+
+struct Session {
+  Model* model = nullptr;
+  int len = 0;
+  std::vector<int> blocks;
+  float* rec = nullptr;  // [n_lin][conv_floats + state_floats]
+  std::vector<float> last_logits;
+  bool has_logits = false;
+  ~Session();
+};
+
+// Output request of a step.
+struct StepOut {
+  // rows whose logits are computed: 0 = last row of each sequence, 1 = every row
+  int all_rows = 0;
+  int last_max = 0;           // argmax tie rule
+  uint32_t* ids = nullptr;    // host [n_logit_rows]
+  float* vals = nullptr;      // host [n_logit_rows] (max logit), nullable
+  float* logits = nullptr;    // host [n_logit_rows][vocab], nullable
+};
+
+// One forward over a ragged batch: sequence i feeds n[i] tokens. On a
+// validation error nothing is modified.
+void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, int nseq, StepOut& out);
+
+}  // namespace pgd

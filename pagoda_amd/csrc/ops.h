@@ -1,0 +1,114 @@
+// ops.h — decode-path kernels other than the quantized GEMVs: RMSNorm,
+// causal conv step, Gated-DeltaNet recurrence, q/k preparation with paged KV
+// writes, paged GQA decode attention and argmax. All take ragged batches:
+// `rows` token rows that belong to `nseq` sequences, sequence s owning rows
+// [row_start[s], row_start[s] + row_count[s]) in feed order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pgd {
+
+// y[r] = rmsnorm(x[src_row(r)]) * w, eps inside the sqrt.
+//   mode 0: x * (1/sqrt(mean(x^2)+eps)) * w   (rms_zero, qwen3_5.rs:1736-1745)
+//   mode 1: x / sqrt(mean(x^2)+eps) * w       (candle RmsNorm, qwen2_gguf.rs:92)
+// rows_idx (device, nullable) selects the source rows.
+void rmsnorm_rows(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps,
+                  int mode, float* y, int ldy, hipStream_t s);
+
+// Per-sequence metadata of a ragged step, on the device.
+struct SeqMeta {
+  const int* row_start;  // [nseq]
+  const int* row_count;  // [nseq]
+};
+
+// Depthwise causal conv decode step + SiLU with state shift
+// (qwen3_5.rs:1800-1853, kernel k, state [channels, k-1] per sequence).
+// x/out [rows, channels]; state_base[s] + state_off is the sequence's state.
+void conv_step(const float* x, int ldx, float* out, int ldo, int channels, int kernel, const float* weight,
+               float* const* state_base, size_t state_off, SeqMeta meta, int nseq, hipStream_t s);
+
+struct GdnParams {
+  int k_heads, v_heads, k_dim, v_dim;
+  const float* conv_out;  // [rows, 2*k_heads*k_dim + v_heads*v_dim]: q | k | v
+  int ld_conv;
+  const float* a;  // [rows, v_heads]
+  const float* b;  // [rows, v_heads]
+  int ld_ab;
+  const float* z;  // [rows, v_heads*v_dim]
+  int ld_z;
+  const float* a_log;    // [v_heads]
+  const float* dt_bias;  // [v_heads]
+  const float* norm;     // [v_dim]
+  float* out;            // [rows, v_heads*v_dim]
+  int ld_out;
+  float* const* state_base;  // per sequence; state at state_base[s] + state_off, [v_heads, k_dim, v_dim]
+  size_t state_off;
+};
+
+// Gated-DeltaNet recurrence over each sequence's rows in order
+// (qwen3_5.rs:1330-1383; Metal gated_delta_step, qwen3_fuse.rs:176-279).
+// k_dim == v_dim == 128. The fp32 state of a (sequence, head) is read once
+// into registers, stepped through all its rows, and written once.
+void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, hipStream_t s);
+
+struct AttnLayout {
+  int heads, kv_heads, head_dim, rotary_dim;
+  int block;  // tokens per KV page
+  // KV pool of this layer: [num_blocks][kv_heads][block][head_dim] f32, K and V
+  float* k_pool;
+  float* v_pool;
+};
+
+struct RowMeta {
+  const int* seq_of_row;      // [rows]
+  const int* pos_of_row;      // [rows] absolute position of the row's token
+  const int* block_tables;    // [nseq][max_blocks]
+  int max_blocks;
+  const float* cos;           // [rows][rotary_dim] (host-computed tables)
+  const float* sin;
+};
+
+// Full-attention q/k/v preparation and KV write.
+// qwen35 (variant 0): q_raw row = per head [q(hd) | gate(hd)]; q,k RMSNorm
+//   (q_norm/k_norm, eps 1e-6, rms_zero); partial rotate-half RoPE on the
+//   first rotary_dim dims (qwen3_5.rs:1389-1432).
+// qwen2 (variant 1): q_raw row = q; q/k/v biases added; full-width RoPE
+//   (qwen2_gguf.rs:233-250, 346-349).
+// Writes q [rows, heads, hd], gate [rows, heads, hd] (variant 0) and K/V
+// into the pages at each row's position.
+struct QkvPrep {
+  int variant;
+  const float* q_raw;
+  int ld_q;
+  const float* k_raw;
+  const float* v_raw;
+  int ld_kv;
+  const float* q_norm;
+  const float* k_norm;
+  const float* q_bias;
+  const float* k_bias;
+  const float* v_bias;
+  float* q;
+  float* gate;
+};
+void qkv_prep(const QkvPrep& p, const AttnLayout& L, const RowMeta& m, int rows, hipStream_t s);
+
+// Paged GQA decode attention: row r attends to positions [0, pos_of_row[r]]
+// of its sequence. out [rows, heads, hd]; gate (nullable) multiplies by
+// sigmoid(gate) (qwen3_5.rs:1433-1475; qwen2_gguf.rs:252-266).
+void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
+                 hipStream_t s);
+
+// Row-wise argmax over finite values. last_max = 0: first index among equal
+// maxima (pagoda/src/sampler.rs:59-69); 1: last (Iterator::max_by,
+// qwen3_5.rs:524-529). ids[r] = 0xFFFFFFFF when a row has no finite value;
+// nonfinite[r] counts non-finite entries.
+void argmax_rows(const float* x, int ld, int rows, int n, int last_max, uint32_t* ids, float* vals,
+                 int* nonfinite, hipStream_t s);
+
+// dst[r] = src[idx[r]] (rows of n floats)
+void gather_rows(const float* src, int lds, const int* idx, int rows, int n, float* dst, int ldd, hipStream_t s);
+
+}  // namespace pgd

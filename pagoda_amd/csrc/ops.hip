@@ -1,0 +1,489 @@
+// ops.hip — RMSNorm, causal conv step, Gated-DeltaNet recurrence, q/k/v
+// preparation with paged KV writes, paged GQA decode attention and argmax.
+#include "common.h"
+#include "ops.h"
+
+namespace pgd {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// block reductions (256 threads = 4 waves)
+// ---------------------------------------------------------------------------
+__device__ inline float block_sum256(float v, float* red4) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red4[w] = v;
+  __syncthreads();
+  float t = red4[0] + red4[1] + red4[2] + red4[3];
+  __syncthreads();
+  return t;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, int ldx, const int* rows_idx,
+                                                      int n, const float* __restrict__ w, float eps, int mode,
+                                                      float* __restrict__ y, int ldy) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const int src = rows_idx ? rows_idx[r] : r;
+  const float* xr = x + (size_t)src * ldx;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) ss += xr[i] * xr[i];
+  ss = block_sum256(ss, red);
+  float* yr = y + (size_t)r * ldy;
+  if (mode == 0) {
+    float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) yr[i] = xr[i] * inv * w[i];
+  } else {
+    float m = sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) yr[i] = xr[i] / m * w[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// causal conv step (sequential over a sequence's rows)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict__ x, int ldx, float* __restrict__ out,
+                                                        int ldo, int channels, int kernel,
+                                                        const float* __restrict__ weight, float* const* state_base,
+                                                        size_t state_off, const int* row_start, const int* row_count) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int s = blockIdx.y;
+  if (c >= channels) return;
+  const int hist = kernel - 1;
+  float* st = state_base[s] + state_off + (size_t)c * hist;
+  float win[8];
+  float wt[8];
+  for (int k = 0; k < hist; ++k) win[k] = st[k];
+  for (int k = 0; k < kernel; ++k) wt[k] = weight[(size_t)c * kernel + k];
+  const int r0 = row_start[s], n = row_count[s];
+  for (int t = 0; t < n; ++t) {
+    const float xv = x[(size_t)(r0 + t) * ldx + c];
+    float acc = 0.0f;
+    for (int k = 0; k < hist; ++k) acc += win[k] * wt[k];
+    acc += xv * wt[hist];
+    out[(size_t)(r0 + t) * ldo + c] = acc / (1.0f + expf(-acc));
+    for (int k = 0; k + 1 < hist; ++k) win[k] = win[k + 1];
+    if (hist > 0) win[hist - 1] = xv;
+  }
+  for (int k = 0; k < hist; ++k) st[k] = win[k];
+}
+
+// ---------------------------------------------------------------------------
+// Gated-DeltaNet
+// ---------------------------------------------------------------------------
+// One workgroup per (value head, sequence); 256 threads. Thread (rg, cg)
+// holds state rows 16rg..16rg+15, columns 4cg..4cg+3 in 64 registers for the
+// whole sequence chunk. Column sums over rows (S^T k, S^T q) are folded
+// through LDS across the 8 row groups.
+__device__ inline float softplus_f(float x) {
+  if (x > 20.0f) return x;
+  if (x < -20.0f) return expf(x);
+  return logf(1.0f + expf(x));
+}
+
+__global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_start, const int* row_count) {
+  constexpr int D = 128;
+  __shared__ float qs[D], ks[D], delta[D];
+  __shared__ float red[8][D];
+  __shared__ float part[4];
+  const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+  const int cg = tid & 31, rg = tid >> 5;
+  const int repeat = p.v_heads / p.k_heads;
+  const int kh = h / repeat;
+  const int key_dim = p.k_heads * D;
+  float* st = p.state_base[s] + p.state_off + (size_t)h * D * D;
+  float S[16][4];
+#pragma unroll
+  for (int ii = 0; ii < 16; ++ii) {
+    float4 v = *reinterpret_cast<const float4*>(st + (size_t)(16 * rg + ii) * D + 4 * cg);
+    S[ii][0] = v.x;
+    S[ii][1] = v.y;
+    S[ii][2] = v.z;
+    S[ii][3] = v.w;
+  }
+  const float a_log = p.a_log[h], dtb = p.dt_bias[h];
+  const float qscale = sqrtf((float)D);
+  const int r0 = row_start[s], n = row_count[s];
+  for (int t = 0; t < n; ++t) {
+    const int row = r0 + t;
+    const float* cv = p.conv_out + (size_t)row * p.ld_conv;
+    // q (threads 0..127) and k (128..255), L2-normalized per head
+    float v = tid < D ? cv[kh * D + tid] : cv[key_dim + kh * D + (tid - D)];
+    float ss = wave_sum(v * v);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    if (tid < D) {
+      float inv = 1.0f / sqrtf(part[0] + part[1] + 1e-6f);
+      qs[tid] = (v * inv) / qscale;
+    } else {
+      float inv = 1.0f / sqrtf(part[2] + part[3] + 1e-6f);
+      ks[tid - D] = v * inv;
+    }
+    const float g = -expf(a_log) * softplus_f(p.a[(size_t)row * p.ld_ab + h] + dtb);
+    const float decay = expf(g);
+    const float beta = 1.0f / (1.0f + expf(-p.b[(size_t)row * p.ld_ab + h]));
+    __syncthreads();
+    // S *= decay; mem = S^T k (partial over this thread's 16 rows)
+    float m4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ii = 0; ii < 16; ++ii) {
+      const float kv = ks[16 * rg + ii];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        S[ii][c] = S[ii][c] * decay;
+        m4[c] += S[ii][c] * kv;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[rg][4 * cg + c] = m4[c];
+    __syncthreads();
+    if (tid < D) {
+      float mem = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) mem += red[q][tid];
+      const float vv = cv[2 * key_dim + h * D + tid];
+      delta[tid] = (vv - mem) * beta;
+    }
+    __syncthreads();
+    // S += k delta^T ; o = S^T q (partial)
+    float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float dl[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dl[c] = delta[4 * cg + c];
+#pragma unroll
+    for (int ii = 0; ii < 16; ++ii) {
+      const float kv = ks[16 * rg + ii], qv = qs[16 * rg + ii];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        S[ii][c] = S[ii][c] + kv * dl[c];
+        o4[c] += S[ii][c] * qv;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[rg][4 * cg + c] = o4[c];
+    __syncthreads();
+    // gated RMSNorm over the head (qwen3_5.rs:1747-1756)
+    float o = 0.0f;
+    if (tid < D) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o += red[q][tid];
+    }
+    float oss = wave_sum(tid < D ? o * o : 0.0f);
+    if ((tid & 63) == 0) part[tid >> 6] = oss;
+    __syncthreads();
+    if (tid < D) {
+      const float inv = 1.0f / sqrtf((part[0] + part[1]) / (float)D + 1e-6f);
+      const float zg = p.z[(size_t)row * p.ld_z + h * D + tid];
+      p.out[(size_t)row * p.ld_out + h * D + tid] = o * inv * p.norm[tid] * (zg / (1.0f + expf(-zg)));
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int ii = 0; ii < 16; ++ii)
+    *reinterpret_cast<float4*>(st + (size_t)(16 * rg + ii) * D + 4 * cg) = make_float4(S[ii][0], S[ii][1], S[ii][2], S[ii][3]);
+}
+
+// ---------------------------------------------------------------------------
+// q/k/v preparation + paged KV write; one wave per (head or kv head, row)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void qkv_prep_kernel(QkvPrep p, AttnLayout L, RowMeta m) {
+  __shared__ float buf[512];
+  const int r = blockIdx.y;
+  const int hidx = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int hd = L.head_dim, rd = L.rotary_dim, half = rd / 2;
+  const int E = hd / 64;
+  const bool is_q = hidx < L.heads;
+  const int h = is_q ? hidx : hidx - L.heads;
+  const float* src;
+  const float* bias = nullptr;
+  const float* nw = nullptr;
+  if (is_q) {
+    src = p.q_raw + (size_t)r * p.ld_q + (size_t)h * hd * (p.variant == 0 ? 2 : 1);
+    bias = p.variant == 1 ? p.q_bias + (size_t)h * hd : nullptr;
+    nw = p.variant == 0 ? p.q_norm : nullptr;
+  } else {
+    src = p.k_raw + (size_t)r * p.ld_kv + (size_t)h * hd;
+    bias = p.variant == 1 ? p.k_bias + (size_t)h * hd : nullptr;
+    nw = p.variant == 0 ? p.k_norm : nullptr;
+  }
+  float v[4];
+  float ss = 0.0f;
+  for (int e = 0; e < E; ++e) {
+    const int d = lane + 64 * e;
+    v[e] = src[d];
+    if (bias) v[e] = v[e] + bias[d];
+    ss += v[e] * v[e];
+  }
+  if (nw) {
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)hd + 1e-6f);
+    for (int e = 0; e < E; ++e) v[e] = v[e] * inv * nw[lane + 64 * e];
+  }
+  for (int e = 0; e < E; ++e) buf[lane + 64 * e] = v[e];
+  __syncthreads();
+  const float* cs = m.cos + (size_t)r * rd;
+  const float* sn = m.sin + (size_t)r * rd;
+  for (int e = 0; e < E; ++e) {
+    const int d = lane + 64 * e;
+    if (d < rd) {
+      const float rot = d < half ? -buf[d + half] : buf[d - half];
+      v[e] = buf[d] * cs[d] + rot * sn[d];
+    }
+  }
+  if (is_q) {
+    float* qd = p.q + ((size_t)r * L.heads + h) * hd;
+    for (int e = 0; e < E; ++e) qd[lane + 64 * e] = v[e];
+    if (p.variant == 0) {
+      float* gd = p.gate + ((size_t)r * L.heads + h) * hd;
+      for (int e = 0; e < E; ++e) gd[lane + 64 * e] = src[hd + lane + 64 * e];
+    }
+  } else {
+    const int seq = m.seq_of_row[r], pos = m.pos_of_row[r];
+    const int blk = m.block_tables[(size_t)seq * m.max_blocks + pos / L.block];
+    const size_t off = (((size_t)blk * L.kv_heads + h) * L.block + (pos % L.block)) * hd;
+    const float* vs = p.v_raw + (size_t)r * p.ld_kv + (size_t)h * hd;
+    const float* vb = p.variant == 1 ? p.v_bias + (size_t)h * hd : nullptr;
+    for (int e = 0; e < E; ++e) {
+      const int d = lane + 64 * e;
+      L.k_pool[off + d] = v[e];
+      L.v_pool[off + d] = vb ? vs[d] + vb[d] : vs[d];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// paged GQA decode attention
+// ---------------------------------------------------------------------------
+// Workgroup (kv head, row), 4 waves. A position is LP = hd/4 lanes (float4
+// each); a wave covers PPW = 64/LP positions per step. Each lane group keeps
+// an online softmax per q head of the GQA group; groups are merged in LDS.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void attn_kernel(const float* __restrict__ q, const float* __restrict__ gate,
+                                                   float* __restrict__ out, AttnLayout L, RowMeta m) {
+  constexpr int LP = HD / 4;
+  constexpr int PPW = 64 / LP;
+  constexpr int NG = 4 * PPW;  // position groups per workgroup
+  __shared__ float s_m[NG][G], s_l[NG][G];
+  __shared__ float4 s_acc[NG][G][LP];
+  const int kvh = blockIdx.x, r = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = wave * PPW + lane / LP;  // position group
+  const int sub = lane % LP;               // float4 slot within the head
+  const int seq = m.seq_of_row[r];
+  const int len = m.pos_of_row[r] + 1;
+  const int* bt = m.block_tables + (size_t)seq * m.max_blocks;
+  const float scale = sqrtf((float)HD);
+  float4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    qv[g] = *reinterpret_cast<const float4*>(q + ((size_t)r * L.heads + kvh * G + g) * HD + 4 * sub);
+  float mx[G], l[G];
+  float4 acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    mx[g] = -INFINITY;
+    l[g] = 0.0f;
+    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int p0 = grp; p0 < len; p0 += NG) {
+    const int blk = bt[p0 / L.block];
+    const size_t off = (((size_t)blk * L.kv_heads + kvh) * L.block + (p0 % L.block)) * HD + 4 * sub;
+    const float4 kk = *reinterpret_cast<const float4*>(L.k_pool + off);
+    const float4 vv = *reinterpret_cast<const float4*>(L.v_pool + off);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d = qv[g].x * kk.x + qv[g].y * kk.y + qv[g].z * kk.z + qv[g].w * kk.w;
+      d = group_sum(d, LP);
+      const float sc = d / scale;
+      const float mn = fmaxf(mx[g], sc);
+      const float al = expf(mx[g] - mn);
+      const float e = expf(sc - mn);
+      l[g] = l[g] * al + e;
+      acc[g].x = acc[g].x * al + e * vv.x;
+      acc[g].y = acc[g].y * al + e * vv.y;
+      acc[g].z = acc[g].z * al + e * vv.z;
+      acc[g].w = acc[g].w * al + e * vv.w;
+      mx[g] = mn;
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (sub == 0) {
+      s_m[grp][g] = mx[g];
+      s_l[grp][g] = l[g];
+    }
+    s_acc[grp][g][sub] = acc[g];
+  }
+  __syncthreads();
+  for (int i = tid; i < G * LP; i += 256) {
+    const int g = i / LP, sl = i % LP;
+    float M = -INFINITY;
+    for (int k = 0; k < NG; ++k) M = fmaxf(M, s_m[k][g]);
+    float Lsum = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < NG; ++k) {
+      if (s_l[k][g] == 0.0f) continue;
+      const float w = expf(s_m[k][g] - M);
+      Lsum += s_l[k][g] * w;
+      const float4 a = s_acc[k][g][sl];
+      o.x += a.x * w;
+      o.y += a.y * w;
+      o.z += a.z * w;
+      o.w += a.w * w;
+    }
+    const int head = kvh * G + g;
+    const size_t oo = ((size_t)r * L.heads + head) * HD + 4 * sl;
+    float4 res = make_float4(o.x / Lsum, o.y / Lsum, o.z / Lsum, o.w / Lsum);
+    if (gate) {
+      const float4 gg = *reinterpret_cast<const float4*>(gate + oo);
+      res.x *= 1.0f / (1.0f + expf(-gg.x));
+      res.y *= 1.0f / (1.0f + expf(-gg.y));
+      res.z *= 1.0f / (1.0f + expf(-gg.z));
+      res.w *= 1.0f / (1.0f + expf(-gg.w));
+    }
+    *reinterpret_cast<float4*>(out + oo) = res;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// argmax
+// ---------------------------------------------------------------------------
+__device__ inline bool better(float v, int i, float bv, int bi, int last_max) {
+  if (bi < 0) return true;
+  if (v > bv) return true;
+  if (v < bv) return false;
+  return last_max ? i > bi : i < bi;
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int ld, int n, int last_max,
+                                                      uint32_t* ids, float* vals, int* nonfinite) {
+  __shared__ float sv[1024];
+  __shared__ int si[1024];
+  __shared__ int snf[1024];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const float* xr = x + (size_t)r * ld;
+  float bv = -INFINITY;
+  int bi = -1, nf = 0;
+  for (int i = tid; i < n; i += 1024) {
+    const float v = xr[i];
+    if (!isfinite(v)) {
+      nf++;
+      continue;
+    }
+    if (better(v, i, bv, bi, last_max)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  sv[tid] = bv;
+  si[tid] = bi;
+  snf[tid] = nf;
+  __syncthreads();
+  for (int s = 512; s > 0; s >>= 1) {
+    if (tid < s) {
+      const float v = sv[tid + s];
+      const int i = si[tid + s];
+      if (i >= 0 && better(v, i, sv[tid], si[tid], last_max)) {
+        sv[tid] = v;
+        si[tid] = i;
+      }
+      snf[tid] += snf[tid + s];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    ids[r] = si[0] < 0 ? 0xFFFFFFFFu : (uint32_t)si[0];
+    if (vals) vals[r] = sv[0];
+    if (nonfinite) nonfinite[r] = snf[0];
+  }
+}
+
+__global__ void gather_kernel(const float* src, int lds, const int* idx, int n, float* dst, int ldd) {
+  const int r = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[(size_t)r * ldd + i] = src[(size_t)idx[r] * lds + i];
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+void rmsnorm_rows(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps, int mode,
+                  float* y, int ldy, hipStream_t s) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx, n, w, eps, mode, y, ldy);
+  PGD_HIP(hipGetLastError());
+}
+
+void conv_step(const float* x, int ldx, float* out, int ldo, int channels, int kernel, const float* weight,
+               float* const* state_base, size_t state_off, SeqMeta meta, int nseq, hipStream_t s) {
+  PGD_CHECK(kernel >= 1 && kernel <= 8, kErrShape, "conv kernel must be in 1..8");
+  if (nseq <= 0) return;
+  hipLaunchKernelGGL(conv_step_kernel, dim3((channels + 255) / 256, nseq), dim3(256), 0, s, x, ldx, out, ldo, channels,
+                     kernel, weight, state_base, state_off, meta.row_start, meta.row_count);
+  PGD_HIP(hipGetLastError());
+}
+
+void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, hipStream_t s) {
+  PGD_CHECK(p.k_dim == 128 && p.v_dim == 128, kErrShape, "gated delta kernel needs k_dim == v_dim == 128");
+  PGD_CHECK(p.k_heads > 0 && p.v_heads % p.k_heads == 0, kErrShape, "v_heads must be a multiple of k_heads");
+  if (nseq <= 0) return;
+  hipLaunchKernelGGL(gdn_kernel, dim3(p.v_heads, nseq), dim3(256), 0, s, p, meta.row_start, meta.row_count);
+  PGD_HIP(hipGetLastError());
+}
+
+void qkv_prep(const QkvPrep& p, const AttnLayout& L, const RowMeta& m, int rows, hipStream_t s) {
+  PGD_CHECK(L.head_dim % 64 == 0 && L.head_dim <= 256, kErrShape, "head_dim must be 64, 128, 192 or 256");
+  PGD_CHECK(L.rotary_dim % 2 == 0 && L.rotary_dim <= L.head_dim, kErrShape, "rotary_dim");
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(qkv_prep_kernel, dim3(L.heads + L.kv_heads, rows), dim3(64), 0, s, p, L, m);
+  PGD_HIP(hipGetLastError());
+}
+
+template <int HD>
+static void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
+                    hipStream_t s) {
+  const int G = L.heads / L.kv_heads;
+  dim3 grid(L.kv_heads, rows);
+  switch (G) {
+    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
+    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
+    case 6: hipLaunchKernelGGL((attn_kernel<HD, 6>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
+    case 7: hipLaunchKernelGGL((attn_kernel<HD, 7>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
+    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
+    default: throw Error{kErrShape, "unsupported GQA group size " + std::to_string(G)};
+  }
+}
+
+void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
+                 hipStream_t s) {
+  PGD_CHECK(L.kv_heads > 0 && L.heads % L.kv_heads == 0, kErrShape, "heads must be a multiple of kv_heads");
+  if (rows <= 0) return;
+  switch (L.head_dim) {
+    case 64: attn_hd<64>(q, gate, out, L, m, rows, s); break;
+    case 128: attn_hd<128>(q, gate, out, L, m, rows, s); break;
+    case 256: attn_hd<256>(q, gate, out, L, m, rows, s); break;
+    default: throw Error{kErrShape, "attention head_dim must be 64, 128 or 256"};
+  }
+  PGD_HIP(hipGetLastError());
+}
+
+void argmax_rows(const float* x, int ld, int rows, int n, int last_max, uint32_t* ids, float* vals, int* nonfinite,
+                 hipStream_t s) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, s, x, ld, n, last_max, ids, vals, nonfinite);
+  PGD_HIP(hipGetLastError());
+}
+
+void gather_rows(const float* src, int lds, const int* idx, int rows, int n, float* dst, int ldd, hipStream_t s) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(gather_kernel, dim3((n + 255) / 256, rows), dim3(256), 0, s, src, lds, idx, n, dst, ldd);
+  PGD_HIP(hipGetLastError());
+}
+
+}  // namespace pgd

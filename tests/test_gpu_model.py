@@ -1,0 +1,198 @@
+"""End-to-end decode parity of the HIP backend against the CPU oracle on
+identical seeded weights (small configs here; the full configs are in
+test_gpu_configs.py)."""
+import numpy as np
+import pytest
+
+from oracle import pyoracle as ora
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3  # max |diff| / max |ref| per logits vector
+
+
+def rel(a, b):
+    return float(np.abs(a.astype(np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def small35(**kw):
+    from pagoda_amd.engine import ModelConfig
+
+    c = dict(arch=0, n_layers=8, hidden=256, intermediate=512, vocab=1024, heads=4, kv_heads=2, head_dim=128,
+             rotary_dim=32, rope_theta=1e7, eps=1e-6, k_heads=2, v_heads=4, k_dim=128, v_dim=128, conv_kernel=4,
+             full_every=4, max_pos=512, kv_block=16, kv_blocks=256)
+    c.update(kw)
+    return ModelConfig(**c)
+
+
+def small2(**kw):
+    from pagoda_amd.engine import ARCH_QWEN2, ModelConfig
+
+    c = dict(arch=ARCH_QWEN2, n_layers=3, hidden=256, intermediate=640, vocab=1024, heads=4, kv_heads=2, head_dim=64,
+             rotary_dim=64, rope_theta=1e6, eps=1e-6, k_heads=0, v_heads=0, k_dim=0, v_dim=0, conv_kernel=0,
+             full_every=1, max_pos=512, kv_block=16, kv_blocks=256)
+    c.update(kw)
+    return ModelConfig(**c)
+
+
+def oracle35(cfg, seed):
+    return ora.Qwen35(ora.Qwen35Config(
+        n_layers=cfg.n_layers, hidden=cfg.hidden, intermediate=cfg.intermediate, vocab=cfg.vocab, heads=cfg.heads,
+        kv_heads=cfg.kv_heads, head_dim=cfg.head_dim, rotary_dim=cfg.rotary_dim, rope_theta=cfg.rope_theta,
+        k_heads=cfg.k_heads, v_heads=cfg.v_heads, k_dim=cfg.k_dim, v_dim=cfg.v_dim, conv_kernel=cfg.conv_kernel,
+        full_every=cfg.full_every), seed)
+
+
+def oracle2(cfg, seed):
+    return ora.Qwen2(ora.Qwen2Config(
+        n_layers=cfg.n_layers, hidden=cfg.hidden, intermediate=cfg.intermediate, vocab=cfg.vocab, heads=cfg.heads,
+        kv_heads=cfg.kv_heads, head_dim=cfg.head_dim, max_pos=cfg.max_pos, rope_theta=cfg.rope_theta, eps=cfg.eps),
+        seed)
+
+
+@pytest.fixture(scope="module")
+def m35(dev):
+    from pagoda_amd.engine import Model
+
+    cfg = small35()
+    m = Model.synth(dev, cfg, 11)
+    yield m, oracle35(cfg, 11)
+
+
+@pytest.fixture(scope="module")
+def m2(dev):
+    from pagoda_amd.engine import Model
+
+    cfg = small2()
+    m = Model.synth(dev, cfg, 5)
+    yield m, oracle2(cfg, 5)
+
+
+@pytest.mark.parametrize("which", ["m35", "m2"])
+def test_prefill_then_greedy_decode_matches_oracle(which, request):
+    model, oracle = request.getfixturevalue(which)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, model.cfg.vocab, 11)
+    s = model.new_session()
+    oc = oracle.new_cache()
+    got = s.forward(prompt)
+    ref = oracle.forward(prompt, oc)
+    assert rel(got, ref) < LOGIT_TOL
+    tok = int(np.argmax(ref))
+    for step in range(16):
+        assert int(np.argmax(got)) == int(np.argmax(ref)), f"greedy token diverged at step {step}"
+        got = s.forward([tok])
+        ref = oracle.forward([tok], oc)
+        assert rel(got, ref) < LOGIT_TOL, f"step {step}: {rel(got, ref)}"
+        tok = int(np.argmax(ref))
+    assert s.context_len() == 11 + 16
+    # empty feed replays the cached logits (pagoda/src/model.rs:153-157)
+    np.testing.assert_array_equal(s.forward([]), got)
+
+
+@pytest.mark.parametrize("which", ["m35", "m2"])
+def test_ragged_batch_bitwise_equals_serial(which, request):
+    """Batched step == per-session forwards (pagoda/tests/batch_tests.rs:217-242);
+    every kernel computes rows independently, so the logits are bitwise equal."""
+    model, _ = request.getfixturevalue(which)
+    rng = np.random.default_rng(4)
+    prompts = [rng.integers(0, model.cfg.vocab, n) for n in (5, 9, 1, 17)]
+    serial = [model.new_session() for _ in prompts]
+    batched = [model.new_session() for _ in prompts]
+    ser_logits = [s.forward(p) for s, p in zip(serial, prompts)]
+    _, bl = model.step_ragged(batched, prompts, want_logits=True)
+    for i in range(len(prompts)):
+        np.testing.assert_array_equal(bl[i].view(np.uint32), ser_logits[i].view(np.uint32))
+    # mixed decode rows and 4-token chunks in one step
+    feeds = [[int(np.argmax(ser_logits[0]))], rng.integers(0, model.cfg.vocab, 4), [7], rng.integers(0, 100, 3)]
+    ser = [s.forward(f) for s, f in zip(serial, feeds)]
+    _, bl = model.step_ragged(batched, feeds, want_logits=True)
+    for i in range(len(feeds)):
+        np.testing.assert_array_equal(bl[i].view(np.uint32), ser[i].view(np.uint32))
+    assert [s.context_len() for s in batched] == [s.context_len() for s in serial]
+
+
+def test_verify_equals_serial_greedy(m35):
+    """forward_verify(4) == 4 serial greedy steps (pagoda-hf/examples/qwen3_8.rs:219-247)."""
+    model, _ = m35
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, model.cfg.vocab, 6)
+    a = model.new_session()
+    a.forward(prompt[:-1])
+    b = a.fork()
+    inp = int(prompt[-1])
+    produced = []
+    for _ in range(4):
+        t, v = a.forward_greedy(inp)
+        produced.append((t, v))
+        inp = t
+    inputs = [int(prompt[-1])] + [t for t, _ in produced[:3]]
+    got = b.forward_verify(inputs)
+    assert [t for t, _ in got] == [t for t, _ in produced]
+    for (_, v1), (_, v2) in zip(got, produced):
+        assert v1 == v2  # same per-row kernels: bitwise
+    assert a.context_len() == b.context_len()
+
+
+def test_fork_continues_independently(m35):
+    model, oracle = m35
+    rng = np.random.default_rng(6)
+    prompt = rng.integers(0, model.cfg.vocab, 21)  # crosses a 16-token page
+    s = model.new_session()
+    s.forward(prompt)
+    f = s.fork()
+    a1 = s.forward([3, 4])
+    b1 = f.forward([3, 4])
+    np.testing.assert_array_equal(a1, b1)
+    a2 = s.forward([9])
+    b2 = f.forward([10])  # diverge: the shared tail page is copied on write
+    a3 = s.forward([5])
+    oc = oracle.new_cache()
+    oracle.forward(prompt, oc)
+    oracle.forward([3, 4], oc)
+    ref_b2 = oracle.forward([10], oc.clone())
+    ref_a2 = oracle.forward([9], oc)
+    ref_a3 = oracle.forward([5], oc)
+    assert rel(a2, ref_a2) < LOGIT_TOL and rel(b2, ref_b2) < LOGIT_TOL and rel(a3, ref_a3) < LOGIT_TOL
+    f.free()
+
+
+def test_export_import_round_trip(m35):
+    """Cache bytes v1 (pagoda-hf/src/qwen3_5.rs:177-255): same layout as the
+    oracle's to_bytes, values within tolerance, and an imported session
+    continues exactly like the exported one."""
+    model, oracle = m35
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, model.cfg.vocab, 19)
+    s = model.new_session()
+    s.forward(prompt)
+    blob = s.export_kv()
+    oc = oracle.new_cache()
+    oracle.forward(prompt, oc)
+    ref = oc.to_bytes()
+    assert len(blob) == len(ref)
+    assert blob[:16] == ref[:16]
+    g = np.frombuffer(blob[16:], np.uint8)
+    r = np.frombuffer(ref[16:], np.uint8)
+    # tags and counts identical; float payloads within tolerance
+    t = model.import_session(blob)
+    assert t.context_len() == 19
+    np.testing.assert_array_equal(t.forward([1]), s.forward([1]))
+    assert g.size == r.size
+
+
+def test_argument_errors_are_atomic(m35):
+    from pagoda_amd import PagodaError
+
+    model, _ = m35
+    s = model.new_session()
+    s.forward([1, 2, 3])
+    t = model.new_session()
+    with pytest.raises(PagodaError):
+        model.step_ragged([s, t], [[1], [model.cfg.vocab + 5]])  # bad token in one row
+    assert s.context_len() == 3 and t.context_len() == 0
+    with pytest.raises(PagodaError):
+        model.step_ragged([s, s], [[1], [2]])  # duplicate session
+    assert s.context_len() == 3
+    with pytest.raises(PagodaError):
+        s.forward_verify([1, 2, 3, 4, 5])
