@@ -155,7 +155,7 @@ static int new_matrix(pgd_dev* dev, int fmt, int n_out, int n_in, pgd_matrix** o
   PGD_CHECK(dev && out, kErrArg, "null argument");
   auto* m = new pgd_matrix{dev, QMat{}};
   *held = m;
-  qmat_alloc(m->m, fmt, n_out, n_in);
+  qmat_alloc(m->m, fmt, n_out, n_in, dev->stream);
   return 0;
 }
 

@@ -1,11 +1,11 @@
 // gemv_impl.h — GEMV kernel templates shared by the per-format
 // instantiation files (gemv_a8.hip, gemv_q4k.hip, gemv_q6k.hip).
 //
-// Dequant-in-register GEMV / skinny GEMM for MLX affine-8 (group 64) and
-// GGML Q4_K / Q6_K matrices.
+// Dequant-in-register GEMV / skinny GEMM on the vector ALUs for GGML Q4_K /
+// Q6_K matrices (MLX affine-8 runs on the matrix cores, gemv_mma.hip).
 //
 // GEMV mapping (wave64): a wave owns ROWS consecutive output rows. A row is
-// cut into 16-byte chunks of its main plane (A8 codes / Q4K qs / Q6K ql);
+// cut into 16-byte chunks of its main plane (Q4K qs / Q6K ql);
 // lane l takes chunks l, l+64, ... so every load instruction of the wave
 // reads 1 KiB of one row contiguously (128-bit per lane). The activation
 // values a chunk needs are loaded once per chunk and reused for the ROWS
@@ -85,35 +85,6 @@ __device__ inline uint32_t byte_of(uint4 q, int i) {
 }
 
 // ---- per-format chunk logic ------------------------------------------------
-// A8: chunk p = codes [16p, 16p+16) of a row; group p/4.
-struct A8 {
-  struct W {
-    uint4 q;
-    uint32_t sb;
-  };
-  static __device__ inline int chunks(const GemvArgs& a) { return a.n_in >> 4; }
-  static __device__ inline bool pos(const GemvArgs& a, int p, int& lo, int& hi) {
-    lo = p << 4;
-    hi = -1;
-    return true;
-  }
-  static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t*, const uint8_t*,
-                                  const GemvArgs& a, int row, int p) {
-    W w;
-    w.q = *reinterpret_cast<const uint4*>(c0 + (size_t)row * a.n_in + ((size_t)p << 4));
-    w.sb = reinterpret_cast<const uint32_t*>(c1)[(size_t)row * (a.n_in >> 6) + (p >> 2)];
-    return w;
-  }
-  // pagoda-hf/src/qwen3_gemv.rs:96-99: r = fma(scale, sum(code*x), fma(sum(x), bias, r))
-  static __device__ inline float acc(float r, const W& w, const float* xl, const float*, float sl, float) {
-    float d = (float)byte_of(w.q, 0) * xl[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) d = fmaf((float)byte_of(w.q, i), xl[i], d);
-    float s = bf16_to_f32(w.sb & 0xffffu), b = bf16_to_f32(w.sb >> 16);
-    return fmaf(s, d, fmaf(sl, b, r));
-  }
-};
-
 // Q4K: chunk p = qs bytes [16p, 16p+16): block p/8, part p%8 -> 64-group
 // j = part/2, half h = part%2. Low nibbles are elements 64j+16h+i of
 // sub-block 2j, high nibbles 64j+32+16h+i of sub-block 2j+1.
@@ -233,15 +204,6 @@ struct Acc {
     return F::acc(r, w, xl, xh, sl, sh, p, has_hi);
   }
 };
-template <>
-struct Acc<A8> {
-  template <class W>
-  static __device__ inline float run(float r, const W& w, const float* xl, const float* xh, float sl, float sh,
-                                     int, bool) {
-    return A8::acc(r, w, xl, xh, sl, sh);
-  }
-};
-
 template <class F, int ROWS, int NB, bool XF16, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
   const int lane = threadIdx.x & 63;
@@ -342,9 +304,13 @@ void launch_rows(GemvArgs a, int nrows, hipStream_t s) {
 
 
 // entry points of the instantiation files
-void run_a8(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 void run_q4k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 void run_q6k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
+// Per-stream device scratch for GEMV activation prep (grows, never shrinks;
+// growing drains the stream first).
+void* gemv_scratch(hipStream_t s, size_t bytes);
+// A8 on the matrix cores (f32 activations)
+void run_a8_mma(const GemvArgs& a, int nrows, int epi, hipStream_t s);
 
 }  // namespace gemv
 }  // namespace pgd

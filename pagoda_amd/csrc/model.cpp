@@ -166,13 +166,13 @@ static void build_synth(Model& m, uint64_t seed) {
     m.value_dim = c.v_heads * c.v_dim;
     m.conv_dim = 2 * m.key_dim + m.value_dim;
     m.q_out = c.heads * c.head_dim * 2;
-    qmat_alloc(m.embed, FMT_A8, c.vocab, H);
+    qmat_alloc(m.embed, FMT_A8, c.vocab, H, s);
     qmat_synth(m.embed, seed, tkey(-1, K_EMBED), 0.02f, s);
-    qmat_alloc(m.head, FMT_A8, c.vocab, H);
+    qmat_alloc(m.head, FMT_A8, c.vocab, H, s);
     qmat_synth(m.head, seed, tkey(-1, K_HEAD), 0.02f, s);
   } else {
     m.q_out = c.heads * c.head_dim;
-    qmat_alloc(m.embed, FMT_Q6K, c.vocab, H);
+    qmat_alloc(m.embed, FMT_Q6K, c.vocab, H, s);
     qmat_synth(m.embed, seed, tkey(-1, K_EMBED), 0.02f, s);
     m.head = m.embed;  // tied lm_head (qwen2_gguf.rs:96-99)
     m.tied = true;
@@ -181,7 +181,7 @@ static void build_synth(Model& m, uint64_t seed) {
   m.layers.resize(c.n_layers);
   size_t kv_per_layer = (size_t)c.kv_blocks * c.kv_heads * c.kv_block * c.head_dim;
   auto mat = [&](QMat& q, int fmt, int n_out, int n_in, int li, int kind) {
-    qmat_alloc(q, fmt, n_out, n_in);
+    qmat_alloc(q, fmt, n_out, n_in, s);
     qmat_synth(q, seed, tkey(li, kind), 0.02f, s);
   };
   for (int i = 0; i < c.n_layers; ++i) {
@@ -845,7 +845,8 @@ int pgd_session_import(pgd_model* pm, const uint8_t* buf, size_t len, pgd_sessio
       hipError_t e = hipMalloc(&p, m.rec_floats * 4);
       PGD_CHECK(e == hipSuccess, kErrAlloc, "hipMalloc session state");
       s.rec = (float*)p;
-      PGD_HIP(hipMemset(p, 0, m.rec_floats * 4));
+      PGD_HIP(hipMemsetAsync(p, 0, m.rec_floats * 4, m.dev->stream));
+      PGD_HIP(hipStreamSynchronize(m.dev->stream));
     }
     if (m.n_full) {
       for (size_t i = 0; i < nblk; ++i) s.blocks.push_back(m.alloc_block());

@@ -4,8 +4,11 @@
 // per matrix holds structure-of-arrays planes so each wave streams one plane
 // with 128-bit loads:
 //
-//   A8  (MLX affine, group 64):  codes u8 [n_out][n_in]        (the packed u32 words, same bytes)
-//                                sb    u32 [n_out][n_in/64]     bf16 scale | bf16 bias << 16
+//   A8  (MLX affine, group 64):  codes u8, tiled: for each 32-row tile and
+//                                64-wide group a 2 KiB block [k half][row][32 codes]
+//                                (the order the matrix-core lanes read it)
+//                                sb    u32, tiled [tile][group][32 rows]: bf16 scale | bf16 bias << 16
+//                                rows are padded to a multiple of 32 with zeros
 //   Q4K (GGML block_q4_K):       qs    u8 [n_out][nsb*128]      the 128 nibble bytes of each block
 //                                hdr   16B [n_out][nsb]         d, dmin (f16) + 12 packed scale bytes
 //   Q6K (GGML block_q6_K):       ql    u8 [n_out][nsb*128]
@@ -36,12 +39,22 @@ struct QMat {
   uint8_t* p3 = nullptr;  //                      Q6K d
 };
 
+// A8 tiled addressing (G = n_in / 64 groups per row)
+__host__ __device__ inline size_t a8_code_off(int row, int k, int G) {
+  return ((((size_t)(row >> 5) * G + (k >> 6)) << 11) + (size_t)(((k >> 5) & 1) << 10) + (size_t)((row & 31) << 5) +
+          (size_t)(k & 31));
+}
+__host__ __device__ inline size_t a8_sb_off(int row, int g, int G) {
+  return (((size_t)(row >> 5) * G + g) << 5) + (size_t)(row & 31);
+}
+
 // algorithmic bytes of the weights (what a GEMV must stream at least once;
 // unpadded n_in as the measurement plan defines it)
 double qmat_algo_bytes(const QMat& m);
 
-// allocate planes for a matrix (device memory, uninitialised)
-void qmat_alloc(QMat& m, int fmt, int n_out, int n_in);
+// allocate planes for a matrix on the device; A8 padding rows are zeroed on
+// stream s (everything else is written by the upload or synth that follows)
+void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s);
 void qmat_free(QMat& m);
 
 // host source blocks -> device planes

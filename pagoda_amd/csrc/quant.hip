@@ -1,6 +1,8 @@
 // quant.hip — quantized matrix storage: allocation, upload, dequant,
 // embedding rows, the GEMV front end and the seeded synthetic generator.
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -15,7 +17,10 @@ namespace {
 
 void run_fmt(const QMat& m, const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s) {
   switch (m.fmt) {
-    case FMT_A8: run_a8(a, nrows, x_f16, epi, s); break;
+    case FMT_A8:
+      PGD_CHECK(!x_f16, kErrArg, "A8 matrices take f32 activations");
+      run_a8_mma(a, nrows, epi, s);
+      break;
     case FMT_Q4K: run_q4k(a, nrows, x_f16, epi, s); break;
     case FMT_Q6K: run_q6k(a, nrows, x_f16, epi, s); break;
     default: throw Error{kErrFormat, "unknown matrix format"};
@@ -44,8 +49,9 @@ __global__ void dequant_a8_kernel(const uint8_t* codes, const uint32_t* sb, int 
   if (t >= (size_t)rows * runs) return;
   int r = (int)(t / runs), c = (int)(t % runs);
   int row = ids ? (int)ids[r] : row0 + r;
-  uint4 q = *reinterpret_cast<const uint4*>(codes + (size_t)row * n_in + c * 16);
-  uint32_t v = sb[(size_t)row * (n_in >> 6) + (c >> 2)];
+  const int G = n_in >> 6;
+  uint4 q = *reinterpret_cast<const uint4*>(codes + a8_code_off(row, c * 16, G));
+  uint32_t v = sb[a8_sb_off(row, c >> 2, G)];
   float s = bf16_to_f32(v & 0xffffu), b = bf16_to_f32(v >> 16);
   float* o = out + (size_t)r * ldo + c * 16;
 #pragma unroll
@@ -202,10 +208,13 @@ __global__ void synth_a8_kernel(uint8_t* codes, uint32_t* sb, int n_out, int n_i
     float q = clampf(rintf((w[i] - bias) / scale), 0.0f, 255.0f);
     words[i >> 2] |= (uint32_t)q << (8 * (i & 3));
   }
-  uint4* dst = reinterpret_cast<uint4*>(codes + base);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dst[i] = make_uint4(words[4 * i], words[4 * i + 1], words[4 * i + 2], words[4 * i + 3]);
-  sb[r * groups + g] = (uint32_t)f32_to_bf16(scale) | ((uint32_t)f32_to_bf16(bias) << 16);
+  uint4* d0 = reinterpret_cast<uint4*>(codes + a8_code_off((int)r, g * 64, groups));
+  uint4* d1 = reinterpret_cast<uint4*>(codes + a8_code_off((int)r, g * 64 + 32, groups));
+  d0[0] = make_uint4(words[0], words[1], words[2], words[3]);
+  d0[1] = make_uint4(words[4], words[5], words[6], words[7]);
+  d1[0] = make_uint4(words[8], words[9], words[10], words[11]);
+  d1[1] = make_uint4(words[12], words[13], words[14], words[15]);
+  sb[a8_sb_off((int)r, g, groups)] = (uint32_t)f32_to_bf16(scale) | ((uint32_t)f32_to_bf16(bias) << 16);
 }
 
 __device__ inline float synth_w(uint64_t stream, float std, size_t r, int n_in, int k) {
@@ -333,6 +342,28 @@ __global__ void fill_kernel(float* out, size_t n, float v) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
+namespace gemv {
+void* gemv_scratch(hipStream_t s, size_t bytes) {
+  static std::mutex mu;
+  static std::map<hipStream_t, std::pair<void*, size_t>> bufs;
+  std::lock_guard<std::mutex> lock(mu);
+  auto& e = bufs[s];
+  if (e.second < bytes) {
+    if (e.first) {
+      PGD_HIP(hipStreamSynchronize(s));
+      PGD_HIP(hipFree(e.first));
+      e.first = nullptr;
+      e.second = 0;
+    }
+    size_t want = std::max(bytes, (size_t)4 << 20);
+    hipError_t err = hipMalloc(&e.first, want);
+    if (err != hipSuccess) throw Error{kErrAlloc, std::string("hipMalloc gemv scratch: ") + hipGetErrorString(err)};
+    e.second = want;
+  }
+  return e.first;
+}
+}  // namespace gemv
+
 double qmat_algo_bytes(const QMat& m) {
   double n = (double)m.n_out * (double)m.n_in;
   switch (m.fmt) {
@@ -343,7 +374,7 @@ double qmat_algo_bytes(const QMat& m) {
   return 0.0;
 }
 
-void qmat_alloc(QMat& m, int fmt, int n_out, int n_in) {
+void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s) {
   PGD_CHECK(n_out > 0 && n_in > 0, kErrShape, "matrix dims must be positive");
   m.fmt = fmt;
   m.n_out = n_out;
@@ -359,8 +390,9 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in) {
   };
   if (fmt == FMT_A8) {
     PGD_CHECK(n_in % 64 == 0, kErrShape, "A8 n_in must be a multiple of 64");
-    place(0, rows * n_in);
-    place(1, rows * (n_in / 64) * 4);
+    size_t tiles = (rows + 31) / 32;
+    place(0, tiles * (n_in / 64) * 2048);
+    place(1, tiles * (n_in / 64) * 128);
   } else if (fmt == FMT_Q4K) {
     PGD_CHECK(n_in % 32 == 0, kErrShape, "Q4K n_in must be a multiple of 32");
     place(0, rows * m.nsb * 128);
@@ -383,6 +415,9 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in) {
   m.p1 = m.base + off[1];
   m.p2 = fmt == FMT_Q6K ? m.base + off[2] : nullptr;
   m.p3 = fmt == FMT_Q6K ? m.base + off[3] : nullptr;
+  // zero the padding rows of the last tile, ordered before the writes that
+  // follow on the same stream
+  if (fmt == FMT_A8) PGD_HIP(hipMemsetAsync(m.base, 0, total, s));
 }
 
 void qmat_free(QMat& m) {
@@ -392,11 +427,20 @@ void qmat_free(QMat& m) {
 
 void qmat_upload_a8(QMat& m, const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
                     hipStream_t s) {
-  size_t groups = (size_t)m.n_out * (m.n_in / 64);
-  std::vector<uint32_t> sb(groups);
-  for (size_t i = 0; i < groups; ++i) sb[i] = (uint32_t)scales[i] | ((uint32_t)biases[i] << 16);
-  PGD_HIP(hipMemcpyAsync(m.p0, packed, (size_t)m.n_out * m.n_in, hipMemcpyHostToDevice, s));
-  PGD_HIP(hipMemcpyAsync(m.p1, sb.data(), groups * 4, hipMemcpyHostToDevice, s));
+  // MLX row-major packed codes -> tiled blocks (same bytes, permuted)
+  const int G = m.n_in / 64;
+  const size_t tiles = ((size_t)m.n_out + 31) / 32;
+  std::vector<uint8_t> codes(tiles * G * 2048, 0);
+  std::vector<uint32_t> sb(tiles * G * 32, 0);
+  const uint8_t* src = reinterpret_cast<const uint8_t*>(packed);
+  for (int r = 0; r < m.n_out; ++r) {
+    for (int k = 0; k < m.n_in; k += 32)
+      std::copy(src + (size_t)r * m.n_in + k, src + (size_t)r * m.n_in + k + 32, codes.data() + a8_code_off(r, k, G));
+    for (int g = 0; g < G; ++g)
+      sb[a8_sb_off(r, g, G)] = (uint32_t)scales[(size_t)r * G + g] | ((uint32_t)biases[(size_t)r * G + g] << 16);
+  }
+  PGD_HIP(hipMemcpyAsync(m.p0, codes.data(), codes.size(), hipMemcpyHostToDevice, s));
+  PGD_HIP(hipMemcpyAsync(m.p1, sb.data(), sb.size() * 4, hipMemcpyHostToDevice, s));
   PGD_HIP(hipStreamSynchronize(s));
 }
 
