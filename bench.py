@@ -37,6 +37,7 @@ def log(*a):
 def gpu_bench(args):
     from pagoda_amd import Device, Event, Matrix
     from pagoda_amd.engine import QWEN35_27B, Model
+    from pagoda_amd.matrix import act_bytes, act_prep_dev
 
     dev = Device(os.environ.get("PAGODA_DEVICE", "hip"))
     batch = args.batch
@@ -91,36 +92,35 @@ def gpu_bench(args):
     model.free()
 
     # ---- dominant kernel: fused gate/up SwiGLU GEMV at the step's shape ----
+    # (the decode step feeds it activations prepared by the fused RMSNorm;
+    # here they are prepared once and only the GEMV kernel is timed)
     H, I = cfg.hidden, cfg.intermediate
     g = Matrix.synth(dev, 0, I, H, 2026, (0 << 8) | 12)
     u = Matrix.synth(dev, 0, I, H, 2026, (0 << 8) | 13)
-    rows = batch
-    x = dev.upload(rng.normal(0, 1, (rows, H)).astype(np.float32))
-    mid = dev.alloc(rows * I * 4)
-    for _ in range(3):
-        Matrix.gemv_swiglu_dev(g, u, x, H, rows, mid, I)
     launches = 40
-    e0 = Event(dev).record()
-    for _ in range(launches):
-        Matrix.gemv_swiglu_dev(g, u, x, H, rows, mid, I)
-    e1 = Event(dev).record()
-    avg_ms = e0.elapsed_ms(e1) / launches
-    algo = g.algo_bytes + u.algo_bytes + rows * H * 4 + rows * I * 4
+
+    def time_swiglu(rows):
+        x = dev.upload(rng.normal(0, 1, (rows, H)).astype(np.float32))
+        act = dev.alloc(act_bytes(rows, H))
+        mid = dev.alloc(rows * I * 4)
+        act_prep_dev(dev, x, H, rows, H, act)
+        for _ in range(3):
+            Matrix.gemv_swiglu_act_dev(g, u, act, rows, mid, I)
+        e0 = Event(dev).record()
+        for _ in range(launches):
+            Matrix.gemv_swiglu_act_dev(g, u, act, rows, mid, I)
+        e1 = Event(dev).record()
+        avg_ms = e0.elapsed_ms(e1) / launches
+        algo = g.algo_bytes + u.algo_bytes + rows * H * 4 + rows * I * 4
+        for p in (x, act, mid):
+            dev.free(p)
+        return avg_ms, algo
+
+    avg_ms, algo = time_swiglu(batch)
     achieved = algo / (avg_ms * 1e-3) / 1e9
-    # batch-1 shape of the same kernel
-    x1 = dev.upload(rng.normal(0, 1, (1, H)).astype(np.float32))
-    for _ in range(3):
-        Matrix.gemv_swiglu_dev(g, u, x1, H, 1, mid, I)
-    e0 = Event(dev).record()
-    for _ in range(launches):
-        Matrix.gemv_swiglu_dev(g, u, x1, H, 1, mid, I)
-    e1 = Event(dev).record()
-    avg1 = e0.elapsed_ms(e1) / launches
-    algo1 = g.algo_bytes + u.algo_bytes + H * 4 + I * 4
-    log(f"swiglu GEMV {rows} rows: {avg_ms * 1e3:.1f} us, {achieved:.0f} GB/s; 1 row: {avg1 * 1e3:.1f} us, "
+    avg1, algo1 = time_swiglu(1)
+    log(f"swiglu GEMV kernel {batch} rows: {avg_ms * 1e3:.1f} us, {achieved:.0f} GB/s; 1 row: {avg1 * 1e3:.1f} us, "
         f"{algo1 / (avg1 * 1e-3) / 1e9:.0f} GB/s")
-    for p in (x, x1, mid):
-        dev.free(p)
     g.free()
     u.free()
     return {

@@ -98,6 +98,16 @@ int pgd_matrix_gemv_dev(const pgd_matrix* m, const void* x, int x_f16, int ldx, 
  * (qwen3_gemv.rs:256-286). */
 int pgd_matrix_gemv_swiglu_dev(const pgd_matrix* gate, const pgd_matrix* up, const float* x, int ldx,
                                int nrows, float* mid, int ldm);
+/* A8 activations converted once into matrix-core operands, shared by every
+ * A8 matrix of width k (the reference shares one x across several matrices
+ * the same way: gemv_shared / affine_gemv_n, qwen3_gemv.rs:149-253).
+ * pgd_act_bytes gives the device buffer size for nrows x k. */
+size_t pgd_act_bytes(int nrows, int k);
+int pgd_act_prep_dev(pgd_dev* dev, const float* x, int ldx, int nrows, int k, void* act);
+int pgd_matrix_gemv_act_dev(const pgd_matrix* m, const void* act, int nrows, float* y, int ldy, const float* res,
+                            int ldres);
+int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up, const void* act, int nrows,
+                                   float* mid, int ldm);
 
 /* ---- models and sessions ---------------------------------------------------
  * Architecture of a model handle. arch 0 is the hybrid Qwen3.5 tower

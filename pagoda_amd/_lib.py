@@ -40,6 +40,10 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_matrix_gemv": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "pgd_matrix_gemv_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int]),
     "pgd_matrix_gemv_swiglu_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int]),
+    "pgd_act_bytes": (c_size_t, [c_int, c_int]),
+    "pgd_act_prep_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "pgd_matrix_gemv_act_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_int]),
+    "pgd_matrix_gemv_swiglu_act_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int]),
     "pgd_model_synth": (c_int, [c_void_p, c_void_p, c_uint64, P(c_void_p)]),
     "pgd_model_free": (c_int, [c_void_p]),
     "pgd_model_info": (c_int, [c_void_p, P(c_size_t), P(c_double), P(c_int)]),

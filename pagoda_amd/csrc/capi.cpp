@@ -280,4 +280,39 @@ int pgd_matrix_gemv_swiglu_dev(const pgd_matrix* gate, const pgd_matrix* up, con
   });
 }
 
+size_t pgd_act_bytes(int nrows, int k) { return nrows > 0 && k > 0 ? a8_act_bytes(nrows, k) : 0; }
+
+int pgd_act_prep_dev(pgd_dev* dev, const float* x, int ldx, int nrows, int k, void* act) {
+  return guard([&] {
+    PGD_CHECK(dev && x && act && nrows > 0, kErrArg, "bad argument");
+    PGD_CHECK(k % 64 == 0 && ldx >= k && ldx % 4 == 0, kErrShape, "activation width must be a multiple of 64");
+    DeviceScope scope(dev);
+    a8_act_prep(x, ldx, nrows, k, act, dev->stream);
+  });
+}
+
+int pgd_matrix_gemv_act_dev(const pgd_matrix* m, const void* act, int nrows, float* y, int ldy, const float* res,
+                            int ldres) {
+  return guard([&] {
+    PGD_CHECK(m && act && y && nrows > 0, kErrArg, "bad argument");
+    PGD_CHECK(m->m.fmt == FMT_A8, kErrFormat, "prepared activations feed A8 matrices");
+    PGD_CHECK(ldy >= m->m.n_out && (!res || ldres >= m->m.n_out), kErrShape, "gemv output stride");
+    DeviceScope scope(m->dev);
+    A8Act a = a8_act_view(const_cast<void*>(act), nrows, m->m.n_in);
+    qmat_gemv_a8(m->m, a, y, ldy, res, ldres, m->dev->stream);
+  });
+}
+
+int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up, const void* act, int nrows,
+                                   float* mid, int ldm) {
+  return guard([&] {
+    PGD_CHECK(gate && up && act && mid && nrows > 0, kErrArg, "bad argument");
+    PGD_CHECK(gate->dev == up->dev, kErrArg, "gate and up live on different devices");
+    PGD_CHECK(ldm >= gate->m.n_out, kErrShape, "swiglu output stride");
+    DeviceScope scope(gate->dev);
+    A8Act a = a8_act_view(const_cast<void*>(act), nrows, gate->m.n_in);
+    qmat_gemv_a8_swiglu(gate->m, up->m, a, mid, ldm, gate->dev->stream);
+  });
+}
+
 }  // extern "C"

@@ -56,8 +56,8 @@ __device__ inline void load_x16(const void* x, size_t off, float* v) {
     uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      v[2 * i] = f16_to_f32(w[i] & 0xffffu);
-      v[2 * i + 1] = f16_to_f32(w[i] >> 16);
+      v[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xffffu));
+      v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
     }
   } else {
     const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + off);
@@ -310,7 +310,7 @@ void run_q6k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 // growing drains the stream first).
 void* gemv_scratch(hipStream_t s, size_t bytes);
 // A8 on the matrix cores (f32 activations)
-void run_a8_mma(const GemvArgs& a, int nrows, int epi, hipStream_t s);
+void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s);
 
 }  // namespace gemv
 }  // namespace pgd

@@ -11,11 +11,12 @@
 // and every batch row goes through the same instruction sequence whatever the
 // batch size, so a batched call is bitwise equal to single-row calls.
 //
-// Activations are converted once per call (a8_xprep_kernel) into the MFMA
-// operand order; weights are stored tiled (32 rows x 64 codes per 2 KiB
-// block), so a wave's 128-bit loads read 512 B runs. A workgroup of KS waves
-// shares one 32-row tile and splits the groups between its waves; each wave
-// double-buffers its loads; partial sums meet in LDS in a fixed order.
+// Activations are converted once (a8_xprep_kernel, or fused into the RMSNorm
+// that produces them, a8_norm_prep_kernel) into the MFMA operand order;
+// weights are stored tiled (32 rows x 64 codes per 2 KiB block), so a wave's
+// 128-bit loads read 512 B runs. A workgroup of KS waves shares one 32-row
+// tile and splits the groups between its waves; each wave keeps PF groups of
+// loads in flight; partial sums meet in LDS in a fixed order.
 //
 // Counterpart of affine_gemv / affine_gemm4 / gemv2_silu / gemv_res
 // (pagoda-hf/src/qwen3_gemv.rs:54-306, 414-567).
@@ -51,56 +52,140 @@ __device__ inline h8 codes8(uint32_t w0, uint32_t w1) {
 }
 
 // ---- activation prep --------------------------------------------------------
-// For batch tile bt (rows 16bt..16bt+15) and group g, item = g * nbt + bt:
+// Rows are cut into chunks of 32 (two 16-row batch tiles). For chunk c,
+// group g, batch tile bt, item = (c * G + g) * 2 + bt:
 //   XA[item][lane] = 64 B: xh step 0 | xh step 1 | xl step 0 | xl step 1,
-//     8 halves each, batch row 16bt + lane % 16, k = 64g + 16(lane/16) + 8 step + e
+//     8 halves each, batch row 32c + 16bt + lane % 16, k = 64g + 16(lane/16) + 8 step + e
 //   CA[item] = 32 floats: 128 * XSP for the 16 rows, then XS for the 16 rows
-// Rows >= nb are zero.
-__global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__ x, int ldx, int nb, int G, int nbt,
-                                                       uint4* __restrict__ XA, float* __restrict__ CA) {
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (item >= G * nbt) return;
-  const int g = item / nbt, bt = item % nbt;
-  const int row = 16 * bt + (lane & 15), q = lane >> 4;
-  float xs = 0.0f, xsp = 0.0f;
+// Rows past the end are never written: their MFMA rows only feed discarded
+// outputs.
+__device__ inline void prep16(const float* v, uint4* o, float& xs, float& xsp) {
   uint32_t hw[8], lw[8];
-  if (row < nb) {
+  xs = 0.0f;
+  xsp = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const _Float16 h0 = (_Float16)v[2 * p], h1 = (_Float16)v[2 * p + 1];
+    const _Float16 l0 = (_Float16)(v[2 * p] - (float)h0), l1 = (_Float16)(v[2 * p + 1] - (float)h1);
+    hw[p] = __builtin_bit_cast(uint32_t, (h2){h0, h1});
+    lw[p] = __builtin_bit_cast(uint32_t, (h2){l0, l1});
+    xs += v[2 * p] + v[2 * p + 1];
+    xsp += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
+  }
+  o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  o[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+  o[2] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  o[3] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+}
+
+__global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__ x, int ldx, int rows, int G,
+                                                       uint4* __restrict__ XA, float* __restrict__ CA) {
+  const size_t item = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int bt = (int)(item & 1);
+  const size_t cg = item >> 1;
+  const int g = (int)(cg % G), c = (int)(cg / G);
+  if (32 * c >= rows) return;
+  const int row = 32 * c + 16 * bt + (lane & 15), q = lane >> 4;
+  float v[16];
+  if (row < rows) {
     const float4* xp = reinterpret_cast<const float4*>(x + (size_t)row * ldx + (g << 6) + 16 * q);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float4 f = xp[i];
-      const float v[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const _Float16 h0 = (_Float16)v[2 * p], h1 = (_Float16)v[2 * p + 1];
-        const _Float16 l0 = (_Float16)(v[2 * p] - (float)h0), l1 = (_Float16)(v[2 * p + 1] - (float)h1);
-        hw[2 * i + p] = __builtin_bit_cast(uint32_t, (h2){h0, h1});
-        lw[2 * i + p] = __builtin_bit_cast(uint32_t, (h2){l0, l1});
-        xs += v[2 * p] + v[2 * p + 1];
-        xsp += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
-      }
+      v[4 * i] = f.x;
+      v[4 * i + 1] = f.y;
+      v[4 * i + 2] = f.z;
+      v[4 * i + 3] = f.w;
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      hw[i] = 0u;
-      lw[i] = 0u;
-    }
+    for (int i = 0; i < 16; ++i) v[i] = 0.0f;
   }
+  float xs, xsp;
+  prep16(v, XA + (item * 64 + lane) * 4, xs, xsp);
   // the four lanes of a row (q = 0..3) hold its four 16-wide k slices
   xs += __shfl_xor(xs, 16, 64);
   xs += __shfl_xor(xs, 32, 64);
   xsp += __shfl_xor(xsp, 16, 64);
   xsp += __shfl_xor(xsp, 32, 64);
-  uint4* o = XA + ((size_t)item * 64 + lane) * 4;
-  o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-  o[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-  o[2] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  o[3] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
   if (q == 0) {
-    CA[(size_t)item * 32 + (lane & 15)] = 128.0f * xsp;
-    CA[(size_t)item * 32 + 16 + (lane & 15)] = xs;
+    CA[item * 32 + (lane & 15)] = 128.0f * xsp;
+    CA[item * 32 + 16 + (lane & 15)] = xs;
+  }
+}
+
+// Fused RMSNorm (rms_zero, pagoda-hf/src/qwen3_5.rs:1736-1745) + activation
+// prep: one workgroup per output row; thread t owns 16-wide slices t, t+256,
+// ... (slice u = 4g + q), kept in registers between the two passes.
+constexpr int kNormMaxSlices = 8;  // n <= 256 * 16 * 8
+__global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restrict__ x, int ldx,
+                                                           const int* __restrict__ rows_idx, int rows, int n,
+                                                           const float* __restrict__ w, float eps, float* y, int ldy,
+                                                           uint4* __restrict__ XA, float* __restrict__ CA) {
+  __shared__ float red[4];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const int src = rows_idx ? rows_idx[r] : r;
+  const float* xr = x + (size_t)src * ldx;
+  const int slices = n >> 4, G = n >> 6;
+  float v[kNormMaxSlices][16];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormMaxSlices; ++i) {
+    const int u = tid + 256 * i;
+    if (u < slices) {
+      const float4* p = reinterpret_cast<const float4*>(xr + 16 * u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float4 f = p[e];
+        v[i][4 * e] = f.x;
+        v[i][4 * e + 1] = f.y;
+        v[i][4 * e + 2] = f.z;
+        v[i][4 * e + 3] = f.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ss += v[i][e] * v[i][e];
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)n + eps);
+  const int c = r >> 5, bt = (r >> 4) & 1, j = r & 15;
+#pragma unroll
+  for (int i = 0; i < kNormMaxSlices; ++i) {
+    const int u = tid + 256 * i;
+    const bool live = u < slices;  // uniform per group of four lanes (slices % 4 == 0)
+    float xs = 0.0f, xsp = 0.0f;
+    if (live) {
+      const float4* wp = reinterpret_cast<const float4*>(w + 16 * u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float4 f = wp[e];
+        v[i][4 * e] = v[i][4 * e] * inv * f.x;
+        v[i][4 * e + 1] = v[i][4 * e + 1] * inv * f.y;
+        v[i][4 * e + 2] = v[i][4 * e + 2] * inv * f.z;
+        v[i][4 * e + 3] = v[i][4 * e + 3] * inv * f.w;
+      }
+      if (y) {
+        float4* yp = reinterpret_cast<float4*>(y + (size_t)r * ldy + 16 * u);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yp[e] = make_float4(v[i][4 * e], v[i][4 * e + 1], v[i][4 * e + 2], v[i][4 * e + 3]);
+      }
+      const int g = u >> 2, q = u & 3;
+      const size_t item = ((size_t)c * G + g) * 2 + bt;
+      prep16(v[i], XA + (item * 64 + q * 16 + j) * 4, xs, xsp);
+    }
+    // group sums over the four slices of a group (adjacent lanes)
+    xs += __shfl_xor(xs, 1, 64);
+    xs += __shfl_xor(xs, 2, 64);
+    xsp += __shfl_xor(xsp, 1, 64);
+    xsp += __shfl_xor(xsp, 2, 64);
+    if (live && (u & 3) == 0) {
+      const size_t item = ((size_t)c * G + (u >> 2)) * 2 + bt;
+      CA[item * 32 + j] = 128.0f * xsp;
+      CA[item * 32 + 16 + j] = xs;
+    }
   }
 }
 
@@ -114,7 +199,7 @@ struct GroupRaw {
 };
 
 // NS = 16-row weight subtiles per wave (2 = one 32-row tile; 4 = gate + up)
-template <int NBT, int KS, int EPI>
+template <int NBT, int KS, int PF, int EPI>
 __global__ __launch_bounds__(64 * KS) void a8_mma_kernel(GemvArgs a, const uint4* __restrict__ XA,
                                                          const float* __restrict__ CA, int nb) {
   constexpr bool DUAL = EPI == EPI_SWIGLU;
@@ -150,7 +235,7 @@ __global__ __launch_bounds__(64 * KS) void a8_mma_kernel(GemvArgs a, const uint4
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) {
       if (bt == 0 || bt1) {
-        const size_t item = (size_t)g * NBT + bt;
+        const size_t item = (size_t)g * 2 + bt;
         const uint4* xp = XA + (item * 64 + lane) * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) R.xa[bt][i] = xp[i];
@@ -187,19 +272,22 @@ __global__ __launch_bounds__(64 * KS) void a8_mma_kernel(GemvArgs a, const uint4
     }
   };
 
-  // groups of this wave: a contiguous range, double-buffered
+  // groups of this wave: a contiguous range, PF groups in flight
   const int per = (G + KS - 1) / KS;
   const int g0 = wave * per, g1 = min(G, g0 + per);
-  GroupRaw<NS, NBT> bufA, bufB;
-  if (g0 < g1) load(g0, bufA);
-  int g = g0;
-  for (; g + 1 < g1; g += 2) {
-    load(g + 1, bufB);
-    compute(bufA);
-    if (g + 2 < g1) load(g + 2, bufA);
-    compute(bufB);
+  GroupRaw<NS, NBT> buf[PF];
+#pragma unroll
+  for (int u = 0; u < PF; ++u)
+    if (g0 + u < g1) load(g0 + u, buf[u]);
+  for (int g = g0; g < g1; g += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      if (g + u < g1) {
+        compute(buf[u]);
+        if (g + u + PF < g1) load(g + u + PF, buf[u]);
+      }
+    }
   }
-  if (g < g1) compute(bufA);
 
   // ---- split-K reduction (fixed order: wave 0 + 1 + ... + KS-1) ----
   if constexpr (KS > 1) {
@@ -236,15 +324,20 @@ __global__ __launch_bounds__(64 * KS) void a8_mma_kernel(GemvArgs a, const uint4
   }
 }
 
+constexpr int kPF = 2;  // groups of loads in flight per wave
+
 template <int NBT, int KS, int EPI>
 void launch_kernel(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
+  constexpr int PF = kPF;
   const int tiles = (a.n_out + 31) / 32;
-  hipLaunchKernelGGL((a8_mma_kernel<NBT, KS, EPI>), dim3(tiles), dim3(64 * KS), 0, s, a, XA, CA, nb);
+  hipLaunchKernelGGL((a8_mma_kernel<NBT, KS, PF, EPI>), dim3(tiles), dim3(64 * KS), 0, s, a, XA, CA, nb);
 }
 
 template <int NBT, int EPI>
 void launch_ks(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
-  // enough waves to fill the GPU (~8 per CU), each wave keeping >= 4 groups
+  // enough waves to fill the GPU (~8 per CU), each wave keeping its prefetch
+  // ring busy. The split depends on the matrix shape only, never on the batch,
+  // so every batch size sums a row's groups in the same order.
   const int tiles = (a.n_out + 31) / 32;
   const int G = a.n_in / 64;
   int ks = 1;
@@ -258,22 +351,19 @@ void launch_ks(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipS
 }
 
 template <int EPI>
-void launch_mma(GemvArgs a, int nrows, hipStream_t s) {
+void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
+  PGD_CHECK(act.K == a.n_in, kErrShape, "prepared activations have the wrong width");
   const int G = a.n_in / 64;
-  // activation operands for up to 32 rows: 2 tiles x (64 lanes x 64 B + 32 floats) per group
-  uint8_t* scr = (uint8_t*)gemv_scratch(s, (size_t)G * 2 * (64 * 64 + 32 * 4));
-  uint4* XA = reinterpret_cast<uint4*>(scr);
-  float* CA = reinterpret_cast<float*>(scr + (size_t)G * 2 * 64 * 64);
-  while (nrows > 0) {
-    const int nb = nrows < 32 ? nrows : 32;
-    const int nbt = nb > 16 ? 2 : 1;
-    hipLaunchKernelGGL(a8_xprep_kernel, dim3((G * nbt + 3) / 4), dim3(256), 0, s, reinterpret_cast<const float*>(a.x),
-                       a.ldx, nb, G, nbt, XA, CA);
-    if (nbt == 2) launch_ks<2, EPI>(a, XA, CA, nb, s);
-    else launch_ks<1, EPI>(a, XA, CA, nb, s);
+  const uint4* XA = reinterpret_cast<const uint4*>(act.XA);
+  int rows = act.rows;
+  for (int c = 0; rows > 0; ++c) {
+    const int nb = rows < 32 ? rows : 32;
+    const uint4* xa = XA + (size_t)c * G * 2 * 64 * 4;
+    const float* ca = act.CA + (size_t)c * G * 2 * 32;
+    if (nb > 16) launch_ks<2, EPI>(a, xa, ca, nb, s);
+    else launch_ks<1, EPI>(a, xa, ca, nb, s);
     PGD_HIP(hipGetLastError());
-    nrows -= nb;
-    a.x = reinterpret_cast<const float*>(a.x) + (size_t)nb * a.ldx;
+    rows -= nb;
     a.y += (size_t)nb * a.ldy;
     if (a.res) a.res += (size_t)nb * a.ldres;
   }
@@ -281,11 +371,52 @@ void launch_mma(GemvArgs a, int nrows, hipStream_t s) {
 
 }  // namespace
 
-void run_a8_mma(const GemvArgs& a, int nrows, int epi, hipStream_t s) {
-  if (epi == EPI_SWIGLU) launch_mma<EPI_SWIGLU>(a, nrows, s);
-  else if (epi == EPI_RES) launch_mma<EPI_RES>(a, nrows, s);
-  else launch_mma<EPI_STORE>(a, nrows, s);
+void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s) {
+  if (epi == EPI_SWIGLU) launch_prepped<EPI_SWIGLU>(a, act, s);
+  else if (epi == EPI_RES) launch_prepped<EPI_RES>(a, act, s);
+  else launch_prepped<EPI_STORE>(a, act, s);
 }
+
+}  // namespace gemv
+
+size_t a8_act_bytes(int rows, int K) {
+  const size_t chunks = ((size_t)rows + 31) / 32, G = (size_t)K / 64;
+  return chunks * G * 2 * (64 * 64 + 32 * 4);
+}
+
+A8Act a8_act_view(void* buf, int rows, int K) {
+  const size_t chunks = ((size_t)rows + 31) / 32, G = (size_t)K / 64;
+  A8Act a;
+  a.XA = buf;
+  a.CA = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(buf) + chunks * G * 2 * 64 * 64);
+  a.rows = rows;
+  a.K = K;
+  return a;
+}
+
+A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream_t s) {
+  PGD_CHECK(K % 64 == 0 && ldx % 4 == 0, kErrShape, "A8 activation width must be a multiple of 64");
+  A8Act a = a8_act_view(buf, rows, K);
+  if (rows <= 0) return a;
+  const size_t items = ((size_t)rows + 31) / 32 * (K / 64) * 2;
+  hipLaunchKernelGGL(gemv::a8_xprep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, x, ldx, rows, K / 64,
+                     reinterpret_cast<uint4*>(buf), const_cast<float*>(a.CA));
+  PGD_HIP(hipGetLastError());
+  return a;
+}
+
+A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps, float* y,
+                   int ldy, void* buf, hipStream_t s) {
+  PGD_CHECK(n % 64 == 0 && n <= 256 * 16 * gemv::kNormMaxSlices && ldx % 4 == 0, kErrShape, "norm prep width");
+  A8Act a = a8_act_view(buf, rows, n);
+  if (rows <= 0) return a;
+  hipLaunchKernelGGL(gemv::a8_norm_prep_kernel, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx, rows, n, w, eps, y,
+                     ldy, reinterpret_cast<uint4*>(buf), const_cast<float*>(a.CA));
+  PGD_HIP(hipGetLastError());
+  return a;
+}
+
+namespace gemv {
 
 }  // namespace gemv
 }  // namespace pgd

@@ -84,7 +84,8 @@ Model::~Model() {
     qmat_free(embed);
     if (!tied) qmat_free(head);
     for (auto& L : layers) {
-      for (QMat* q : {&L.gate, &L.up, &L.down, &L.qkv, &L.z, &L.a, &L.b, &L.out, &L.q, &L.k, &L.v, &L.o}) qmat_free(*q);
+      for (QMat* q : {&L.gate, &L.up, &L.down, &L.proj, &L.qkv, &L.z, &L.a, &L.b, &L.out, &L.q, &L.k, &L.v, &L.o})
+        qmat_free(*q);
     }
     for (void* p : allocs) (void)hipFree(p);
     if (meta_host) (void)hipHostFree(meta_host);
@@ -166,6 +167,8 @@ static void build_synth(Model& m, uint64_t seed) {
     m.value_dim = c.v_heads * c.v_dim;
     m.conv_dim = 2 * m.key_dim + m.value_dim;
     m.q_out = c.heads * c.head_dim * 2;
+    m.proj_lin = m.conv_dim + m.value_dim + 2 * c.v_heads;
+    m.proj_full = m.q_out + 2 * m.kv_width;
     qmat_alloc(m.embed, FMT_A8, c.vocab, H, s);
     qmat_synth(m.embed, seed, tkey(-1, K_EMBED), 0.02f, s);
     qmat_alloc(m.head, FMT_A8, c.vocab, H, s);
@@ -195,10 +198,12 @@ static void build_synth(Model& m, uint64_t seed) {
       mat(L.down, FMT_A8, H, c.intermediate, i, K_DOWN);
       if (!L.full) {
         L.lin_index = m.n_lin++;
-        mat(L.qkv, FMT_A8, m.conv_dim, H, i, K_QKV);
-        mat(L.z, FMT_A8, m.value_dim, H, i, K_Z);
-        mat(L.a, FMT_A8, c.v_heads, H, i, K_A);
-        mat(L.b, FMT_A8, c.v_heads, H, i, K_B);
+        // [qkv | z | b | a] stacked; each range keeps its own tensor key
+        qmat_alloc(L.proj, FMT_A8, m.proj_lin, H, s);
+        qmat_synth_rows(L.proj, 0, m.conv_dim, seed, tkey(i, K_QKV), 0.02f, s);
+        qmat_synth_rows(L.proj, m.conv_dim, m.value_dim, seed, tkey(i, K_Z), 0.02f, s);
+        qmat_synth_rows(L.proj, m.conv_dim + m.value_dim, c.v_heads, seed, tkey(i, K_B), 0.02f, s);
+        qmat_synth_rows(L.proj, m.conv_dim + m.value_dim + c.v_heads, c.v_heads, seed, tkey(i, K_A), 0.02f, s);
         mat(L.out, FMT_A8, H, m.value_dim, i, K_OUT);
         L.conv = dev_floats(m, (size_t)m.conv_dim * c.conv_kernel);
         synth_normal_f32(L.conv, (size_t)m.conv_dim * c.conv_kernel, seed, tkey(i, K_CONV), 0.2f, s);
@@ -209,9 +214,10 @@ static void build_synth(Model& m, uint64_t seed) {
         L.gnorm = dev_const(m, c.v_dim, 1.0f, s);
       } else {
         L.full_index = m.n_full++;
-        mat(L.q, FMT_A8, m.q_out, H, i, K_Q);
-        mat(L.k, FMT_A8, m.kv_width, H, i, K_K);
-        mat(L.v, FMT_A8, m.kv_width, H, i, K_V);
+        qmat_alloc(L.proj, FMT_A8, m.proj_full, H, s);
+        qmat_synth_rows(L.proj, 0, m.q_out, seed, tkey(i, K_Q), 0.02f, s);
+        qmat_synth_rows(L.proj, m.q_out, m.kv_width, seed, tkey(i, K_K), 0.02f, s);
+        qmat_synth_rows(L.proj, m.q_out + m.kv_width, m.kv_width, seed, tkey(i, K_V), 0.02f, s);
         mat(L.o, FMT_A8, H, c.heads * c.head_dim, i, K_O);
         L.q_norm = dev_const(m, c.head_dim, 1.0f, s);
         L.k_norm = dev_const(m, c.head_dim, 1.0f, s);
@@ -257,19 +263,26 @@ namespace {
 
 struct Ws {
   float *x, *xn, *A, *B, *C0, *C1, *D, *E, *F, *G, *logits;
+  void* act;  // prepared A8 activation operands
   size_t lda, ldb, ldd, lde;
 };
 
 Ws carve_ws(Model& m, int rows, int lrows) {
   const pgd_model_config& c = m.cfg;
   size_t H = c.hidden;
-  size_t lda = std::max<size_t>(m.conv_dim, m.q_out);
+  size_t lda = std::max<size_t>(std::max<size_t>(m.conv_dim, m.q_out), std::max(m.proj_lin, m.proj_full));
   size_t ldb = std::max<size_t>(m.value_dim, m.kv_width);
   size_t ldc = std::max<size_t>(align_up(std::max(c.v_heads, 1), 8), m.kv_width);
   size_t ldd = std::max<size_t>(m.conv_dim, (size_t)c.heads * c.head_dim);
   size_t lde = std::max<size_t>(m.value_dim, (size_t)c.heads * c.head_dim);
+  size_t act_floats = 0;
+  if (c.arch == PGD_ARCH_QWEN35) {
+    int kmax = std::max(std::max(c.hidden, c.intermediate), std::max(m.value_dim, c.heads * c.head_dim));
+    act_floats = (a8_act_bytes(rows, kmax) + 3) / 4;
+  }
   size_t sizes[] = {rows * H, rows * H, rows * lda, rows * ldb, rows * ldc, rows * ldc, rows * ldd, rows * lde,
-                    rows * (size_t)c.heads * c.head_dim, rows * (size_t)c.intermediate, (size_t)lrows * c.vocab};
+                    rows * (size_t)c.heads * c.head_dim, rows * (size_t)c.intermediate, (size_t)lrows * c.vocab,
+                    act_floats};
   size_t total = 0;
   for (size_t v : sizes) total += align_up(v, 64);
   if (m.ws.bytes < total * 4) {
@@ -277,13 +290,13 @@ Ws carve_ws(Model& m, int rows, int lrows) {
     m.ws = DevBuf(total * 4);
   }
   float* p = m.ws.as<float>();
-  float* ptrs[11];
-  for (int i = 0; i < 11; ++i) {
+  float* ptrs[12];
+  for (int i = 0; i < 12; ++i) {
     ptrs[i] = p;
     p += align_up(sizes[i], 64);
   }
   Ws w{ptrs[0], ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], ptrs[6], ptrs[7], ptrs[8], ptrs[9], ptrs[10],
-       lda, ldb, ldd, lde};
+       (void*)ptrs[11], lda, ldb, ldd, lde};
   return w;
 }
 
@@ -413,15 +426,38 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   const float eps = c.arch == PGD_ARCH_QWEN35 ? 1e-6f : c.eps;
   qmat_embed(m.embed, d_tok, rows, w.x, H, st);
   const size_t per_lin = m.conv_floats + m.state_floats;
+  const bool hybrid = c.arch == PGD_ARCH_QWEN35;
   for (auto& L : m.layers) {
-    rmsnorm_rows(w.x, H, nullptr, rows, H, L.in_norm, eps, norm_mode, w.xn, H, st);
+    // ---- projections of the normed input ----
+    const float *q_raw = nullptr, *k_raw = nullptr, *v_raw = nullptr;
+    int ld_q = 0, ld_kv = 0;
+    if (hybrid) {
+      // one fused norm + operand prep, one launch for all projections
+      A8Act act = a8_norm_prep(w.x, H, nullptr, rows, H, L.in_norm, eps, nullptr, 0, w.act, st);
+      qmat_gemv_a8(L.proj, act, w.A, (int)w.lda, nullptr, 0, st);
+      if (L.full) {
+        q_raw = w.A;
+        k_raw = w.A + m.q_out;
+        v_raw = w.A + m.q_out + m.kv_width;
+        ld_q = ld_kv = (int)w.lda;
+      }
+    } else {
+      rmsnorm_rows(w.x, H, nullptr, rows, H, L.in_norm, eps, norm_mode, w.xn, H, st);
+      qmat_gemv(L.q, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
+      qmat_gemv(L.k, w.xn, 0, H, rows, w.B, (int)w.ldb, nullptr, 0, st);
+      qmat_gemv(L.v, w.xn, 0, H, rows, w.C0, (int)w.ldb, nullptr, 0, st);
+      q_raw = w.A;
+      k_raw = w.B;
+      v_raw = w.C0;
+      ld_q = (int)w.lda;
+      ld_kv = (int)w.ldb;
+    }
     if (!L.full) {
-      qmat_gemv(L.qkv, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
-      qmat_gemv(L.z, w.xn, 0, H, rows, w.B, (int)w.ldb, nullptr, 0, st);
-      qmat_gemv(L.b, w.xn, 0, H, rows, w.C0, c.v_heads, nullptr, 0, st);
-      qmat_gemv(L.a, w.xn, 0, H, rows, w.C1, c.v_heads, nullptr, 0, st);
-      conv_step(w.A, (int)w.lda, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb,
-                (size_t)L.lin_index * per_lin, sm, nseq, st);
+      // stacked rows: [qkv (conv_dim) | z (value_dim) | b (v_heads) | a (v_heads)]
+      const float* P = w.A;
+      const int ldp = (int)w.lda;
+      conv_step(P, ldp, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb, (size_t)L.lin_index * per_lin, sm,
+                nseq, st);
       GdnParams gp{};
       gp.k_heads = c.k_heads;
       gp.v_heads = c.v_heads;
@@ -429,11 +465,11 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       gp.v_dim = c.v_dim;
       gp.conv_out = w.D;
       gp.ld_conv = (int)w.ldd;
-      gp.a = w.C1;
-      gp.b = w.C0;
-      gp.ld_ab = c.v_heads;
-      gp.z = w.B;
-      gp.ld_z = (int)w.ldb;
+      gp.z = P + m.conv_dim;
+      gp.ld_z = ldp;
+      gp.b = P + m.conv_dim + m.value_dim;
+      gp.a = P + m.conv_dim + m.value_dim + c.v_heads;
+      gp.ld_ab = ldp;
       gp.a_log = L.a_log;
       gp.dt_bias = L.dt_bias;
       gp.norm = L.gnorm;
@@ -442,19 +478,17 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       gp.state_base = d_sb;
       gp.state_off = (size_t)L.lin_index * per_lin + m.conv_floats;
       gdn_step(gp, sm, nseq, st);
-      qmat_gemv(L.out, w.E, 0, (int)w.lde, rows, w.x, H, w.x, H, st);
+      A8Act act = a8_act_prep(w.E, (int)w.lde, rows, m.value_dim, w.act, st);
+      qmat_gemv_a8(L.out, act, w.x, H, w.x, H, st);
     } else {
-      qmat_gemv(L.q, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
-      qmat_gemv(L.k, w.xn, 0, H, rows, w.B, (int)w.ldb, nullptr, 0, st);
-      qmat_gemv(L.v, w.xn, 0, H, rows, w.C0, (int)w.ldb, nullptr, 0, st);
       AttnLayout al{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.kv_block, L.k_pool, L.v_pool};
       QkvPrep qp{};
-      qp.variant = c.arch == PGD_ARCH_QWEN35 ? 0 : 1;
-      qp.q_raw = w.A;
-      qp.ld_q = (int)w.lda;
-      qp.k_raw = w.B;
-      qp.v_raw = w.C0;
-      qp.ld_kv = (int)w.ldb;
+      qp.variant = hybrid ? 0 : 1;
+      qp.q_raw = q_raw;
+      qp.ld_q = ld_q;
+      qp.k_raw = k_raw;
+      qp.v_raw = v_raw;
+      qp.ld_kv = ld_kv;
       qp.q_norm = L.q_norm;
       qp.k_norm = L.k_norm;
       qp.q_bias = L.qb;
@@ -463,16 +497,34 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       qp.q = w.D;
       qp.gate = w.F;
       qkv_prep(qp, al, rm, rows, st);
-      attn_decode(w.D, qp.variant == 0 ? w.F : nullptr, w.E, al, rm, rows, st);
-      qmat_gemv(L.o, w.E, 0, c.heads * c.head_dim, rows, w.x, H, w.x, H, st);
+      attn_decode(w.D, hybrid ? w.F : nullptr, w.E, al, rm, rows, st);
+      if (hybrid) {
+        A8Act act = a8_act_prep(w.E, c.heads * c.head_dim, rows, c.heads * c.head_dim, w.act, st);
+        qmat_gemv_a8(L.o, act, w.x, H, w.x, H, st);
+      } else {
+        qmat_gemv(L.o, w.E, 0, c.heads * c.head_dim, rows, w.x, H, w.x, H, st);
+      }
     }
-    rmsnorm_rows(w.x, H, nullptr, rows, H, L.post_norm, eps, norm_mode, w.xn, H, st);
-    qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
-    qmat_gemv(L.down, w.G, 0, c.intermediate, rows, w.x, H, w.x, H, st);
+    // ---- SwiGLU MLP ----
+    if (hybrid) {
+      A8Act act = a8_norm_prep(w.x, H, nullptr, rows, H, L.post_norm, eps, nullptr, 0, w.act, st);
+      qmat_gemv_a8_swiglu(L.gate, L.up, act, w.G, c.intermediate, st);
+      A8Act act2 = a8_act_prep(w.G, c.intermediate, rows, c.intermediate, w.act, st);
+      qmat_gemv_a8(L.down, act2, w.x, H, w.x, H, st);
+    } else {
+      rmsnorm_rows(w.x, H, nullptr, rows, H, L.post_norm, eps, norm_mode, w.xn, H, st);
+      qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
+      qmat_gemv(L.down, w.G, 0, c.intermediate, rows, w.x, H, w.x, H, st);
+    }
   }
   // ---- head ----
-  rmsnorm_rows(w.x, H, d_lr, lrows, H, m.final_norm, eps, norm_mode, w.xn, H, st);
-  qmat_gemv(m.head, w.xn, 0, H, lrows, w.logits, c.vocab, nullptr, 0, st);
+  if (hybrid) {
+    A8Act act = a8_norm_prep(w.x, H, d_lr, lrows, H, m.final_norm, eps, nullptr, 0, w.act, st);
+    qmat_gemv_a8(m.head, act, w.logits, c.vocab, nullptr, 0, st);
+  } else {
+    rmsnorm_rows(w.x, H, d_lr, lrows, H, m.final_norm, eps, norm_mode, w.xn, H, st);
+    qmat_gemv(m.head, w.xn, 0, H, lrows, w.logits, c.vocab, nullptr, 0, st);
+  }
   size_t out_bytes = (size_t)lrows * 12;
   if (m.out_dev.bytes < out_bytes) m.out_dev = DevBuf(out_bytes * 2);
   if (m.out_host_cap < out_bytes) {
@@ -535,7 +587,8 @@ int pgd_model_info(const pgd_model* pm, size_t* weight_bytes, double* algo, int*
     size_t wb = m.embed.bytes + (m.tied ? 0 : m.head.bytes);
     double ab = qmat_algo_bytes(m.head);  // one embedding row is negligible
     for (auto& L : m.layers)
-      for (const QMat* q : {&L.gate, &L.up, &L.down, &L.qkv, &L.z, &L.a, &L.b, &L.out, &L.q, &L.k, &L.v, &L.o}) {
+      for (const QMat* q :
+           {&L.gate, &L.up, &L.down, &L.proj, &L.qkv, &L.z, &L.a, &L.b, &L.out, &L.q, &L.k, &L.v, &L.o}) {
         wb += q->bytes;
         ab += q->base ? qmat_algo_bytes(*q) : 0.0;
       }

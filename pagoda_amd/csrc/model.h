@@ -19,6 +19,9 @@ struct Layer {
   float* in_norm = nullptr;
   float* post_norm = nullptr;
   QMat gate, up, down;
+  // hybrid model: the projections that read the normed input, stacked into
+  // one matrix (rows [qkv | z | b | a] or [q | k | v]), one launch
+  QMat proj;
   // gated-delta (linear attention) layer
   QMat qkv, z, a, b, out;
   float* conv = nullptr;
@@ -44,6 +47,7 @@ struct Model {
   pgd_dev* dev = nullptr;
   pgd_model_config cfg{};
   int conv_dim = 0, key_dim = 0, value_dim = 0, q_out = 0, kv_width = 0;
+  int proj_lin = 0, proj_full = 0;  // stacked projection widths (hybrid model)
   QMat embed, head;
   bool tied = false;
   float* final_norm = nullptr;

@@ -76,6 +76,26 @@ void qmat_gemv(const QMat& m, const void* x, int x_f16, int ldx, int nrows, floa
 void qmat_gemv_swiglu(const QMat& gate, const QMat& up, const float* x, int ldx, int nrows, float* mid,
                       int ldm, hipStream_t s);
 
+// ---- A8 activation operands ------------------------------------------------
+// The A8 GEMV consumes activations converted once into matrix-core operands
+// (f16 hi/lo pairs + per-group sums), in chunks of 32 rows. One prepared
+// buffer can feed every A8 matrix with the same input width.
+struct A8Act {
+  const void* XA = nullptr;
+  const float* CA = nullptr;
+  int rows = 0, K = 0;
+};
+size_t a8_act_bytes(int rows, int K);
+A8Act a8_act_view(void* buf, int rows, int K);
+// from f32 rows x [rows, ldx]
+A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream_t s);
+// fused RMSNorm (x * rsqrt(mean x^2 + eps) * w) + prep; y (nullable) also
+// receives the normalized rows; rows_idx (nullable) selects source rows
+A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps, float* y,
+                   int ldy, void* buf, hipStream_t s);
+void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const float* res, int ldres, hipStream_t s);
+void qmat_gemv_a8_swiglu(const QMat& gate, const QMat& up, const A8Act& act, float* mid, int ldm, hipStream_t s);
+
 // embedding rows: out[r, :] = dequant(W[ids[r], :]) (ids on device)
 void qmat_embed(const QMat& m, const uint32_t* ids, int nrows, float* out, int ldo, hipStream_t s);
 
@@ -83,6 +103,9 @@ void qmat_embed(const QMat& m, const uint32_t* ids, int nrows, float* out, int l
 // N(0, std) weights (counter-based generator, reproduced bit for bit by the
 // CPU checker).
 void qmat_synth(QMat& m, uint64_t seed, uint64_t key, float std, hipStream_t s);
+// rows [row0, row0 + rows) of an A8 matrix from their own key (a stacked
+// matrix whose row ranges are separate tensors)
+void qmat_synth_rows(QMat& m, int row0, int rows, uint64_t seed, uint64_t key, float std, hipStream_t s);
 
 // seeded f32 vectors
 void synth_normal_f32(float* out, size_t n, uint64_t seed, uint64_t key, float scale, hipStream_t s);

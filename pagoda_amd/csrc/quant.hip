@@ -17,10 +17,13 @@ namespace {
 
 void run_fmt(const QMat& m, const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s) {
   switch (m.fmt) {
-    case FMT_A8:
+    case FMT_A8: {
       PGD_CHECK(!x_f16, kErrArg, "A8 matrices take f32 activations");
-      run_a8_mma(a, nrows, epi, s);
+      void* buf = gemv_scratch(s, a8_act_bytes(nrows, a.n_in));
+      A8Act act = a8_act_prep(reinterpret_cast<const float*>(a.x), a.ldx, nrows, a.n_in, buf, s);
+      run_a8_mma(a, act, epi, s);
       break;
+    }
     case FMT_Q4K: run_q4k(a, nrows, x_f16, epi, s); break;
     case FMT_Q6K: run_q6k(a, nrows, x_f16, epi, s); break;
     default: throw Error{kErrFormat, "unknown matrix format"};
@@ -171,13 +174,15 @@ __device__ inline float synth_uniform(uint64_t stream, uint64_t idx) {
 __device__ inline float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 // MLX affine quantizer, one thread per (row, group of 64).
-__global__ void synth_a8_kernel(uint8_t* codes, uint32_t* sb, int n_out, int n_in, uint64_t stream, float std) {
+__global__ void synth_a8_kernel(uint8_t* codes, uint32_t* sb, int row0, int nrows, int n_in, uint64_t stream,
+                                float std) {
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   int groups = n_in >> 6;
-  if (t >= (size_t)n_out * groups) return;
-  size_t r = t / groups;
+  if (t >= (size_t)nrows * groups) return;
+  size_t rl = t / groups;  // row within the tensor (its own element numbering)
+  size_t r = rl + row0;    // row within the stored matrix
   int g = (int)(t % groups);
-  size_t base = r * n_in + (size_t)g * 64;
+  size_t base = rl * n_in + (size_t)g * 64;
   float w[64];
   float mx, mn;
 #pragma unroll
@@ -517,12 +522,34 @@ void qmat_gemv_swiglu(const QMat& gate, const QMat& up, const float* x, int ldx,
   run_fmt(gate, a, nrows, 0, EPI_SWIGLU, s);
 }
 
+void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const float* res, int ldres, hipStream_t s) {
+  PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "prepared activations feed A8 matrices");
+  if (act.rows <= 0) return;
+  GemvArgs a = make_args(m);
+  a.y = y;
+  a.ldy = ldy;
+  a.res = res;
+  a.ldres = ldres;
+  run_a8_mma(a, act, res ? EPI_RES : EPI_STORE, s);
+}
+
+void qmat_gemv_a8_swiglu(const QMat& gate, const QMat& up, const A8Act& act, float* mid, int ldm, hipStream_t s) {
+  PGD_CHECK(gate.fmt == FMT_A8 && up.fmt == FMT_A8 && gate.n_out == up.n_out && gate.n_in == up.n_in, kErrShape,
+            "swiglu gate/up shapes differ");
+  if (act.rows <= 0) return;
+  GemvArgs a = make_args(gate);
+  a.u0 = up.p0;
+  a.u1 = up.p1;
+  a.y = mid;
+  a.ldy = ldm;
+  run_a8_mma(a, act, EPI_SWIGLU, s);
+}
+
 void qmat_synth(QMat& m, uint64_t seed, uint64_t key, float std, hipStream_t s) {
   uint64_t stream = synth_stream(seed, key);
   if (m.fmt == FMT_A8) {
-    size_t n = (size_t)m.n_out * (m.n_in / 64);
-    hipLaunchKernelGGL(synth_a8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, m.p0,
-                       reinterpret_cast<uint32_t*>(m.p1), m.n_out, m.n_in, stream, std);
+    qmat_synth_rows(m, 0, m.n_out, seed, key, std, s);
+    return;
   } else if (m.fmt == FMT_Q4K) {
     size_t n = (size_t)m.n_out * m.nsb;
     hipLaunchKernelGGL(synth_q4k_kernel, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, s, m.p0,
@@ -533,6 +560,16 @@ void qmat_synth(QMat& m, uint64_t seed, uint64_t key, float std, hipStream_t s) 
                        reinterpret_cast<int8_t*>(m.p2), reinterpret_cast<uint16_t*>(m.p3), m.n_out, m.n_in, m.nsb,
                        stream, std);
   }
+  PGD_HIP(hipGetLastError());
+}
+
+void qmat_synth_rows(QMat& m, int row0, int rows, uint64_t seed, uint64_t key, float std, hipStream_t s) {
+  PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "row-window synthesis is for A8 matrices");
+  PGD_CHECK(row0 >= 0 && rows >= 0 && row0 + rows <= m.n_out, kErrShape, "synth row window");
+  if (!rows) return;
+  size_t n = (size_t)rows * (m.n_in / 64);
+  hipLaunchKernelGGL(synth_a8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, m.p0,
+                     reinterpret_cast<uint32_t*>(m.p1), row0, rows, m.n_in, synth_stream(seed, key), std);
   PGD_HIP(hipGetLastError());
 }
 

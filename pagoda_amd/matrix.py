@@ -16,6 +16,16 @@ def _ptr(a: np.ndarray) -> C.c_void_p:
     return a.ctypes.data_as(C.c_void_p)
 
 
+def act_bytes(nrows: int, k: int) -> int:
+    from ._lib import lib
+
+    return int(lib().pgd_act_bytes(nrows, k))
+
+
+def act_prep_dev(dev: Device, x_ptr: int, ldx: int, nrows: int, k: int, act_ptr: int) -> None:
+    call("pgd_act_prep_dev", dev.handle, C.c_void_p(x_ptr), ldx, nrows, k, C.c_void_p(act_ptr))
+
+
 class Matrix:
     def __init__(self, dev: Device, handle: C.c_void_p):
         self.dev = dev
@@ -83,6 +93,14 @@ class Matrix:
                  res_ptr: int = 0, ldres: int = 0) -> None:
         call("pgd_matrix_gemv_dev", self.handle, C.c_void_p(x_ptr), int(x_f16), ldx, nrows, C.c_void_p(y_ptr), ldy,
              C.c_void_p(res_ptr or None), ldres)
+
+    def gemv_act_dev(self, act_ptr: int, nrows: int, y_ptr: int, ldy: int, res_ptr: int = 0, ldres: int = 0) -> None:
+        call("pgd_matrix_gemv_act_dev", self.handle, C.c_void_p(act_ptr), nrows, C.c_void_p(y_ptr), ldy,
+             C.c_void_p(res_ptr or None), ldres)
+
+    @staticmethod
+    def gemv_swiglu_act_dev(gate: "Matrix", up: "Matrix", act_ptr: int, nrows: int, mid_ptr: int, ldm: int):
+        call("pgd_matrix_gemv_swiglu_act_dev", gate.handle, up.handle, C.c_void_p(act_ptr), nrows, C.c_void_p(mid_ptr), ldm)
 
     @staticmethod
     def gemv_swiglu_dev(gate: "Matrix", up: "Matrix", x_ptr: int, ldx: int, nrows: int, mid_ptr: int, ldm: int):

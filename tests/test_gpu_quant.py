@@ -177,3 +177,33 @@ def test_config2_sweep_f16_activations(dev, fmt, shape, rows):
     assert rel_err(y, ref) < GEMV_TOL
     dev.free(xd)
     dev.free(yd)
+
+
+def test_prepared_activations_shared_across_matrices(dev):
+    """One activation prep feeds several A8 matrices (qwen3_gemv.rs:149-253
+    gemv_shared); results are bitwise those of the unprepared calls."""
+    from pagoda_amd import Matrix
+    from pagoda_amd.matrix import act_bytes, act_prep_dev
+
+    rng = np.random.default_rng(12)
+    K = 640
+    mats = [Matrix.synth(dev, 0, n, K, 9, 100 + n, 0.02) for n in (96, 33, 512)]
+    for rows in (1, 5, 17, 40):
+        x = rng.normal(0, 1, (rows, K)).astype(np.float32)
+        xd = dev.upload(x)
+        act = dev.alloc(act_bytes(rows, K))
+        act_prep_dev(dev, xd, K, rows, K, act)
+        for m in mats:
+            y1 = dev.alloc(rows * m.n_out * 4)
+            y2 = dev.alloc(rows * m.n_out * 4)
+            m.gemv_dev(xd, K, rows, y1, m.n_out)
+            m.gemv_act_dev(act, rows, y2, m.n_out)
+            a = dev.download(y1, (rows, m.n_out), np.float32)
+            b = dev.download(y2, (rows, m.n_out), np.float32)
+            np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+            ref = x.astype(np.float64) @ m.dequant().astype(np.float64).T
+            assert rel_err(b, ref) < GEMV_TOL
+            dev.free(y1)
+            dev.free(y2)
+        dev.free(xd)
+        dev.free(act)
