@@ -128,7 +128,7 @@ def gpu_bench(args):
         "weight_gb": info["weight_bytes"] / 1e9, "algo_gb_per_step": info["algo_bytes_per_token"] / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": f"A8 fused gate/up SwiGLU GEMV 5120->2x17408, {rows} rows",
+                     "kernel": f"a8_mma_kernel (fused gate/up SwiGLU A8 GEMV 5120->2x17408), {batch} rows",
                      "algo_bytes_per_launch": algo, "avg_launch_us": avg_ms * 1e3,
                      "batch1": {"achieved": algo1 / (avg1 * 1e-3) / 1e9, "avg_launch_us": avg1 * 1e3}},
     }
