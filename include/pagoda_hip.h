@@ -109,6 +109,29 @@ int pgd_matrix_gemv_act_dev(const pgd_matrix* m, const void* act, int nrows, flo
 int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up, const void* act, int nrows,
                                    float* mid, int ldm);
 
+/* ---- decode-step kernels (device pointers, queued on the device stream) ----
+ * Gated-DeltaNet recurrence over a ragged batch: sequence i owns rows
+ * [row_start[i], row_start[i] + row_count[i]) and its fp32 state
+ * states[i] -> [v_heads, 128, 128], updated in place, rows in order.
+ * conv_out [rows, 2*k_heads*128 + v_heads*128] (post conv + SiLU: q | k | v),
+ * a, b [rows, v_heads], z [rows, v_heads*128], out [rows, v_heads*128].
+ * row_start, row_count and states are device arrays.
+ * Replaces the per-token loop of LinearAttn::forward (pagoda-hf/src/
+ * qwen3_5.rs:1330-1383) and gated_delta_step (qwen3_fuse.rs:176-279). */
+int pgd_gdn_step_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_out, const float* a,
+                     const float* b, const float* z, const float* a_log, const float* dt_bias,
+                     const float* norm, float* const* states, const int* row_start, const int* row_count,
+                     int nseq, float* out);
+/* Paged GQA decode attention: row r attends to positions [0, pos_of_row[r]]
+ * of sequence seq_of_row[r], whose pages are block_tables[seq * max_blocks
+ * + p / block] in pools [pages][kv_heads][block][head_dim]. q, gate, out
+ * [rows, heads, head_dim]; gate (nullable) applies sigmoid(gate). Replaces
+ * FullAttn::forward's softmax attention (pagoda-hf/src/qwen3_5.rs:1433-1475)
+ * and full_attn_heads (qwen3_fuse.rs:384-440) over a contiguous cache. */
+int pgd_attn_decode_dev(pgd_dev* dev, int heads, int kv_heads, int head_dim, int block, const float* q,
+                        const float* gate, const float* k_pool, const float* v_pool, const int* seq_of_row,
+                        const int* pos_of_row, const int* block_tables, int max_blocks, int rows, float* out);
+
 /* ---- models and sessions ---------------------------------------------------
  * Architecture of a model handle. arch 0 is the hybrid Qwen3.5 tower
  * (Gated-DeltaNet + gated full attention, MLX affine-8 weights; Qwen35::load

@@ -8,6 +8,7 @@
 #include "../../include/pagoda_hip.h"
 #include "common.h"
 #include "device.h"
+#include "ops.h"
 #include "quant.h"
 
 namespace pgd {
@@ -277,6 +278,51 @@ int pgd_matrix_gemv_swiglu_dev(const pgd_matrix* gate, const pgd_matrix* up, con
     PGD_CHECK(ldm >= gate->m.n_out, kErrShape, "swiglu output stride");
     DeviceScope scope(gate->dev);
     qmat_gemv_swiglu(gate->m, up->m, x, ldx, nrows, mid, ldm, gate->dev->stream);
+  });
+}
+
+int pgd_gdn_step_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_out, const float* a, const float* b,
+                     const float* z, const float* a_log, const float* dt_bias, const float* norm, float* const* states,
+                     const int* row_start, const int* row_count, int nseq, float* out) {
+  return guard([&] {
+    PGD_CHECK(dev && conv_out && a && b && z && a_log && dt_bias && norm && states && row_start && row_count && out,
+              kErrArg, "null argument");
+    PGD_CHECK(nseq >= 0, kErrArg, "nseq");
+    DeviceScope scope(dev);
+    GdnParams p{};
+    p.k_heads = k_heads;
+    p.v_heads = v_heads;
+    p.k_dim = 128;
+    p.v_dim = 128;
+    p.conv_out = conv_out;
+    p.ld_conv = 2 * k_heads * 128 + v_heads * 128;
+    p.a = a;
+    p.b = b;
+    p.ld_ab = v_heads;
+    p.z = z;
+    p.ld_z = v_heads * 128;
+    p.a_log = a_log;
+    p.dt_bias = dt_bias;
+    p.norm = norm;
+    p.out = out;
+    p.ld_out = v_heads * 128;
+    p.state_base = states;
+    p.state_off = 0;
+    gdn_step(p, SeqMeta{row_start, row_count}, nseq, dev->stream);
+  });
+}
+
+int pgd_attn_decode_dev(pgd_dev* dev, int heads, int kv_heads, int head_dim, int block, const float* q,
+                        const float* gate, const float* k_pool, const float* v_pool, const int* seq_of_row,
+                        const int* pos_of_row, const int* block_tables, int max_blocks, int rows, float* out) {
+  return guard([&] {
+    PGD_CHECK(dev && q && k_pool && v_pool && seq_of_row && pos_of_row && block_tables && out, kErrArg,
+              "null argument");
+    PGD_CHECK(block > 0 && max_blocks > 0 && rows >= 0, kErrArg, "bad page geometry");
+    DeviceScope scope(dev);
+    AttnLayout L{heads, kv_heads, head_dim, head_dim, block, const_cast<float*>(k_pool), const_cast<float*>(v_pool)};
+    RowMeta m{seq_of_row, pos_of_row, block_tables, max_blocks, nullptr, nullptr};
+    attn_decode(q, gate, out, L, m, rows, dev->stream);
   });
 }
 

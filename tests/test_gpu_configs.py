@@ -1,0 +1,103 @@
+"""Full-size configurations against the CPU oracle on identical seeded weights.
+
+Config 1: Qwen2.5-0.5B architecture, Q4_K_M-style
+GGUF weights, 81-token random prompt, 32 greedy tokens; then the warm rerun
+where the prefix cache supplies 80 prompt tokens and only 32 are fed
+(pagoda/docs/BENCHMARK-METAL.md:25-33; examples/qwen2_gguf.rs:121-136: cold
+and warm token streams are identical).
+
+Config 4 widths on one 3:1 layer group: hidden 5120, SwiGLU
+17408, 24/4 heads of 256, 16/32 GDN heads of 128, A8 weights.
+
+The greedy rule is the engine sampler's (first max, pagoda/src/sampler.rs:59-69);
+the top-2 logit margin of every step is printed so a near-tie is visible.
+"""
+import numpy as np
+import pytest
+
+from oracle import pyoracle as ora
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3
+
+
+def rel(a, b):
+    return float(np.abs(a.astype(np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def margin(x):
+    t = np.sort(x)[-2:]
+    return float(t[1] - t[0])
+
+
+def test_config1_qwen2_05b_greedy_32_cold_and_warm(dev):
+    from pagoda_amd.engine import QWEN2_05B, Model, argmax_first
+
+    cfg = QWEN2_05B
+    seed = 1
+    print("config1: building device model", flush=True)
+    model = Model.synth(dev, cfg, seed)
+    print("config1: building oracle model", flush=True)
+    oracle = ora.Qwen2(ora.Qwen2Config(), seed)
+    rng = np.random.default_rng(81)
+    prompt = rng.integers(0, cfg.vocab, 81)
+    s = model.new_session()
+    oc = oracle.new_cache()
+    got = s.forward(prompt)
+    ref = oracle.forward(prompt, oc)
+    assert rel(got, ref) < LOGIT_TOL
+    gen_gpu, gen_ref, margins = [], [], []
+    for step in range(32):
+        tg, tr = argmax_first(got), ora.argmax_first(ref)
+        margins.append(margin(ref))
+        gen_gpu.append(tg)
+        gen_ref.append(tr)
+        assert tg == tr, f"step {step}: gpu {tg} oracle {tr} (margin {margins[-1]:.3g})"
+        if step == 31:
+            break
+        got = s.forward([tg])
+        ref = oracle.forward([tr], oc)
+        assert rel(got, ref) < LOGIT_TOL, f"step {step}: {rel(got, ref)}"
+    print("config1: min top-2 margin", min(margins), flush=True)
+    # warm rerun: a session holding the first 80 prompt tokens (the graft) feeds
+    # the last prompt token, then the 31 generated tokens it samples itself
+    warm = model.new_session()
+    warm.forward(prompt[:80])
+    w2 = warm.fork()
+    fed = 0
+    logits = w2.forward(prompt[80:])
+    fed += 1
+    warm_ids = []
+    for step in range(32):
+        t = argmax_first(logits)
+        warm_ids.append(t)
+        if step == 31:
+            break
+        logits = w2.forward([t])
+        fed += 1
+    assert fed == 32
+    assert warm_ids == gen_gpu
+
+
+def test_config4_widths_one_layer_group(dev):
+    from pagoda_amd.engine import QWEN35_27B, Model, argmax_first
+    from dataclasses import replace
+
+    cfg = replace(QWEN35_27B, n_layers=4, vocab=32768, max_pos=256, kv_blocks=64)
+    seed = 4
+    model = Model.synth(dev, cfg, seed)
+    oracle = ora.Qwen35(ora.Qwen35Config(n_layers=4, vocab=32768), seed)
+    rng = np.random.default_rng(19)
+    prompt = rng.integers(0, cfg.vocab, 19)
+    s = model.new_session()
+    oc = oracle.new_cache()
+    got = s.forward(prompt)
+    ref = oracle.forward(prompt, oc)
+    assert rel(got, ref) < LOGIT_TOL
+    for step in range(8):
+        assert argmax_first(got) == ora.argmax_first(ref), step
+        t = ora.argmax_first(ref)
+        got = s.forward([t])
+        ref = oracle.forward([t], oc)
+        assert rel(got, ref) < LOGIT_TOL, (step, rel(got, ref))
