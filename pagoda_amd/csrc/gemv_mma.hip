@@ -7,22 +7,32 @@
 // xh = f16(x) and xl = f16(x - xh) carry x to ~22 bits, codes - 128 are
 // exact in f16, XS = sum x and XSP = sum (xh + xl) over the group in f32.
 // The batch row is the MFMA's M index and the weight row its N index: a lane
-// owns one weight row (one scale/bias load per group) and four batch rows,
-// and every batch row goes through the same instruction sequence whatever the
-// batch size, so a batched call is bitwise equal to single-row calls.
+// owns one weight row (one scale/bias per group) and four batch rows. Every
+// batch row goes through the same instruction sequence and the same split of
+// the groups whatever the batch size, so a batched call is bitwise equal to
+// single-row calls.
 //
 // Activations are converted once (a8_xprep_kernel, or fused into the RMSNorm
 // that produces them, a8_norm_prep_kernel) into the MFMA operand order;
-// weights are stored tiled (32 rows x 64 codes per 2 KiB block), so a wave's
-// 128-bit loads read 512 B runs. A workgroup of KS waves shares one 32-row
-// tile and splits the groups between its waves; each wave keeps PF groups of
-// loads in flight; partial sums meet in LDS in a fixed order.
+// weights are stored tiled (32 rows x 64 codes per 2 KiB block).
+//
+// Streaming: a workgroup of kKS waves shares one 32-row tile (two for wide
+// matrices at full batch) and splits its groups between the waves. Each wave
+// keeps a private LDS ring of P stages; a stage holds everything one group
+// needs and is filled by direct global->LDS loads (weights, scale/bias,
+// activation operands, per-row constants). All loads of the loop go to LDS,
+// so they retire in issue order and one explicit vmcnt wait per group keeps
+// the next P-1 groups in flight; the compiler sees no loaded registers to
+// wait on. Only the rows the batch needs are staged (one row, four rows, one
+// or two 16-row tiles), which keeps stages small and many waves resident.
+// Partial sums of the waves meet in LDS in a fixed order.
 //
 // Counterpart of affine_gemv / affine_gemm4 / gemv2_silu / gemv_res
 // (pagoda-hf/src/qwen3_gemv.rs:54-306, 414-567).
 #include "common.h"
 #include "gemv_impl.h"
 #include "quant.h"
+#include "a8_stage_reads.h"
 
 namespace pgd {
 namespace gemv {
@@ -54,11 +64,13 @@ __device__ inline h8 codes8(uint32_t w0, uint32_t w1) {
 // ---- activation prep --------------------------------------------------------
 // Rows are cut into chunks of 32 (two 16-row batch tiles). For chunk c,
 // group g, batch tile bt, item = (c * G + g) * 2 + bt:
-//   XA[item][lane] = 64 B: xh step 0 | xh step 1 | xl step 0 | xl step 1,
-//     8 halves each, batch row 32c + 16bt + lane % 16, k = 64g + 16(lane/16) + 8 step + e
+//   XA[item][i][lane] = 16 B, operand i = xh step 0 | xh step 1 | xl step 0 |
+//     xl step 1 (8 halves), batch row 32c + 16bt + lane % 16,
+//     k = 64g + 16(lane/16) + 8 step + e
 //   CA[item] = 32 floats: 128 * XSP for the 16 rows, then XS for the 16 rows
 // Rows past the end are never written: their MFMA rows only feed discarded
 // outputs.
+// o points at lane's slot of operand 0; operand i sits 64 slots further
 __device__ inline void prep16(const float* v, uint4* o, float& xs, float& xsp) {
   uint32_t hw[8], lw[8];
   xs = 0.0f;
@@ -73,9 +85,9 @@ __device__ inline void prep16(const float* v, uint4* o, float& xs, float& xsp) {
     xsp += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
   }
   o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-  o[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-  o[2] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  o[3] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+  o[64] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+  o[128] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  o[192] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
 }
 
 __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__ x, int ldx, int rows, int G,
@@ -103,7 +115,7 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
     for (int i = 0; i < 16; ++i) v[i] = 0.0f;
   }
   float xs, xsp;
-  prep16(v, XA + (item * 64 + lane) * 4, xs, xsp);
+  prep16(v, XA + item * 256 + lane, xs, xsp);
   // the four lanes of a row (q = 0..3) hold its four 16-wide k slices
   xs += __shfl_xor(xs, 16, 64);
   xs += __shfl_xor(xs, 32, 64);
@@ -174,7 +186,7 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
       }
       const int g = u >> 2, q = u & 3;
       const size_t item = ((size_t)c * G + g) * 2 + bt;
-      prep16(v[i], XA + (item * 64 + q * 16 + j) * 4, xs, xsp);
+      prep16(v[i], XA + item * 256 + q * 16 + j, xs, xsp);
     }
     // group sums over the four slices of a group (adjacent lanes)
     xs += __shfl_xor(xs, 1, 64);
@@ -189,126 +201,209 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
   }
 }
 
-template <int NS, int NBT>
-struct GroupRaw {
-  uint4 w[NS];       // 16 codes per weight subtile
-  uint32_t sb[NS];   // scale | bias
-  uint4 xa[NBT][4];  // A operands
-  float4 cp[NBT];    // 128 * XSP of this lane's 4 batch rows
-  float4 xs[NBT];    // XS of this lane's 4 batch rows
-};
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
 
-// NS = 16-row weight subtiles per wave (2 = one 32-row tile; 4 = gate + up)
-template <int NBT, int KS, int PF, int EPI>
-__global__ __launch_bounds__(64 * KS) void a8_mma_kernel(GemvArgs a, const uint4* __restrict__ XA,
-                                                         const float* __restrict__ CA, int nb) {
+// per-mode stage geometry: activation bytes, constant bytes, loads of both
+template <int MODE> struct StageGeo;
+template <> struct StageGeo<0> { static constexpr int NBT = 1, XB = 1024, CB = 256, KX = 2; };
+template <> struct StageGeo<1> { static constexpr int NBT = 1, XB = 4096, CB = 256, KX = 5; };
+template <> struct StageGeo<2> { static constexpr int NBT = 2, XB = 8192, CB = 512, KX = 10; };
+template <> struct StageGeo<3> { static constexpr int NBT = 1, XB = 256, CB = 16, KX = 2; };
+
+constexpr int kKS = 4;  // waves per workgroup (groups split between them); fixed, so every batch sums alike
+
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)((const __attribute__((address_space(3))) char*)p);
+}
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left at their maxima
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void dma16(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, void* l) {
+  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 4, 0, 0);
+}
+
+template <int MODE, int P, int MT, int EPI>
+__global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint4* __restrict__ XA,
+                                                          const float* __restrict__ CA, int nb) {
+  using Geo = StageGeo<MODE>;
+  constexpr int KS = kKS;
+  constexpr int NBT = Geo::NBT;
   constexpr bool DUAL = EPI == EPI_SWIGLU;
-  constexpr int NS = DUAL ? 4 : 2;
-  __shared__ f4 red[KS > 1 ? KS - 1 : 1][NS][NBT][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  static_assert(!DUAL || MT == 1, "SwiGLU pairs the gate and up subtiles of one tile");
+  constexpr int NS = DUAL ? 4 : 2 * MT;  // 16-row weight subtiles per wave
+  constexpr int SBOFF = NS * 1024, XOFF = SBOFF + (MODE == 3 ? NS * 64 : 256), COFF = XOFF + Geo::XB;
+  constexpr int STAGE = COFF + Geo::CB;
+  constexpr int NDMA = NS + 1 + Geo::KX;  // loads per group
+  constexpr int NWAIT = (P - 1) * NDMA;
+  constexpr size_t RING = (size_t)KS * P * STAGE;
+  constexpr size_t RED = sizeof(f4) * (KS - 1) * NS * NBT * 64;
+  static_assert(RING <= 160 * 1024 && RED <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) char smem[RING > RED ? RING : RED];
+  auto& red = *reinterpret_cast<f4(*)[KS - 1][NS][NBT][64]>(smem);
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, q = lane >> 4;  // MFMA column (weight row in subtile), k quarter / row quad
-  const int tile = blockIdx.x;
   const int G = a.n_in >> 6;
-  const uint8_t* wbase[NS];
-  const uint32_t* sbase[NS];
+  const int ntiles = (a.n_out + 31) >> 5;
+  char* ring = smem + (size_t)wave * P * STAGE;
+  const uint32_t ring_lds = lds_addr(ring);
+
+  // weights: each lane stages (and later reads back) its own 16 B of each subtile
+  const uint8_t* wsrc[NS];
 #pragma unroll
   for (int st = 0; st < NS; ++st) {
     const uint8_t* p = (DUAL && st >= 2) ? a.u0 : a.p0;
-    const uint8_t* ps = (DUAL && st >= 2) ? a.u1 : a.p1;
-    const int r = 16 * (st & 1) + j;  // row within the 32-row tile
-    wbase[st] = p + ((size_t)tile * G << 11) + (q >> 1) * 1024 + r * 32 + (q & 1) * 16;
-    sbase[st] = reinterpret_cast<const uint32_t*>(ps) + ((size_t)tile * G << 5) + r;
+    // a missing second tile re-reads the last one; its outputs are dropped
+    const int tile = min(blockIdx.x * MT + (DUAL ? 0 : st >> 1), ntiles - 1);
+    const int r = 16 * (st & 1) + j;
+    wsrc[st] = p + ((size_t)tile * G << 11) + (q >> 1) * 1024 + r * 32 + (q & 1) * 16;
   }
-  const bool bt1 = NBT > 1 && nb > 16;
+  // scale/bias: lane L stages subtile min(L / 16, NS - 1), row L % 16
+  const uint32_t* ssrc;
+  {
+    const int st = min(lane >> 4, NS - 1);
+    const uint8_t* ps = (DUAL && st >= 2) ? a.u1 : a.p1;
+    const int tile = min(blockIdx.x * MT + (DUAL ? 0 : st >> 1), ntiles - 1);
+    ssrc = reinterpret_cast<const uint32_t*>(ps) + ((size_t)tile * G << 5) + 16 * (st & 1) + j;
+  }
+  // activation sources (uint4 / float offsets within an item) and LDS read offsets
+  int xsrc, csrc;
+  uint32_t xrd, crd;
+  if constexpr (MODE == 3) {  // lane L < 16: operand L / 4 of k quarter L % 4, row 0
+    xsrc = (lane >> 2) * 64 + (lane & 3) * 16;
+    csrc = (lane & 1) ? 16 : 0;
+    xrd = q * 16;
+    crd = 0;
+  } else if constexpr (MODE == 0) {  // lane L: operand L / 16, k quarter (L / 4) % 4, row L % 4
+    xsrc = (lane >> 4) * 64 + ((lane >> 2) & 3) * 16 + (lane & 3);
+    csrc = ((lane & 4) ? 16 : 0) + (lane & 3);
+    xrd = (q * 4 + (j & 3)) * 16;
+    crd = 0;
+  } else {
+    xsrc = lane;
+    csrc = lane & 31;
+    xrd = lane * 16;
+    crd = 16 * q;
+  }
+
   f4 Y[NS][NBT];
 #pragma unroll
   for (int st = 0; st < NS; ++st)
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
 
-  auto load = [&](int g, GroupRaw<NS, NBT>& R) {
+  // stage u <- group g: exactly NDMA loads, whatever the mode's lane masks
+  auto issue = [&](int g, int u) {
+    char* sb = ring + u * STAGE;
 #pragma unroll
-    for (int st = 0; st < NS; ++st) {
-      R.w[st] = *reinterpret_cast<const uint4*>(wbase[st] + ((size_t)g << 11));
-      R.sb[st] = sbase[st][(size_t)g << 5];
-    }
+    for (int st = 0; st < NS; ++st) dma16(wsrc[st] + ((size_t)g << 11), sb + st * 1024);
+    if (MODE != 3 || lane < 16 * NS) dma4(ssrc + ((size_t)g << 5), sb + SBOFF);
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) {
-      if (bt == 0 || bt1) {
-        const size_t item = (size_t)g * 2 + bt;
-        const uint4* xp = XA + (item * 64 + lane) * 4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) R.xa[bt][i] = xp[i];
-        R.cp[bt] = *reinterpret_cast<const float4*>(CA + item * 32 + 4 * q);
-        R.xs[bt] = *reinterpret_cast<const float4*>(CA + item * 32 + 16 + 4 * q);
+      const size_t item = (size_t)g * 2 + bt;
+      if constexpr (MODE == 3) {
+        if (lane < 16) dma16(XA + item * 256 + xsrc, sb + XOFF);
+        if (lane < 2) dma4(CA + item * 32 + csrc, sb + COFF);
+      } else if constexpr (MODE == 0) {
+        dma16(XA + item * 256 + xsrc, sb + XOFF);
+        dma4(CA + item * 32 + csrc, sb + COFF);
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) R.xa[bt][i] = make_uint4(0u, 0u, 0u, 0u);
-        R.cp[bt] = make_float4(0.f, 0.f, 0.f, 0.f);
-        R.xs[bt] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int i = 0; i < 4; ++i) dma16(XA + item * 256 + i * 64 + xsrc, sb + XOFF + bt * 4096 + i * 1024);
+        dma4(CA + item * 32 + csrc, sb + COFF + bt * 256);
       }
     }
   };
 
-  auto compute = [&](const GroupRaw<NS, NBT>& R) {
+  auto compute = [&](int u) {
+    const uint32_t base = ring_lds + u * STAGE;
+    uint4 W[NS];
+    uint32_t S[NS];
+    uint4 X[NBT][4];
+    float4 CP[NBT], XS[NBT];
+    if constexpr (MODE == 3) {
+      float2 c1;
+      StageReads<MODE, NS>::run(base + 16 * lane, base + SBOFF + 4 * j, base + XOFF + xrd, base + COFF + crd, W, S, X,
+                                c1);
+      CP[0] = make_float4(c1.x, c1.x, c1.x, c1.x);
+      XS[0] = make_float4(c1.y, c1.y, c1.y, c1.y);
+    } else {
+      StageReads<MODE, NS>::run(base + 16 * lane, base + SBOFF + 4 * j, base + XOFF + xrd, base + COFF + crd, W, S, X,
+                                CP, XS);
+    }
 #pragma unroll
     for (int st = 0; st < NS; ++st) {
-      const h8 b0 = codes8(R.w[st].x, R.w[st].y);
-      const h8 b1 = codes8(R.w[st].z, R.w[st].w);
-      const float sc = bf16_to_f32(R.sb[st] & 0xffffu);
-      const float bi = bf16_to_f32(R.sb[st] >> 16);
+      const h8 b0 = codes8(W[st].x, W[st].y);
+      const h8 b1 = codes8(W[st].z, W[st].w);
+      const float sc = bf16_to_f32(S[st] & 0xffffu);
+      const float bi = bf16_to_f32(S[st] >> 16);
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) {
-        f4 P = {0.f, 0.f, 0.f, 0.f};
-        P = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, R.xa[bt][0]), b0, P, 0, 0, 0);
-        P = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, R.xa[bt][1]), b1, P, 0, 0, 0);
-        P = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, R.xa[bt][2]), b0, P, 0, 0, 0);
-        P = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, R.xa[bt][3]), b1, P, 0, 0, 0);
-        const float cp[4] = {R.cp[bt].x, R.cp[bt].y, R.cp[bt].z, R.cp[bt].w};
-        const float xs[4] = {R.xs[bt].x, R.xs[bt].y, R.xs[bt].z, R.xs[bt].w};
+        f4 Pm = {0.f, 0.f, 0.f, 0.f};
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][0]), b0, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][1]), b1, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][2]), b0, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][3]), b1, Pm, 0, 0, 0);
+        const float cpa[4] = {CP[bt].x, CP[bt].y, CP[bt].z, CP[bt].w};
+        const float xsa[4] = {XS[bt].x, XS[bt].y, XS[bt].z, XS[bt].w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(bi, xs[r], fmaf(sc, P[r] + cp[r], Y[st][bt][r]));
+        for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(bi, xsa[r], fmaf(sc, Pm[r] + cpa[r], Y[st][bt][r]));
       }
     }
   };
 
-  // groups of this wave: a contiguous range, PF groups in flight
+  // groups of this wave: a contiguous range; prefetches past its end re-read
+  // the last group (an L2 hit), so every step issues NDMA loads and the wait
+  // count stays fixed
   const int per = (G + KS - 1) / KS;
   const int g0 = wave * per, g1 = min(G, g0 + per);
-  GroupRaw<NS, NBT> buf[PF];
+  if (g0 < g1) {
 #pragma unroll
-  for (int u = 0; u < PF; ++u)
-    if (g0 + u < g1) load(g0 + u, buf[u]);
-  for (int g = g0; g < g1; g += PF) {
+    for (int u = 0; u < P; ++u) issue(min(g0 + u, g1 - 1), u);
+    int g = g0;
+    for (; g + P <= g1; g += P) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      if (g + u < g1) {
-        compute(buf[u]);
-        if (g + u + PF < g1) load(g + u + PF, buf[u]);
+      for (int u = 0; u < P; ++u) {
+        wait_vmcnt<NWAIT>();  // group g + u has landed; the next P - 1 stay in flight
+        compute(u);
+        issue(min(g + u + P, g1 - 1), u);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int u = 0; u < P - 1; ++u)
+      if (g + u < g1) compute(u);
   }
 
   // ---- split-K reduction (fixed order: wave 0 + 1 + ... + KS-1) ----
-  if constexpr (KS > 1) {
-    if (wave > 0) {
+  wait_vmcnt<0>();
+  __syncthreads();  // the reduction buffer overlays the rings
+  if (wave > 0) {
 #pragma unroll
-      for (int st = 0; st < NS; ++st)
+    for (int st = 0; st < NS; ++st)
 #pragma unroll
-        for (int bt = 0; bt < NBT; ++bt) red[wave - 1][st][bt][lane] = Y[st][bt];
-    }
-    __syncthreads();
-    if (wave != 0) return;
-    for (int w = 0; w < KS - 1; ++w)
-#pragma unroll
-      for (int st = 0; st < NS; ++st)
-#pragma unroll
-        for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[w][st][bt][lane];
+      for (int bt = 0; bt < NBT; ++bt) red[wave - 1][st][bt][lane] = Y[st][bt];
   }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w = 0; w < KS - 1; ++w)
+#pragma unroll
+    for (int st = 0; st < NS; ++st)
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[w][st][bt][lane];
+
   // ---- epilogue: lane holds weight row n for batch rows 16bt + 4q + r ----
 #pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    const int n = tile * 32 + 16 * st + j;
+  for (int st = 0; st < (DUAL ? 2 : NS); ++st) {
+    const int n = (blockIdx.x * MT + (DUAL ? 0 : st >> 1)) * 32 + 16 * (st & 1) + j;
     if (n >= a.n_out) continue;
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt)
@@ -324,30 +419,24 @@ __global__ __launch_bounds__(64 * KS) void a8_mma_kernel(GemvArgs a, const uint4
   }
 }
 
-constexpr int kPF = 2;  // groups of loads in flight per wave
-
-template <int NBT, int KS, int EPI>
+template <int MODE, int P, int MT, int EPI>
 void launch_kernel(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
-  constexpr int PF = kPF;
   const int tiles = (a.n_out + 31) / 32;
-  hipLaunchKernelGGL((a8_mma_kernel<NBT, KS, PF, EPI>), dim3(tiles), dim3(64 * KS), 0, s, a, XA, CA, nb);
+  hipLaunchKernelGGL((a8_mma_kernel<MODE, P, MT, EPI>), dim3((tiles + MT - 1) / MT), dim3(64 * kKS), 0, s, a, XA, CA,
+                     nb);
 }
 
-template <int NBT, int EPI>
-void launch_ks(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
-  // enough waves to fill the GPU (~8 per CU), each wave keeping its prefetch
-  // ring busy. The split depends on the matrix shape only, never on the batch,
-  // so every batch size sums a row's groups in the same order.
-  const int tiles = (a.n_out + 31) / 32;
-  const int G = a.n_in / 64;
-  int ks = 1;
-  while (ks < 8 && tiles * ks < 2048 && G / (2 * ks) >= 4) ks *= 2;
-  switch (ks) {
-    case 1: launch_kernel<NBT, 1, EPI>(a, XA, CA, nb, s); break;
-    case 2: launch_kernel<NBT, 2, EPI>(a, XA, CA, nb, s); break;
-    case 4: launch_kernel<NBT, 4, EPI>(a, XA, CA, nb, s); break;
-    default: launch_kernel<NBT, 8, EPI>(a, XA, CA, nb, s); break;
+// one launch per chunk of up to 32 rows; the mode stages only the rows present
+template <int EPI>
+void launch_chunk(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
+  if (nb == 1) return launch_kernel<3, 3, 1, EPI>(a, XA, CA, nb, s);
+  if (nb <= 4) return launch_kernel<0, 4, 1, EPI>(a, XA, CA, nb, s);
+  if (nb <= 16) return launch_kernel<1, 4, 1, EPI>(a, XA, CA, nb, s);
+  if constexpr (EPI != EPI_SWIGLU) {
+    // wide matrices: two tiles per wave halve the activation traffic per weight byte
+    if ((a.n_out + 31) / 32 >= 256) return launch_kernel<2, 3, 2, EPI>(a, XA, CA, nb, s);
   }
+  launch_kernel<2, 3, 1, EPI>(a, XA, CA, nb, s);
 }
 
 template <int EPI>
@@ -358,10 +447,9 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   int rows = act.rows;
   for (int c = 0; rows > 0; ++c) {
     const int nb = rows < 32 ? rows : 32;
-    const uint4* xa = XA + (size_t)c * G * 2 * 64 * 4;
+    const uint4* xa = XA + (size_t)c * G * 2 * 256;
     const float* ca = act.CA + (size_t)c * G * 2 * 32;
-    if (nb > 16) launch_ks<2, EPI>(a, xa, ca, nb, s);
-    else launch_ks<1, EPI>(a, xa, ca, nb, s);
+    launch_chunk<EPI>(a, xa, ca, nb, s);
     PGD_HIP(hipGetLastError());
     rows -= nb;
     a.y += (size_t)nb * a.ldy;

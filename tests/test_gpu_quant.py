@@ -207,3 +207,24 @@ def test_prepared_activations_shared_across_matrices(dev):
             dev.free(y2)
         dev.free(xd)
         dev.free(act)
+
+
+@pytest.mark.parametrize("n_out", [8200, 8192 + 64])
+@pytest.mark.parametrize("rows", [19, 32, 45])
+def test_a8_two_tile_waves_large_matrix(dev, n_out, rows):
+    """Matrices of 256+ row tiles run two tiles per wave when a launch holds
+    17-32 rows; an odd tile count leaves the last wave with one real tile.
+    Checked against fp64 and the batched == serial bitwise bar (the serial
+    calls take the one-row staging)."""
+    from pagoda_amd import Matrix
+
+    K = 512
+    m = Matrix.synth(dev, 0, n_out, K, 31, 7, 0.02)
+    deq = m.dequant()
+    rng = np.random.default_rng(n_out)
+    x = rng.normal(0, 1, (rows, K)).astype(np.float32)
+    y = m.gemv(x)
+    ref = x.astype(np.float64) @ deq.astype(np.float64).T
+    assert rel_err(y, ref) < GEMV_TOL
+    for i in (0, 7, rows - 1):
+        np.testing.assert_array_equal(m.gemv(x[i]).view(np.uint32), y[i].view(np.uint32))
