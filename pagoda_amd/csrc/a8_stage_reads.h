@@ -10,9 +10,9 @@
 // Stage layout (bytes from the stage base): weights NS x 1 KiB at 0 (lane's
 // own 16 B at 16 * lane), scale/bias u32 at SBOFF (subtile st, row j at
 // 4 * (16 st + j)), activation operands at XOFF, per-row constants at COFF.
-// MODE 0: <= 4 batch rows, 4-row compact operands ([i][q][row] 16 B each)
+// MODE 0: <= 4 batch rows, operands of 4 rows staged as [i][q][row] 16 B
 // MODE 1: <= 16 rows ([i][lane] 16 B), MODE 2: <= 32 rows (two such tiles)
-// MODE 3: one row (row 0 only, [i][q] 16 B; constants as one float2)
+// MODE 3: one row (row 0 only, [i][q] 16 B; its two constants as one float2)
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>

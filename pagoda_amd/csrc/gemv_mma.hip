@@ -68,10 +68,16 @@ __device__ inline h8 codes8(uint32_t w0, uint32_t w1) {
 //     xl step 1 (8 halves), batch row 32c + 16bt + lane % 16,
 //     k = 64g + 16(lane/16) + 8 step + e
 //   CA[item] = 32 floats: 128 * XSP for the 16 rows, then XS for the 16 rows
+// A chunk holding at most 4 rows (the decode batches of 1..4) is stored
+// compact instead, in the first part of the same region, so that one row's
+// operands are one contiguous run:
+//   X4[g][row][i][q] = 16 B (row < 4),   C4[g] = 128 * XSP[4 rows], XS[4 rows]
 // Rows past the end are never written: their MFMA rows only feed discarded
 // outputs.
-// o points at lane's slot of operand 0; operand i sits 64 slots further
-__device__ inline void prep16(const float* v, uint4* o, float& xs, float& xsp) {
+__device__ inline bool chunk_compact(int rows, int c) { return rows - 32 * c <= 4; }
+
+// the four operands of one 16-wide k slice and its partial sums
+__device__ inline void prep16(const float* v, uint4 (&o)[4], float& xs, float& xsp) {
   uint32_t hw[8], lw[8];
   xs = 0.0f;
   xsp = 0.0f;
@@ -85,9 +91,16 @@ __device__ inline void prep16(const float* v, uint4* o, float& xs, float& xsp) {
     xsp += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
   }
   o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-  o[64] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-  o[128] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  o[192] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+  o[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+  o[2] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  o[3] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+}
+
+// store operand i at dst[i * S]
+template <int S>
+__device__ inline void put4(uint4* dst, const uint4 (&o)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[i * S] = o[i];
 }
 
 __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__ x, int ldx, int rows, int G,
@@ -98,7 +111,9 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
   const size_t cg = item >> 1;
   const int g = (int)(cg % G), c = (int)(cg / G);
   if (32 * c >= rows) return;
-  const int row = 32 * c + 16 * bt + (lane & 15), q = lane >> 4;
+  const bool compact = chunk_compact(rows, c);
+  if (compact && bt) return;
+  const int row = 32 * c + 16 * bt + (lane & 15), q = lane >> 4, j = lane & 15;
   float v[16];
   if (row < rows) {
     const float4* xp = reinterpret_cast<const float4*>(x + (size_t)row * ldx + (g << 6) + 16 * q);
@@ -115,15 +130,23 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
     for (int i = 0; i < 16; ++i) v[i] = 0.0f;
   }
   float xs, xsp;
-  prep16(v, XA + item * 256 + lane, xs, xsp);
+  uint4 o[4];
+  prep16(v, o, xs, xsp);
+  if (!compact) put4<64>(XA + item * 256 + lane, o);
+  else if (j < 4) put4<4>(XA + (size_t)c * G * 512 + ((size_t)g * 4 + j) * 16 + q, o);
   // the four lanes of a row (q = 0..3) hold its four 16-wide k slices
   xs += __shfl_xor(xs, 16, 64);
   xs += __shfl_xor(xs, 32, 64);
   xsp += __shfl_xor(xsp, 16, 64);
   xsp += __shfl_xor(xsp, 32, 64);
   if (q == 0) {
-    CA[item * 32 + (lane & 15)] = 128.0f * xsp;
-    CA[item * 32 + 16 + (lane & 15)] = xs;
+    if (!compact) {
+      CA[item * 32 + j] = 128.0f * xsp;
+      CA[item * 32 + 16 + j] = xs;
+    } else if (j < 4) {
+      CA[(size_t)c * G * 64 + (size_t)g * 8 + j] = 128.0f * xsp;
+      CA[(size_t)c * G * 64 + (size_t)g * 8 + 4 + j] = xs;
+    }
   }
 }
 
@@ -164,6 +187,7 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
   __syncthreads();
   const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)n + eps);
   const int c = r >> 5, bt = (r >> 4) & 1, j = r & 15;
+  const bool compact = chunk_compact(rows, c);  // then r % 32 < 4
 #pragma unroll
   for (int i = 0; i < kNormMaxSlices; ++i) {
     const int u = tid + 256 * i;
@@ -186,7 +210,10 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
       }
       const int g = u >> 2, q = u & 3;
       const size_t item = ((size_t)c * G + g) * 2 + bt;
-      prep16(v[i], XA + item * 256 + q * 16 + j, xs, xsp);
+      uint4 o[4];
+      prep16(v[i], o, xs, xsp);
+      if (compact) put4<4>(XA + (size_t)c * G * 512 + ((size_t)g * 4 + j) * 16 + q, o);
+      else put4<64>(XA + item * 256 + q * 16 + j, o);
     }
     // group sums over the four slices of a group (adjacent lanes)
     xs += __shfl_xor(xs, 1, 64);
@@ -195,8 +222,13 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
     xsp += __shfl_xor(xsp, 2, 64);
     if (live && (u & 3) == 0) {
       const size_t item = ((size_t)c * G + (u >> 2)) * 2 + bt;
-      CA[item * 32 + j] = 128.0f * xsp;
-      CA[item * 32 + 16 + j] = xs;
+      if (compact) {
+        CA[(size_t)c * G * 64 + (size_t)(u >> 2) * 8 + j] = 128.0f * xsp;
+        CA[(size_t)c * G * 64 + (size_t)(u >> 2) * 8 + 4 + j] = xs;
+      } else {
+        CA[item * 32 + j] = 128.0f * xsp;
+        CA[item * 32 + 16 + j] = xs;
+      }
     }
   }
 }
@@ -211,7 +243,6 @@ template <> struct StageGeo<1> { static constexpr int NBT = 1, XB = 4096, CB = 2
 template <> struct StageGeo<2> { static constexpr int NBT = 2, XB = 8192, CB = 512, KX = 10; };
 template <> struct StageGeo<3> { static constexpr int NBT = 1, XB = 256, CB = 16, KX = 2; };
 
-constexpr int kKS = 4;  // waves per workgroup (groups split between them); fixed, so every batch sums alike
 
 __device__ inline uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)((const __attribute__((address_space(3))) char*)p);
@@ -229,11 +260,15 @@ __device__ __forceinline__ void dma4(const void* g, void* l) {
   __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 4, 0, 0);
 }
 
-template <int MODE, int P, int MT, int EPI>
-__global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint4* __restrict__ XA,
-                                                          const float* __restrict__ CA, int nb) {
+// KS: ranges the groups are split into (fixed per matrix shape, so every batch
+// size sums alike); KP: waves per workgroup, each summing R = KS / KP
+// consecutive ranges into separate accumulators; P: ring stages per wave.
+template <int MODE, int KS, int KP, int P, int MT, int EPI>
+__global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4* __restrict__ XA,
+                                                         const float* __restrict__ CA, int nb) {
   using Geo = StageGeo<MODE>;
-  constexpr int KS = kKS;
+  static_assert(KS % KP == 0, "whole ranges per wave");
+  constexpr int R = KS / KP;
   constexpr int NBT = Geo::NBT;
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   static_assert(!DUAL || MT == 1, "SwiGLU pairs the gate and up subtiles of one tile");
@@ -242,7 +277,7 @@ __global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint
   constexpr int STAGE = COFF + Geo::CB;
   constexpr int NDMA = NS + 1 + Geo::KX;  // loads per group
   constexpr int NWAIT = (P - 1) * NDMA;
-  constexpr size_t RING = (size_t)KS * P * STAGE;
+  constexpr size_t RING = (size_t)KP * P * STAGE;
   constexpr size_t RED = sizeof(f4) * (KS - 1) * NS * NBT * 64;
   static_assert(RING <= 160 * 1024 && RED <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(16))) char smem[RING > RED ? RING : RED];
@@ -276,14 +311,14 @@ __global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint
   // activation sources (uint4 / float offsets within an item) and LDS read offsets
   int xsrc, csrc;
   uint32_t xrd, crd;
-  if constexpr (MODE == 3) {  // lane L < 16: operand L / 4 of k quarter L % 4, row 0
-    xsrc = (lane >> 2) * 64 + (lane & 3) * 16;
-    csrc = (lane & 1) ? 16 : 0;
+  if constexpr (MODE == 3) {  // compact; lane L < 16: operand L / 4 of k quarter L % 4, row 0
+    xsrc = lane;
+    csrc = (lane & 1) ? 4 : 0;
     xrd = q * 16;
     crd = 0;
-  } else if constexpr (MODE == 0) {  // lane L: operand L / 16, k quarter (L / 4) % 4, row L % 4
-    xsrc = (lane >> 4) * 64 + ((lane >> 2) & 3) * 16 + (lane & 3);
-    csrc = ((lane & 4) ? 16 : 0) + (lane & 3);
+  } else if constexpr (MODE == 0) {  // compact; lane L: operand L / 16, k quarter (L / 4) % 4, row L % 4
+    xsrc = (lane & 3) * 16 + (lane >> 4) * 4 + ((lane >> 2) & 3);
+    csrc = lane & 7;
     xrd = (q * 4 + (j & 3)) * 16;
     crd = 0;
   } else {
@@ -294,10 +329,15 @@ __global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint
   }
 
   f4 Y[NS][NBT];
+  f4 Ys[R > 1 ? R - 1 : 1][NS][NBT];  // finished ranges of this wave
 #pragma unroll
   for (int st = 0; st < NS; ++st)
 #pragma unroll
-    for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+    for (int bt = 0; bt < NBT; ++bt) {
+      Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < (R > 1 ? R - 1 : 1); ++r) Ys[r][st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+    }
 
   // stage u <- group g: exactly NDMA loads, whatever the mode's lane masks
   auto issue = [&](int g, int u) {
@@ -309,11 +349,11 @@ __global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint
     for (int bt = 0; bt < NBT; ++bt) {
       const size_t item = (size_t)g * 2 + bt;
       if constexpr (MODE == 3) {
-        if (lane < 16) dma16(XA + item * 256 + xsrc, sb + XOFF);
-        if (lane < 2) dma4(CA + item * 32 + csrc, sb + COFF);
+        if (lane < 16) dma16(XA + (size_t)g * 64 + xsrc, sb + XOFF);
+        if (lane < 2) dma4(CA + (size_t)g * 8 + csrc, sb + COFF);
       } else if constexpr (MODE == 0) {
-        dma16(XA + item * 256 + xsrc, sb + XOFF);
-        dma4(CA + item * 32 + csrc, sb + COFF);
+        dma16(XA + (size_t)g * 64 + xsrc, sb + XOFF);
+        dma4(CA + (size_t)g * 8 + csrc, sb + COFF);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) dma16(XA + item * 256 + i * 64 + xsrc, sb + XOFF + bt * 4096 + i * 1024);
@@ -359,11 +399,32 @@ __global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint
     }
   };
 
-  // groups of this wave: a contiguous range; prefetches past its end re-read
-  // the last group (an L2 hit), so every step issues NDMA loads and the wait
-  // count stays fixed
+  // groups of this wave: R consecutive ranges of `per` groups, streamed as one
+  // run; prefetches past its end re-read the last group (an L2 hit), so every
+  // step issues NDMA loads and the wait count stays fixed
   const int per = (G + KS - 1) / KS;
-  const int g0 = wave * per, g1 = min(G, g0 + per);
+  const int g0 = min(G, wave * R * per), g1 = min(G, g0 + R * per);
+  int rc = 0, rend = g0 + per;  // current range and its end
+  auto close_range = [&](int gg) {
+    if constexpr (R > 1) {
+      if (gg + 1 == rend && rc < R - 1) {
+#pragma unroll
+        for (int r = 0; r < R - 1; ++r)
+          if (r == rc) {
+#pragma unroll
+            for (int st = 0; st < NS; ++st)
+#pragma unroll
+              for (int bt = 0; bt < NBT; ++bt) Ys[r][st][bt] = Y[st][bt];
+          }
+#pragma unroll
+        for (int st = 0; st < NS; ++st)
+#pragma unroll
+          for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+        ++rc;
+        rend += per;
+      }
+    }
+  };
   if (g0 < g1) {
 #pragma unroll
     for (int u = 0; u < P; ++u) issue(min(g0 + u, g1 - 1), u);
@@ -373,6 +434,7 @@ __global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint
       for (int u = 0; u < P; ++u) {
         wait_vmcnt<NWAIT>();  // group g + u has landed; the next P - 1 stay in flight
         compute(u);
+        close_range(g + u);
         issue(min(g + u + P, g1 - 1), u);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -380,25 +442,48 @@ __global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint
     wait_vmcnt<0>();
 #pragma unroll
     for (int u = 0; u < P - 1; ++u)
-      if (g + u < g1) compute(u);
+      if (g + u < g1) {
+        compute(u);
+        close_range(g + u);
+      }
   }
 
-  // ---- split-K reduction (fixed order: wave 0 + 1 + ... + KS-1) ----
+  // ---- split-K reduction (fixed order: range 0 + 1 + ... + KS-1) ----
+  // range wave * R + r holds Ys[r] for r < rc, Y for r == rc, zero after
   wait_vmcnt<0>();
   __syncthreads();  // the reduction buffer overlays the rings
-  if (wave > 0) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int v = wave * R + r;
+    if (v == 0) continue;
 #pragma unroll
     for (int st = 0; st < NS; ++st)
 #pragma unroll
-      for (int bt = 0; bt < NBT; ++bt) red[wave - 1][st][bt][lane] = Y[st][bt];
+      for (int bt = 0; bt < NBT; ++bt) {
+        f4 val = (f4){0.f, 0.f, 0.f, 0.f};
+        if (r == rc) val = Y[st][bt];
+        if constexpr (R > 1) {
+          if (r < rc && r < R - 1) val = Ys[r < R - 1 ? r : 0][st][bt];
+        }
+        red[v - 1][st][bt][lane] = val;
+      }
   }
   __syncthreads();
   if (wave != 0) return;
-  for (int w = 0; w < KS - 1; ++w)
+  if constexpr (R > 1) {
+    // wave 0's own first range
+    if (rc > 0) {
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = Ys[0][st][bt];
+    }
+  }
+  for (int v = 0; v < KS - 1; ++v)
 #pragma unroll
     for (int st = 0; st < NS; ++st)
 #pragma unroll
-      for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[w][st][bt][lane];
+      for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[v][st][bt][lane];
 
   // ---- epilogue: lane holds weight row n for batch rows 16bt + 4q + r ----
 #pragma unroll
@@ -419,24 +504,42 @@ __global__ __launch_bounds__(64 * kKS) void a8_mma_kernel(GemvArgs a, const uint
   }
 }
 
-template <int MODE, int P, int MT, int EPI>
+template <int MODE, int KS, int KP, int P, int MT, int EPI>
 void launch_kernel(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
   const int tiles = (a.n_out + 31) / 32;
-  hipLaunchKernelGGL((a8_mma_kernel<MODE, P, MT, EPI>), dim3((tiles + MT - 1) / MT), dim3(64 * kKS), 0, s, a, XA, CA,
-                     nb);
+  hipLaunchKernelGGL((a8_mma_kernel<MODE, KS, KP, P, MT, EPI>), dim3((tiles + MT - 1) / MT), dim3(64 * KP), 0, s, a,
+                     XA, CA, nb);
+}
+
+// split of the groups: enough ranges that every matrix puts ~2000+ waves' worth
+// of work on the GPU. Depends on the shape only.
+inline int split_ranges(const GemvArgs& a) {
+  const int tiles = (a.n_out + 31) / 32;
+  return tiles >= 512 ? 4 : tiles >= 256 ? 8 : 16;
 }
 
 // one launch per chunk of up to 32 rows; the mode stages only the rows present
+// and picks waves per workgroup / ring depth within the LDS budget
+template <int KS, int EPI>
+void launch_chunk_ks(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
+  constexpr int KP4 = KS < 4 ? KS : 4, KP8 = KS < 8 ? KS : 8;
+  if (nb == 1) return launch_kernel<3, KS, KP8, 3, 1, EPI>(a, XA, CA, nb, s);
+  if (nb <= 4) return launch_kernel<0, KS, KP8, 3, 1, EPI>(a, XA, CA, nb, s);
+  if (nb <= 16) return launch_kernel<1, KS, KP4, 4, 1, EPI>(a, XA, CA, nb, s);
+  if constexpr (EPI != EPI_SWIGLU && KS <= 8) {
+    // wide matrices: two tiles per wave halve the activation traffic per weight byte
+    if ((a.n_out + 31) / 32 >= 256) return launch_kernel<2, KS, KP4, 3, 2, EPI>(a, XA, CA, nb, s);
+  }
+  launch_kernel<2, KS, KP4, 3, 1, EPI>(a, XA, CA, nb, s);
+}
+
 template <int EPI>
 void launch_chunk(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
-  if (nb == 1) return launch_kernel<3, 3, 1, EPI>(a, XA, CA, nb, s);
-  if (nb <= 4) return launch_kernel<0, 4, 1, EPI>(a, XA, CA, nb, s);
-  if (nb <= 16) return launch_kernel<1, 4, 1, EPI>(a, XA, CA, nb, s);
-  if constexpr (EPI != EPI_SWIGLU) {
-    // wide matrices: two tiles per wave halve the activation traffic per weight byte
-    if ((a.n_out + 31) / 32 >= 256) return launch_kernel<2, 3, 2, EPI>(a, XA, CA, nb, s);
+  switch (split_ranges(a)) {
+    case 4: return launch_chunk_ks<4, EPI>(a, XA, CA, nb, s);
+    case 8: return launch_chunk_ks<8, EPI>(a, XA, CA, nb, s);
+    default: return launch_chunk_ks<16, EPI>(a, XA, CA, nb, s);
   }
-  launch_kernel<2, 3, 1, EPI>(a, XA, CA, nb, s);
 }
 
 template <int EPI>
