@@ -33,6 +33,7 @@
 #include "gemv_impl.h"
 #include "quant.h"
 #include "a8_stage_reads.h"
+#include "a8_act.h"
 
 namespace pgd {
 namespace gemv {
@@ -61,61 +62,20 @@ __device__ inline h8 codes8(uint32_t w0, uint32_t w1) {
   return __builtin_bit_cast(h8, make_uint4(c0, c1, c2, c3));
 }
 
-// ---- activation prep --------------------------------------------------------
-// Rows are cut into chunks of 32 (two 16-row batch tiles). For chunk c,
-// group g, batch tile bt, item = (c * G + g) * 2 + bt:
-//   XA[item][i][lane] = 16 B, operand i = xh step 0 | xh step 1 | xl step 0 |
-//     xl step 1 (8 halves), batch row 32c + 16bt + lane % 16,
-//     k = 64g + 16(lane/16) + 8 step + e
-//   CA[item] = 32 floats: 128 * XSP for the 16 rows, then XS for the 16 rows
-// A chunk holding at most 4 rows (the decode batches of 1..4) is stored
-// compact instead, in the first part of the same region, so that one row's
-// operands are one contiguous run:
-//   X4[g][row][i][q] = 16 B (row < 4),   C4[g] = 128 * XSP[4 rows], XS[4 rows]
-// Rows past the end are never written: their MFMA rows only feed discarded
-// outputs.
-__device__ inline bool chunk_compact(int rows, int c) { return rows - 32 * c <= 4; }
-
-// the four operands of one 16-wide k slice and its partial sums
-__device__ inline void prep16(const float* v, uint4 (&o)[4], float& xs, float& xsp) {
-  uint32_t hw[8], lw[8];
-  xs = 0.0f;
-  xsp = 0.0f;
-#pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const _Float16 h0 = (_Float16)v[2 * p], h1 = (_Float16)v[2 * p + 1];
-    const _Float16 l0 = (_Float16)(v[2 * p] - (float)h0), l1 = (_Float16)(v[2 * p + 1] - (float)h1);
-    hw[p] = __builtin_bit_cast(uint32_t, (h2){h0, h1});
-    lw[p] = __builtin_bit_cast(uint32_t, (h2){l0, l1});
-    xs += v[2 * p] + v[2 * p + 1];
-    xsp += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
-  }
-  o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-  o[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-  o[2] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  o[3] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
-}
-
-// store operand i at dst[i * S]
-template <int S>
-__device__ inline void put4(uint4* dst, const uint4 (&o)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dst[i * S] = o[i];
-}
-
-__global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__ x, int ldx, int rows, int G,
-                                                       uint4* __restrict__ XA, float* __restrict__ CA) {
+// ---- activation prep (layout: a8_act.h) ----------------------------------
+// one wave per (chunk, group, batch tile); lane = 4 * row + quarter
+__global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__ x, int ldx, a8act::Dst d) {
   const size_t item = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int bt = (int)(item & 1);
   const size_t cg = item >> 1;
-  const int g = (int)(cg % G), c = (int)(cg / G);
-  if (32 * c >= rows) return;
-  const bool compact = chunk_compact(rows, c);
-  if (compact && bt) return;
-  const int row = 32 * c + 16 * bt + (lane & 15), q = lane >> 4, j = lane & 15;
+  const int g = (int)(cg % d.G), c = (int)(cg / d.G);
+  if (32 * c >= d.rows) return;
+  if (a8act::chunk_compact(d.rows, c) && bt) return;
+  const int jr = lane >> 2, q = lane & 3;
+  const int row = 32 * c + 16 * bt + jr;
   float v[16];
-  if (row < rows) {
+  if (row < d.rows) {
     const float4* xp = reinterpret_cast<const float4*>(x + (size_t)row * ldx + (g << 6) + 16 * q);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -129,25 +89,8 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = 0.0f;
   }
-  float xs, xsp;
-  uint4 o[4];
-  prep16(v, o, xs, xsp);
-  if (!compact) put4<64>(XA + item * 256 + lane, o);
-  else if (j < 4) put4<4>(XA + (size_t)c * G * 512 + ((size_t)g * 4 + j) * 16 + q, o);
-  // the four lanes of a row (q = 0..3) hold its four 16-wide k slices
-  xs += __shfl_xor(xs, 16, 64);
-  xs += __shfl_xor(xs, 32, 64);
-  xsp += __shfl_xor(xsp, 16, 64);
-  xsp += __shfl_xor(xsp, 32, 64);
-  if (q == 0) {
-    if (!compact) {
-      CA[item * 32 + j] = 128.0f * xsp;
-      CA[item * 32 + 16 + j] = xs;
-    } else if (j < 4) {
-      CA[(size_t)c * G * 64 + (size_t)g * 8 + j] = 128.0f * xsp;
-      CA[(size_t)c * G * 64 + (size_t)g * 8 + 4 + j] = xs;
-    }
-  }
+  const bool live = a8act::chunk_compact(d.rows, c) ? (jr < 4) : true;
+  a8act::emit_slice(d, row, g, q, v, live);
 }
 
 // Fused RMSNorm (rms_zero, pagoda-hf/src/qwen3_5.rs:1736-1745) + activation
@@ -157,7 +100,7 @@ constexpr int kNormMaxSlices = 8;  // n <= 256 * 16 * 8
 __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restrict__ x, int ldx,
                                                            const int* __restrict__ rows_idx, int rows, int n,
                                                            const float* __restrict__ w, float eps, float* y, int ldy,
-                                                           uint4* __restrict__ XA, float* __restrict__ CA) {
+                                                           a8act::Dst d) {
   __shared__ float red[4];
   const int r = blockIdx.x, tid = threadIdx.x;
   const int src = rows_idx ? rows_idx[r] : r;
@@ -186,13 +129,10 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)n + eps);
-  const int c = r >> 5, bt = (r >> 4) & 1, j = r & 15;
-  const bool compact = chunk_compact(rows, c);  // then r % 32 < 4
 #pragma unroll
   for (int i = 0; i < kNormMaxSlices; ++i) {
     const int u = tid + 256 * i;
     const bool live = u < slices;  // uniform per group of four lanes (slices % 4 == 0)
-    float xs = 0.0f, xsp = 0.0f;
     if (live) {
       const float4* wp = reinterpret_cast<const float4*>(w + 16 * u);
 #pragma unroll
@@ -208,28 +148,9 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
 #pragma unroll
         for (int e = 0; e < 4; ++e) yp[e] = make_float4(v[i][4 * e], v[i][4 * e + 1], v[i][4 * e + 2], v[i][4 * e + 3]);
       }
-      const int g = u >> 2, q = u & 3;
-      const size_t item = ((size_t)c * G + g) * 2 + bt;
-      uint4 o[4];
-      prep16(v[i], o, xs, xsp);
-      if (compact) put4<4>(XA + (size_t)c * G * 512 + ((size_t)g * 4 + j) * 16 + q, o);
-      else put4<64>(XA + item * 256 + q * 16 + j, o);
     }
-    // group sums over the four slices of a group (adjacent lanes)
-    xs += __shfl_xor(xs, 1, 64);
-    xs += __shfl_xor(xs, 2, 64);
-    xsp += __shfl_xor(xsp, 1, 64);
-    xsp += __shfl_xor(xsp, 2, 64);
-    if (live && (u & 3) == 0) {
-      const size_t item = ((size_t)c * G + (u >> 2)) * 2 + bt;
-      if (compact) {
-        CA[(size_t)c * G * 64 + (size_t)(u >> 2) * 8 + j] = 128.0f * xsp;
-        CA[(size_t)c * G * 64 + (size_t)(u >> 2) * 8 + 4 + j] = xs;
-      } else {
-        CA[item * 32 + j] = 128.0f * xsp;
-        CA[item * 32 + 16 + j] = xs;
-      }
-    }
+    // slice u = 4 g + q: quarter partners are adjacent lanes
+    if (i * 256 < slices) a8act::emit_slice(d, r, u >> 2, u & 3, v[i], live);
   }
 }
 
@@ -313,17 +234,17 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
   uint32_t xrd, crd;
   if constexpr (MODE == 3) {  // compact; lane L < 16: operand L / 4 of k quarter L % 4, row 0
     xsrc = lane;
-    csrc = (lane & 1) ? 4 : 0;
+    csrc = (lane & 3) * 4;
     xrd = q * 16;
     crd = 0;
   } else if constexpr (MODE == 0) {  // compact; lane L: operand L / 16, k quarter (L / 4) % 4, row L % 4
     xsrc = (lane & 3) * 16 + (lane >> 4) * 4 + ((lane >> 2) & 3);
-    csrc = lane & 7;
+    csrc = lane & 15;
     xrd = (q * 4 + (j & 3)) * 16;
     crd = 0;
   } else {
     xsrc = lane;
-    csrc = lane & 31;
+    csrc = lane;
     xrd = lane * 16;
     crd = 16 * q;
   }
@@ -350,14 +271,14 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
       const size_t item = (size_t)g * 2 + bt;
       if constexpr (MODE == 3) {
         if (lane < 16) dma16(XA + (size_t)g * 64 + xsrc, sb + XOFF);
-        if (lane < 2) dma4(CA + (size_t)g * 8 + csrc, sb + COFF);
+        if (lane < 4) dma4(CA + (size_t)g * 16 + csrc, sb + COFF);
       } else if constexpr (MODE == 0) {
         dma16(XA + (size_t)g * 64 + xsrc, sb + XOFF);
-        dma4(CA + (size_t)g * 8 + csrc, sb + COFF);
+        dma4(CA + (size_t)g * 16 + csrc, sb + COFF);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) dma16(XA + item * 256 + i * 64 + xsrc, sb + XOFF + bt * 4096 + i * 1024);
-        dma4(CA + item * 32 + csrc, sb + COFF + bt * 256);
+        dma4(CA + item * 64 + csrc, sb + COFF + bt * 256);
       }
     }
   };
@@ -367,16 +288,32 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
     uint4 W[NS];
     uint32_t S[NS];
     uint4 X[NBT][4];
-    float4 CP[NBT], XS[NBT];
+    float CPv[NBT][4], XSv[NBT][4];  // 128 XSP and XS of batch rows 16 bt + 4 q + r: half A + half B
     if constexpr (MODE == 3) {
-      float2 c1;
+      float4 c1;
       StageReads<MODE, NS>::run(base + 16 * lane, base + SBOFF + 4 * j, base + XOFF + xrd, base + COFF + crd, W, S, X,
                                 c1);
-      CP[0] = make_float4(c1.x, c1.x, c1.x, c1.x);
-      XS[0] = make_float4(c1.y, c1.y, c1.y, c1.y);
+      const float cp = c1.x + c1.y, xs = c1.z + c1.w;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        CPv[0][r] = cp;
+        XSv[0][r] = xs;
+      }
     } else {
+      float4 CC[NBT][4];
       StageReads<MODE, NS>::run(base + 16 * lane, base + SBOFF + 4 * j, base + XOFF + xrd, base + COFF + crd, W, S, X,
-                                CP, XS);
+                                CC);
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        CPv[bt][0] = CC[bt][0].x + CC[bt][1].x;
+        CPv[bt][1] = CC[bt][0].y + CC[bt][1].y;
+        CPv[bt][2] = CC[bt][0].z + CC[bt][1].z;
+        CPv[bt][3] = CC[bt][0].w + CC[bt][1].w;
+        XSv[bt][0] = CC[bt][2].x + CC[bt][3].x;
+        XSv[bt][1] = CC[bt][2].y + CC[bt][3].y;
+        XSv[bt][2] = CC[bt][2].z + CC[bt][3].z;
+        XSv[bt][3] = CC[bt][2].w + CC[bt][3].w;
+      }
     }
 #pragma unroll
     for (int st = 0; st < NS; ++st) {
@@ -391,10 +328,8 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][1]), b1, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][2]), b0, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][3]), b1, Pm, 0, 0, 0);
-        const float cpa[4] = {CP[bt].x, CP[bt].y, CP[bt].z, CP[bt].w};
-        const float xsa[4] = {XS[bt].x, XS[bt].y, XS[bt].z, XS[bt].w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(bi, xsa[r], fmaf(sc, Pm[r] + cpa[r], Y[st][bt][r]));
+        for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(bi, XSv[bt][r], fmaf(sc, Pm[r] + CPv[bt][r], Y[st][bt][r]));
       }
     }
   };
@@ -551,7 +486,7 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   for (int c = 0; rows > 0; ++c) {
     const int nb = rows < 32 ? rows : 32;
     const uint4* xa = XA + (size_t)c * G * 2 * 256;
-    const float* ca = act.CA + (size_t)c * G * 2 * 32;
+    const float* ca = act.CA + (size_t)c * G * 2 * 64;
     launch_chunk<EPI>(a, xa, ca, nb, s);
     PGD_HIP(hipGetLastError());
     rows -= nb;
@@ -571,18 +506,20 @@ void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s) {
 }  // namespace gemv
 
 size_t a8_act_bytes(int rows, int K) {
-  const size_t chunks = ((size_t)rows + 31) / 32, G = (size_t)K / 64;
-  return chunks * G * 2 * (64 * 64 + 32 * 4);
+  return a8act::xa_bytes(rows, K / 64) + a8act::ca_bytes(rows, K / 64);
 }
 
 A8Act a8_act_view(void* buf, int rows, int K) {
-  const size_t chunks = ((size_t)rows + 31) / 32, G = (size_t)K / 64;
   A8Act a;
   a.XA = buf;
-  a.CA = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(buf) + chunks * G * 2 * 64 * 64);
+  a.CA = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(buf) + a8act::xa_bytes(rows, K / 64));
   a.rows = rows;
   a.K = K;
   return a;
+}
+
+a8act::Dst a8_act_dst(const A8Act& a) {
+  return a8act::Dst{reinterpret_cast<uint4*>(const_cast<void*>(a.XA)), const_cast<float*>(a.CA), a.rows, a.K / 64};
 }
 
 A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream_t s) {
@@ -590,8 +527,7 @@ A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream
   A8Act a = a8_act_view(buf, rows, K);
   if (rows <= 0) return a;
   const size_t items = ((size_t)rows + 31) / 32 * (K / 64) * 2;
-  hipLaunchKernelGGL(gemv::a8_xprep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, x, ldx, rows, K / 64,
-                     reinterpret_cast<uint4*>(buf), const_cast<float*>(a.CA));
+  hipLaunchKernelGGL(gemv::a8_xprep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, x, ldx, a8_act_dst(a));
   PGD_HIP(hipGetLastError());
   return a;
 }
@@ -602,7 +538,7 @@ A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n
   A8Act a = a8_act_view(buf, rows, n);
   if (rows <= 0) return a;
   hipLaunchKernelGGL(gemv::a8_norm_prep_kernel, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx, rows, n, w, eps, y,
-                     ldy, reinterpret_cast<uint4*>(buf), const_cast<float*>(a.CA));
+                     ldy, a8_act_dst(a));
   PGD_HIP(hipGetLastError());
   return a;
 }

@@ -2,6 +2,7 @@
 // preparation with paged KV writes, paged GQA decode attention and argmax.
 #include "common.h"
 #include "ops.h"
+#include "gemv_impl.h"
 
 namespace pgd {
 
@@ -360,46 +361,72 @@ __device__ inline bool better(float v, int i, float bv, int bi, int last_max) {
   return last_max ? i > bi : i < bi;
 }
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int ld, int n, int last_max,
-                                                      uint32_t* ids, float* vals, int* nonfinite) {
-  __shared__ float sv[1024];
-  __shared__ int si[1024];
-  __shared__ int snf[1024];
-  const int r = blockIdx.x, tid = threadIdx.x;
+// Row argmax in two passes: kArgChunks workgroups per row each reduce one
+// contiguous chunk, then one wave per row merges the chunk winners. better()
+// is a total order on (value, index), so the merge order does not matter.
+constexpr int kArgChunks = 64;
+struct ArgPart {
+  float v;
+  int i, nf;
+};
+
+__device__ inline void arg_merge(float& bv, int& bi, int& nf, float v, int i, int n2, int last_max) {
+  if (i >= 0 && better(v, i, bv, bi, last_max)) {
+    bv = v;
+    bi = i;
+  }
+  nf += n2;
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float* __restrict__ x, int ld, int n, int last_max,
+                                                          ArgPart* __restrict__ part) {
+  __shared__ ArgPart sp[4];
+  const int r = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
+  const int len = (n + kArgChunks - 1) / kArgChunks;
+  const int lo = b * len, hi = min(n, lo + len);
   const float* xr = x + (size_t)r * ld;
   float bv = -INFINITY;
   int bi = -1, nf = 0;
-  for (int i = tid; i < n; i += 1024) {
+  for (int i = lo + tid; i < hi; i += 256) {
     const float v = xr[i];
-    if (!isfinite(v)) {
-      nf++;
-      continue;
-    }
-    if (better(v, i, bv, bi, last_max)) {
+    if (!isfinite(v)) nf++;
+    else if (better(v, i, bv, bi, last_max)) {
       bv = v;
       bi = i;
     }
   }
-  sv[tid] = bv;
-  si[tid] = bi;
-  snf[tid] = nf;
-  __syncthreads();
-  for (int s = 512; s > 0; s >>= 1) {
-    if (tid < s) {
-      const float v = sv[tid + s];
-      const int i = si[tid + s];
-      if (i >= 0 && better(v, i, sv[tid], si[tid], last_max)) {
-        sv[tid] = v;
-        si[tid] = i;
-      }
-      snf[tid] += snf[tid + s];
-    }
-    __syncthreads();
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(bv, o, 64);
+    const int i = __shfl_xor(bi, o, 64);
+    const int f = __shfl_xor(nf, o, 64);
+    arg_merge(bv, bi, nf, v, i, f, last_max);
   }
+  if ((tid & 63) == 0) sp[tid >> 6] = ArgPart{bv, bi, nf};
+  __syncthreads();
   if (tid == 0) {
-    ids[r] = si[0] < 0 ? 0xFFFFFFFFu : (uint32_t)si[0];
-    if (vals) vals[r] = sv[0];
-    if (nonfinite) nonfinite[r] = snf[0];
+    for (int w = 1; w < 4; ++w) arg_merge(bv, bi, nf, sp[w].v, sp[w].i, sp[w].nf, last_max);
+    part[(size_t)r * kArgChunks + b] = ArgPart{bv, bi, nf};
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const ArgPart* __restrict__ part, int last_max,
+                                                          uint32_t* ids, float* vals, int* nonfinite) {
+  const int r = blockIdx.x, lane = threadIdx.x;
+  ArgPart p = part[(size_t)r * kArgChunks + lane];
+  float bv = p.v;
+  int bi = p.i, nf = p.nf;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(bv, o, 64);
+    const int i = __shfl_xor(bi, o, 64);
+    const int f = __shfl_xor(nf, o, 64);
+    arg_merge(bv, bi, nf, v, i, f, last_max);
+  }
+  if (lane == 0) {
+    ids[r] = bi < 0 ? 0xFFFFFFFFu : (uint32_t)bi;
+    if (vals) vals[r] = bv;
+    if (nonfinite) nonfinite[r] = nf;
   }
 }
 
@@ -476,7 +503,10 @@ void attn_decode(const float* q, const float* gate, float* out, const AttnLayout
 void argmax_rows(const float* x, int ld, int rows, int n, int last_max, uint32_t* ids, float* vals, int* nonfinite,
                  hipStream_t s) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(1024), 0, s, x, ld, n, last_max, ids, vals, nonfinite);
+  static_assert(kArgChunks == 64, "one wave merges the chunks");
+  auto* part = static_cast<ArgPart*>(gemv::gemv_scratch(s, (size_t)rows * kArgChunks * sizeof(ArgPart)));
+  hipLaunchKernelGGL(argmax_part_kernel, dim3(kArgChunks, rows), dim3(256), 0, s, x, ld, n, last_max, part);
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(rows), dim3(64), 0, s, part, last_max, ids, vals, nonfinite);
   PGD_HIP(hipGetLastError());
 }
 

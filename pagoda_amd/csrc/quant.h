@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "a8_act.h"
+
 namespace pgd {
 
 enum Fmt : int { FMT_A8 = 0, FMT_Q4K = 1, FMT_Q6K = 2 };
@@ -87,6 +89,8 @@ struct A8Act {
 };
 size_t a8_act_bytes(int rows, int K);
 A8Act a8_act_view(void* buf, int rows, int K);
+// destination descriptor for kernels that write prepared activations directly
+a8act::Dst a8_act_dst(const A8Act& a);
 // from f32 rows x [rows, ldx]
 A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream_t s);
 // fused RMSNorm (x * rsqrt(mean x^2 + eps) * w) + prep; y (nullable) also
