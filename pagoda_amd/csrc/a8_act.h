@@ -87,16 +87,17 @@ __device__ inline void put_half(const Dst& d, int row, int g, int half, float xs
   }
 }
 
-// One 16-wide slice (k = 64 g + 16 q ...) of `row`. The lanes holding
-// quarters q ^ 1 of the same (row, g) must be lane ^ 1 of the same wave and
+// One 16-wide slice (k = 64 g + 16 q ...) of `row`. The lane holding quarter
+// q ^ 1 of the same (row, g) must be lane ^ PARTNER of the same wave and
 // execute this call together (the two quarters of a half are summed with one
-// XOR-1 shuffle, the lower quarter first).
+// XOR shuffle; fp addition commutes, so both lanes get the same sum).
+template <int PARTNER = 1>
 __device__ inline void emit_slice(const Dst& d, int row, int g, int q, const float (&v)[16], bool live) {
   uint4 o[4];
   float xs, xsp;
   prep16(v, o, xs, xsp);
-  xs += __shfl_xor(xs, 1, 64);
-  xsp += __shfl_xor(xsp, 1, 64);
+  xs += __shfl_xor(xs, PARTNER, 64);
+  xsp += __shfl_xor(xsp, PARTNER, 64);
   if (!live) return;
   put_operands(d, row, g, q, o);
   if ((q & 1) == 0) put_half(d, row, g, q >> 1, xs, xsp);

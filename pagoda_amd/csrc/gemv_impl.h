@@ -43,6 +43,10 @@ struct GemvArgs {
   int ldy;
   const float* res;
   int ldres;
+  // SwiGLU only: also write the product as prepared A8 activations (XA null:
+  // no); row0 = first row of this launch within that activation
+  a8act::Dst oact;
+  int row0;
 };
 
 enum { EPI_STORE = 0, EPI_RES = 1, EPI_SWIGLU = 2 };

@@ -421,6 +421,32 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
       for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[v][st][bt][lane];
 
   // ---- epilogue: lane holds weight row n for batch rows 16bt + 4q + r ----
+  if constexpr (DUAL) {
+    if (a.oact.XA) {
+      // the tile's 32 products of each batch row are one half of group
+      // tile / 2 of the down projection's input: transpose through LDS, then
+      // lane L prepares 16 of them (row L % 32, quarter pair L / 32)
+      float* hb = reinterpret_cast<float*>(smem);  // [32][33]
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int b = 16 * bt + 4 * q + r;
+            if (b < nb) hb[b * 33 + 16 * st + j] = silu_f(Y[st][bt][r]) * Y[2 + st][bt][r];
+          }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int b = lane & 31, st = lane >> 5;
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = b < nb ? hb[b * 33 + 16 * st + e] : 0.0f;
+      a8act::emit_slice<32>(a.oact, a.row0 + b, blockIdx.x >> 1, (blockIdx.x & 1) * 2 + st, v, b < nb);
+      if (!a.y) return;
+    }
+  }
 #pragma unroll
   for (int st = 0; st < (DUAL ? 2 : NS); ++st) {
     const int n = (blockIdx.x * MT + (DUAL ? 0 : st >> 1)) * 32 + 16 * (st & 1) + j;
@@ -490,8 +516,9 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
     launch_chunk<EPI>(a, xa, ca, nb, s);
     PGD_HIP(hipGetLastError());
     rows -= nb;
-    a.y += (size_t)nb * a.ldy;
+    if (a.y) a.y += (size_t)nb * a.ldy;
     if (a.res) a.res += (size_t)nb * a.ldres;
+    a.row0 += nb;
   }
 }
 

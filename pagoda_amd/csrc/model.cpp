@@ -263,7 +263,8 @@ namespace {
 
 struct Ws {
   float *x, *xn, *A, *B, *C0, *C1, *D, *E, *F, *G, *logits;
-  void* act;  // prepared A8 activation operands
+  void* act;   // prepared A8 activation operands
+  void* act2;  // second set: the SwiGLU product feeding the down projection
   size_t lda, ldb, ldd, lde;
 };
 
@@ -275,14 +276,15 @@ Ws carve_ws(Model& m, int rows, int lrows) {
   size_t ldc = std::max<size_t>(align_up(std::max(c.v_heads, 1), 8), m.kv_width);
   size_t ldd = std::max<size_t>(m.conv_dim, (size_t)c.heads * c.head_dim);
   size_t lde = std::max<size_t>(m.value_dim, (size_t)c.heads * c.head_dim);
-  size_t act_floats = 0;
+  size_t act_floats = 0, act2_floats = 0;
   if (c.arch == PGD_ARCH_QWEN35) {
     int kmax = std::max(std::max(c.hidden, c.intermediate), std::max(m.value_dim, c.heads * c.head_dim));
     act_floats = (a8_act_bytes(rows, kmax) + 3) / 4;
+    act2_floats = (a8_act_bytes(rows, c.intermediate) + 3) / 4;
   }
   size_t sizes[] = {rows * H, rows * H, rows * lda, rows * ldb, rows * ldc, rows * ldc, rows * ldd, rows * lde,
                     rows * (size_t)c.heads * c.head_dim, rows * (size_t)c.intermediate, (size_t)lrows * c.vocab,
-                    act_floats};
+                    act_floats, act2_floats};
   size_t total = 0;
   for (size_t v : sizes) total += align_up(v, 64);
   if (m.ws.bytes < total * 4) {
@@ -290,13 +292,13 @@ Ws carve_ws(Model& m, int rows, int lrows) {
     m.ws = DevBuf(total * 4);
   }
   float* p = m.ws.as<float>();
-  float* ptrs[12];
-  for (int i = 0; i < 12; ++i) {
+  float* ptrs[13];
+  for (int i = 0; i < 13; ++i) {
     ptrs[i] = p;
     p += align_up(sizes[i], 64);
   }
   Ws w{ptrs[0], ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], ptrs[6], ptrs[7], ptrs[8], ptrs[9], ptrs[10],
-       (void*)ptrs[11], lda, ldb, ldd, lde};
+       (void*)ptrs[11], (void*)ptrs[12], lda, ldb, ldd, lde};
   return w;
 }
 
@@ -473,12 +475,13 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       gp.a_log = L.a_log;
       gp.dt_bias = L.dt_bias;
       gp.norm = L.gnorm;
-      gp.out = w.E;
-      gp.ld_out = (int)w.lde;
+      // the gated norm writes the out projection's operands itself
+      const A8Act act = a8_act_view(w.act, rows, m.value_dim);
+      gp.out = nullptr;
+      gp.act = a8_act_dst(act);
       gp.state_base = d_sb;
       gp.state_off = (size_t)L.lin_index * per_lin + m.conv_floats;
       gdn_step(gp, sm, nseq, st);
-      A8Act act = a8_act_prep(w.E, (int)w.lde, rows, m.value_dim, w.act, st);
       qmat_gemv_a8(L.out, act, w.x, H, w.x, H, st);
     } else {
       AttnLayout al{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.kv_block, L.k_pool, L.v_pool};
@@ -497,20 +500,24 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       qp.q = w.D;
       qp.gate = w.F;
       qkv_prep(qp, al, rm, rows, st);
-      attn_decode(w.D, hybrid ? w.F : nullptr, w.E, al, rm, rows, st);
       if (hybrid) {
-        A8Act act = a8_act_prep(w.E, c.heads * c.head_dim, rows, c.heads * c.head_dim, w.act, st);
+        // attention writes the o projection's operands itself
+        const A8Act act = a8_act_view(w.act, rows, c.heads * c.head_dim);
+        const a8act::Dst dst = a8_act_dst(act);
+        attn_decode(w.D, w.F, nullptr, al, rm, rows, st, &dst);
         qmat_gemv_a8(L.o, act, w.x, H, w.x, H, st);
       } else {
+        attn_decode(w.D, nullptr, w.E, al, rm, rows, st);
         qmat_gemv(L.o, w.E, 0, c.heads * c.head_dim, rows, w.x, H, w.x, H, st);
       }
     }
     // ---- SwiGLU MLP ----
     if (hybrid) {
       A8Act act = a8_norm_prep(w.x, H, nullptr, rows, H, L.post_norm, eps, nullptr, 0, w.act, st);
-      qmat_gemv_a8_swiglu(L.gate, L.up, act, w.G, c.intermediate, st);
-      A8Act act2 = a8_act_prep(w.G, c.intermediate, rows, c.intermediate, w.act, st);
-      qmat_gemv_a8(L.down, act2, w.x, H, w.x, H, st);
+      // the SwiGLU epilogue writes the down projection's operands itself
+      const A8Act mid = a8_act_view(w.act2, rows, c.intermediate);
+      qmat_gemv_a8_swiglu(L.gate, L.up, act, nullptr, 0, st, &mid);
+      qmat_gemv_a8(L.down, mid, w.x, H, w.x, H, st);
     } else {
       rmsnorm_rows(w.x, H, nullptr, rows, H, L.post_norm, eps, norm_mode, w.xn, H, st);
       qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);

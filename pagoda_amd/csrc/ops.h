@@ -5,6 +5,7 @@
 // [row_start[s], row_start[s] + row_count[s]) in feed order.
 #pragma once
 
+#include "a8_act.h"
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -41,8 +42,9 @@ struct GdnParams {
   const float* a_log;    // [v_heads]
   const float* dt_bias;  // [v_heads]
   const float* norm;     // [v_dim]
-  float* out;            // [rows, v_heads*v_dim]
+  float* out;            // [rows, v_heads*v_dim] (nullable when act is set)
   int ld_out;
+  a8act::Dst act;        // the same output as prepared A8 activations (XA null: no)
   float* const* state_base;  // per sequence; state at state_base[s] + state_off, [v_heads, k_dim, v_dim]
   size_t state_off;
 };
@@ -99,7 +101,7 @@ void qkv_prep(const QkvPrep& p, const AttnLayout& L, const RowMeta& m, int rows,
 // of its sequence. out [rows, heads, hd]; gate (nullable) multiplies by
 // sigmoid(gate) (qwen3_5.rs:1433-1475; qwen2_gguf.rs:252-266).
 void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
-                 hipStream_t s);
+                 hipStream_t s, const a8act::Dst* act = nullptr);
 
 // Row-wise argmax over finite values. last_max = 0: first index among equal
 // maxima (pagoda/src/sampler.rs:59-69); 1: last (Iterator::max_by,

@@ -91,6 +91,7 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
   __shared__ float qs[D], ks[D], delta[D];
   __shared__ float red[8][D];
   __shared__ float part[4];
+  __shared__ float obuf[D];
   const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
   const int cg = tid & 31, rg = tid >> 5;
   const int repeat = p.v_heads / p.k_heads;
@@ -179,7 +180,17 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
     if (tid < D) {
       const float inv = 1.0f / sqrtf((part[0] + part[1]) / (float)D + 1e-6f);
       const float zg = p.z[(size_t)row * p.ld_z + h * D + tid];
-      p.out[(size_t)row * p.ld_out + h * D + tid] = o * inv * p.norm[tid] * (zg / (1.0f + expf(-zg)));
+      const float val = o * inv * p.norm[tid] * (zg / (1.0f + expf(-zg)));
+      if (p.out) p.out[(size_t)row * p.ld_out + h * D + tid] = val;
+      obuf[tid] = val;
+    }
+    __syncthreads();
+    if (p.act.XA && tid < D / 16) {
+      // the head's 128 outputs are two whole groups of the out projection's input
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = obuf[16 * tid + e];
+      a8act::emit_slice(p.act, row, (h * D + 16 * tid) >> 6, tid & 3, v, true);
     }
     __syncthreads();
   }
@@ -265,12 +276,13 @@ __global__ __launch_bounds__(64) void qkv_prep_kernel(QkvPrep p, AttnLayout L, R
 // an online softmax per q head of the GQA group; groups are merged in LDS.
 template <int HD, int G>
 __global__ __launch_bounds__(256) void attn_kernel(const float* __restrict__ q, const float* __restrict__ gate,
-                                                   float* __restrict__ out, AttnLayout L, RowMeta m) {
+                                                   float* __restrict__ out, AttnLayout L, RowMeta m, a8act::Dst act) {
   constexpr int LP = HD / 4;
   constexpr int PPW = 64 / LP;
   constexpr int NG = 4 * PPW;  // position groups per workgroup
   __shared__ float s_m[NG][G], s_l[NG][G];
   __shared__ float4 s_acc[NG][G][LP];
+  __shared__ __attribute__((aligned(16))) float obuf[G * HD];
   const int kvh = blockIdx.x, r = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave * PPW + lane / LP;  // position group
@@ -347,7 +359,21 @@ __global__ __launch_bounds__(256) void attn_kernel(const float* __restrict__ q, 
       res.z *= 1.0f / (1.0f + expf(-gg.z));
       res.w *= 1.0f / (1.0f + expf(-gg.w));
     }
-    *reinterpret_cast<float4*>(out + oo) = res;
+    if (out) *reinterpret_cast<float4*>(out + oo) = res;
+    if (act.XA) *reinterpret_cast<float4*>(&obuf[g * HD + 4 * sl]) = res;
+  }
+  if (act.XA) {
+    // the group's G heads are whole groups of the o projection's input
+    __syncthreads();
+    constexpr int SL = G * HD / 16;
+    for (int u0 = 0; u0 < SL; u0 += 256) {
+      const int u = u0 + tid;
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = u < SL ? obuf[16 * u + e] : 0.0f;
+      const int col = kvh * G * HD + 16 * u;
+      a8act::emit_slice(act, r, col >> 6, (col >> 4) & 3, v, u < SL);
+    }
   }
 }
 
@@ -473,28 +499,31 @@ void qkv_prep(const QkvPrep& p, const AttnLayout& L, const RowMeta& m, int rows,
 
 template <int HD>
 static void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
-                    hipStream_t s) {
+                    hipStream_t s, const a8act::Dst& act) {
   const int G = L.heads / L.kv_heads;
   dim3 grid(L.kv_heads, rows);
   switch (G) {
-    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
-    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
-    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
-    case 6: hipLaunchKernelGGL((attn_kernel<HD, 6>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
-    case 7: hipLaunchKernelGGL((attn_kernel<HD, 7>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
-    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, s, q, gate, out, L, m); break;
+    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
+    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
+    case 6: hipLaunchKernelGGL((attn_kernel<HD, 6>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
+    case 7: hipLaunchKernelGGL((attn_kernel<HD, 7>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
+    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
     default: throw Error{kErrShape, "unsupported GQA group size " + std::to_string(G)};
   }
 }
 
 void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
-                 hipStream_t s) {
+                 hipStream_t s, const a8act::Dst* act) {
   PGD_CHECK(L.kv_heads > 0 && L.heads % L.kv_heads == 0, kErrShape, "heads must be a multiple of kv_heads");
+  PGD_CHECK(out || act, kErrArg, "attention needs an output");
   if (rows <= 0) return;
+  const a8act::Dst d = act ? *act : a8act::Dst{nullptr, nullptr, 0, 0};
+  if (act) PGD_CHECK(act->G * 64 == L.heads * L.head_dim && act->rows == rows, kErrShape, "prepared attention output");
   switch (L.head_dim) {
-    case 64: attn_hd<64>(q, gate, out, L, m, rows, s); break;
-    case 128: attn_hd<128>(q, gate, out, L, m, rows, s); break;
-    case 256: attn_hd<256>(q, gate, out, L, m, rows, s); break;
+    case 64: attn_hd<64>(q, gate, out, L, m, rows, s, d); break;
+    case 128: attn_hd<128>(q, gate, out, L, m, rows, s, d); break;
+    case 256: attn_hd<256>(q, gate, out, L, m, rows, s, d); break;
     default: throw Error{kErrShape, "attention head_dim must be 64, 128 or 256"};
   }
   PGD_HIP(hipGetLastError());

@@ -98,7 +98,10 @@ A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream
 A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps, float* y,
                    int ldy, void* buf, hipStream_t s);
 void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const float* res, int ldres, hipStream_t s);
-void qmat_gemv_a8_swiglu(const QMat& gate, const QMat& up, const A8Act& act, float* mid, int ldm, hipStream_t s);
+// mid (nullable when mid_act is given): silu(gate x) * (up x) in f32;
+// mid_act (nullable): the same product written as prepared activations
+void qmat_gemv_a8_swiglu(const QMat& gate, const QMat& up, const A8Act& act, float* mid, int ldm, hipStream_t s,
+                         const A8Act* mid_act = nullptr);
 
 // embedding rows: out[r, :] = dequant(W[ids[r], :]) (ids on device)
 void qmat_embed(const QMat& m, const uint32_t* ids, int nrows, float* out, int ldo, hipStream_t s);

@@ -533,15 +533,22 @@ void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const floa
   run_a8_mma(a, act, res ? EPI_RES : EPI_STORE, s);
 }
 
-void qmat_gemv_a8_swiglu(const QMat& gate, const QMat& up, const A8Act& act, float* mid, int ldm, hipStream_t s) {
+void qmat_gemv_a8_swiglu(const QMat& gate, const QMat& up, const A8Act& act, float* mid, int ldm, hipStream_t s,
+                         const A8Act* mid_act) {
   PGD_CHECK(gate.fmt == FMT_A8 && up.fmt == FMT_A8 && gate.n_out == up.n_out && gate.n_in == up.n_in, kErrShape,
             "swiglu gate/up shapes differ");
+  PGD_CHECK(mid || mid_act, kErrArg, "swiglu needs an output");
   if (act.rows <= 0) return;
   GemvArgs a = make_args(gate);
   a.u0 = up.p0;
   a.u1 = up.p1;
   a.y = mid;
   a.ldy = ldm;
+  if (mid_act) {
+    PGD_CHECK(gate.n_out % 64 == 0 && mid_act->K == gate.n_out && mid_act->rows == act.rows, kErrShape,
+              "prepared SwiGLU output needs n_out % 64 == 0 and matching rows");
+    a.oact = a8_act_dst(*mid_act);
+  }
   run_a8_mma(a, act, EPI_SWIGLU, s);
 }
 
