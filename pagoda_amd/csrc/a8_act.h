@@ -8,12 +8,12 @@
 //   XA[item][i][lane] = 16 B: operand i = xh step 0 | xh step 1 | xl step 0 |
 //     xl step 1 (8 halves), batch row 32c + 16bt + lane % 16,
 //     k = 64g + 16(lane / 16) + 8 step + e, with xh = f16(x), xl = f16(x - xh)
-//   CA[item][64] = 128 XSP_A[16] | 128 XSP_B[16] | XS_A[16] | XS_B[16]
+//   CA[item][64] = -1024 XSP_A[16] | -1024 XSP_B[16] | XS_A[16] | XS_B[16]
 // where A sums k quarters 0-1 of the group and B quarters 2-3, XS = sum x and
 // XSP = sum (xh + xl) (the consumer adds A + B, which is the same sum as over
 // the four quarters in order). A chunk of at most 4 rows (decode batches
 // 1..4) is stored compact instead, at the start of the same region:
-//   X4[g][row][i][q] = 16 B (row < 4),   C4[g][16] = 128 XSP_A[4] | 128 XSP_B[4] | XS_A[4] | XS_B[4]
+//   X4[g][row][i][q] = 16 B (row < 4),   C4[g][16] = -1024 XSP_A[4] | -1024 XSP_B[4] | XS_A[4] | XS_B[4]
 // so that one row's operands are one contiguous 256 B run. Rows past the end
 // are never written: their MFMA rows only feed discarded outputs.
 #pragma once
@@ -77,12 +77,12 @@ __device__ inline void put_half(const Dst& d, int row, int g, int half, float xs
   const int c = row >> 5;
   if (chunk_compact(d.rows, c)) {
     float* p = d.CA + (size_t)c * d.G * 128 + (size_t)g * 16 + half * 4 + (row & 31);
-    p[0] = 128.0f * xsp;
+    p[0] = -1024.0f * xsp;
     p[8] = xs;
   } else {
     const size_t item = ((size_t)c * d.G + g) * 2 + ((row >> 4) & 1);
     float* p = d.CA + item * 64 + half * 16 + (row & 15);
-    p[0] = 128.0f * xsp;
+    p[0] = -1024.0f * xsp;
     p[32] = xs;
   }
 }

@@ -312,7 +312,10 @@ void run_q4k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 void run_q6k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 // Per-stream device scratch for GEMV activation prep (grows, never shrinks;
 // growing drains the stream first).
-void* gemv_scratch(hipStream_t s, size_t bytes);
+// per-stream device scratch that grows on demand (the stream is synchronized
+// before a buffer is replaced). Slots are independent buffers: 0 for prepared
+// activations and small reductions, 1 for split-K partial sums.
+void* gemv_scratch(hipStream_t s, size_t bytes, int slot = 0);
 // A8 on the matrix cores (f32 activations)
 void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s);
 

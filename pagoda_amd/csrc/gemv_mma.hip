@@ -2,10 +2,12 @@
 //
 // Y[b, n] = sum_k x[b, k] * (s[n, g] * c[n, k] + bias[n, g]),  g = k / 64,
 // for up to 32 batch rows per launch, in two 16-row batch tiles. Per group:
-//   P[b, n] = sum_k (c[n,k] - 128) * (xh[b,k] + xl[b,k])     4 x v_mfma_f32_16x16x32_f16
-//   Y[b, n] += s[n,g] * (P[b, n] + 128 * XSP[b,g]) + bias[n,g] * XS[b,g]
-// xh = f16(x) and xl = f16(x - xh) carry x to ~22 bits, codes - 128 are
-// exact in f16, XS = sum x and XSP = sum (xh + xl) over the group in f32.
+//   P[b, n] = sum_k (1024 + c[n,k]) * (xh[b,k] + xl[b,k])    4 x v_mfma_f32_16x16x32_f16
+//   Y[b, n] += s[n,g] * (P[b, n] - 1024 * XSP[b,g]) + bias[n,g] * XS[b,g]
+// xh = f16(x) and xl = f16(x - xh) carry x to ~22 bits; 1024 + c is exact in
+// f16 and is what one byte permute makes of a code; XS = sum x and XSP =
+// sum (xh + xl) over the group in f32 (the subtraction cancels the offset to
+// ~1e-6 of the group's sum).
 // The batch row is the MFMA's M index and the weight row its N index: a lane
 // owns one weight row (one scale/bias per group) and four batch rows. Every
 // batch row goes through the same instruction sequence and the same split of
@@ -46,13 +48,9 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 // four codes (one u32) -> two f16 pairs holding (code - 128)
 __device__ inline void codes_to_h(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  // bytes [c, 0x64] form the f16 1024 + c; subtracting 1152 leaves c - 128
-  const uint32_t a = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);
-  const uint32_t b = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);
-  const h2 ha = __builtin_bit_cast(h2, a) - (h2){(_Float16)1152.0f, (_Float16)1152.0f};
-  const h2 hb = __builtin_bit_cast(h2, b) - (h2){(_Float16)1152.0f, (_Float16)1152.0f};
-  lo = __builtin_bit_cast(uint32_t, ha);
-  hi = __builtin_bit_cast(uint32_t, hb);
+  // bytes [c, 0x64] form the f16 1024 + c
+  lo = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);
+  hi = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);
 }
 
 __device__ inline h8 codes8(uint32_t w0, uint32_t w1) {
@@ -192,11 +190,13 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
   constexpr int R = KS / KP;
   constexpr int NBT = Geo::NBT;
   constexpr bool DUAL = EPI == EPI_SWIGLU;
-  static_assert(!DUAL || MT == 1, "SwiGLU pairs the gate and up subtiles of one tile");
-  constexpr int NS = DUAL ? 4 : 2 * MT;  // 16-row weight subtiles per wave
-  constexpr int SBOFF = NS * 1024, XOFF = SBOFF + (MODE == 3 ? NS * 64 : 256), COFF = XOFF + Geo::XB;
+  constexpr int NSM = 2 * MT;              // 16-row subtiles per matrix (MT 32-row tiles)
+  constexpr int NS = DUAL ? 2 * NSM : NSM;  // subtiles per wave; SwiGLU: gate ones, then up ones
+  constexpr int SBD = (NS + 3) / 4;         // scale/bias loads per group (16 rows x 4 subtiles each)
+  static_assert(MODE == 2 || NS <= 4, "wide waves only with 32-row launches");
+  constexpr int SBOFF = NS * 1024, XOFF = SBOFF + (MODE == 3 ? NS * 64 : SBD * 256), COFF = XOFF + Geo::XB;
   constexpr int STAGE = COFF + Geo::CB;
-  constexpr int NDMA = NS + 1 + Geo::KX;  // loads per group
+  constexpr int NDMA = NS + SBD + Geo::KX;  // loads per group
   constexpr int NWAIT = (P - 1) * NDMA;
   constexpr size_t RING = (size_t)KP * P * STAGE;
   constexpr size_t RED = sizeof(f4) * (KS - 1) * NS * NBT * 64;
@@ -211,23 +211,29 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
   char* ring = smem + (size_t)wave * P * STAGE;
   const uint32_t ring_lds = lds_addr(ring);
 
+  // subtile st: matrix (gate / up), tile, row within the tile
+  auto sub_src = [&](int st, const uint8_t* g0p, const uint8_t* u0p, int& tile, int& r) -> const uint8_t* {
+    const int sl = DUAL ? st % NSM : st;
+    // a missing last tile re-reads the last real one; its outputs are dropped
+    tile = min(blockIdx.x * MT + (sl >> 1), ntiles - 1);
+    r = 16 * (sl & 1) + j;
+    return (DUAL && st >= NSM) ? u0p : g0p;
+  };
   // weights: each lane stages (and later reads back) its own 16 B of each subtile
   const uint8_t* wsrc[NS];
 #pragma unroll
   for (int st = 0; st < NS; ++st) {
-    const uint8_t* p = (DUAL && st >= 2) ? a.u0 : a.p0;
-    // a missing second tile re-reads the last one; its outputs are dropped
-    const int tile = min(blockIdx.x * MT + (DUAL ? 0 : st >> 1), ntiles - 1);
-    const int r = 16 * (st & 1) + j;
+    int tile, r;
+    const uint8_t* p = sub_src(st, a.p0, a.u0, tile, r);
     wsrc[st] = p + ((size_t)tile * G << 11) + (q >> 1) * 1024 + r * 32 + (q & 1) * 16;
   }
-  // scale/bias: lane L stages subtile min(L / 16, NS - 1), row L % 16
-  const uint32_t* ssrc;
-  {
-    const int st = min(lane >> 4, NS - 1);
-    const uint8_t* ps = (DUAL && st >= 2) ? a.u1 : a.p1;
-    const int tile = min(blockIdx.x * MT + (DUAL ? 0 : st >> 1), ntiles - 1);
-    ssrc = reinterpret_cast<const uint32_t*>(ps) + ((size_t)tile * G << 5) + 16 * (st & 1) + j;
+  // scale/bias: load d, lane L stages subtile min(4 d + L / 16, NS - 1), row L % 16
+  const uint32_t* ssrc[SBD];
+#pragma unroll
+  for (int d = 0; d < SBD; ++d) {
+    int tile, r;
+    const uint8_t* ps = sub_src(min(4 * d + (lane >> 4), NS - 1), a.p1, a.u1, tile, r);
+    ssrc[d] = reinterpret_cast<const uint32_t*>(ps) + ((size_t)tile * G << 5) + r;
   }
   // activation sources (uint4 / float offsets within an item) and LDS read offsets
   int xsrc, csrc;
@@ -265,7 +271,9 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
     char* sb = ring + u * STAGE;
 #pragma unroll
     for (int st = 0; st < NS; ++st) dma16(wsrc[st] + ((size_t)g << 11), sb + st * 1024);
-    if (MODE != 3 || lane < 16 * NS) dma4(ssrc + ((size_t)g << 5), sb + SBOFF);
+#pragma unroll
+    for (int d = 0; d < SBD; ++d)
+      if (MODE != 3 || lane < 16 * NS) dma4(ssrc[d] + ((size_t)g << 5), sb + SBOFF + d * 256);
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) {
       const size_t item = (size_t)g * 2 + bt;
@@ -288,7 +296,7 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
     uint4 W[NS];
     uint32_t S[NS];
     uint4 X[NBT][4];
-    float CPv[NBT][4], XSv[NBT][4];  // 128 XSP and XS of batch rows 16 bt + 4 q + r: half A + half B
+    float CPv[NBT][4], XSv[NBT][4];  // -1024 XSP and XS of batch rows 16 bt + 4 q + r: half A + half B
     if constexpr (MODE == 3) {
       float4 c1;
       StageReads<MODE, NS>::run(base + 16 * lane, base + SBOFF + 4 * j, base + XOFF + xrd, base + COFF + crd, W, S, X,
@@ -328,8 +336,11 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][1]), b1, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][2]), b0, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][3]), b1, Pm, 0, 0, 0);
+        // one-row launches keep only row 0 (the rows of the other lanes are
+        // never stored)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(bi, XSv[bt][r], fmaf(sc, Pm[r] + CPv[bt][r], Y[st][bt][r]));
+        for (int r = 0; r < (MODE == 3 ? 1 : 4); ++r)
+          Y[st][bt][r] = fmaf(bi, XSv[bt][r], fmaf(sc, Pm[r] + CPv[bt][r], Y[st][bt][r]));
       }
     }
   };
@@ -423,33 +434,39 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
   // ---- epilogue: lane holds weight row n for batch rows 16bt + 4q + r ----
   if constexpr (DUAL) {
     if (a.oact.XA) {
-      // the tile's 32 products of each batch row are one half of group
-      // tile / 2 of the down projection's input: transpose through LDS, then
-      // lane L prepares 16 of them (row L % 32, quarter pair L / 32)
+      // each tile's 32 products of a batch row are one half of group tile / 2
+      // of the down projection's input: transpose through LDS, then lane L
+      // prepares 16 of them (row L % 32, quarter pair L / 32)
       float* hb = reinterpret_cast<float*>(smem);  // [32][33]
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int ti = 0; ti < MT; ++ti) {
+        const int tile = blockIdx.x * MT + ti;
+        if (tile >= ntiles) break;
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int bt = 0; bt < NBT; ++bt)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int b = 16 * bt + 4 * q + r;
-            if (b < nb) hb[b * 33 + 16 * st + j] = silu_f(Y[st][bt][r]) * Y[2 + st][bt][r];
-          }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int b = lane & 31, st = lane >> 5;
-      float v[16];
+          for (int bt = 0; bt < NBT; ++bt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = b < nb ? hb[b * 33 + 16 * st + e] : 0.0f;
-      a8act::emit_slice<32>(a.oact, a.row0 + b, blockIdx.x >> 1, (blockIdx.x & 1) * 2 + st, v, b < nb);
+            for (int r = 0; r < 4; ++r) {
+              const int b = 16 * bt + 4 * q + r;
+              if (b < nb) hb[b * 33 + 16 * h + j] = silu_f(Y[2 * ti + h][bt][r]) * Y[NSM + 2 * ti + h][bt][r];
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int b = lane & 31, h = lane >> 5;
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = b < nb ? hb[b * 33 + 16 * h + e] : 0.0f;
+        a8act::emit_slice<32>(a.oact, a.row0 + b, tile >> 1, (tile & 1) * 2 + h, v, b < nb);
+      }
       if (!a.y) return;
     }
   }
 #pragma unroll
-  for (int st = 0; st < (DUAL ? 2 : NS); ++st) {
-    const int n = (blockIdx.x * MT + (DUAL ? 0 : st >> 1)) * 32 + 16 * (st & 1) + j;
+  for (int st = 0; st < NSM; ++st) {
+    const int n = (blockIdx.x * MT + (st >> 1)) * 32 + 16 * (st & 1) + j;
     if (n >= a.n_out) continue;
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt)
@@ -460,9 +477,177 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
         const size_t o = (size_t)b * a.ldy + n;
         if constexpr (EPI == EPI_STORE) a.y[o] = Y[st][bt][r];
         if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];
-        if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(Y[st][bt][r]) * Y[2 + st][bt][r];
+        if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(Y[st][bt][r]) * Y[NSM + st][bt][r];
       }
   }
+}
+
+// ---- 17..32 rows: activation stage shared by the waves of a workgroup ----
+// A workgroup holds T waves on T consecutive tiles, all on the same range r
+// of the KS-way split of the groups (grid: tile blocks x KS). Each group's
+// 32-row operands (8.5 KiB) are staged once per workgroup instead of once
+// per tile: every wave loads a quarter of them next to its own weights, and
+// one barrier per group publishes the stage. The range's partial sums go to
+// part[r][row][n]; a8_reduce_kernel adds the KS ranges in order 0, 1, ...
+// (the order of the in-workgroup reduction above), so results equal the
+// other modes bit for bit.
+template <int KS, int T, int P, int EPI>
+__global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const uint4* __restrict__ XA,
+                                                               const float* __restrict__ CA, int nb,
+                                                               float* __restrict__ part) {
+  static_assert(T == 2 || T == 4 || T == 8, "operand quarters per wave");
+  constexpr int NBT = 2;
+  static_assert(EPI != EPI_SWIGLU, "one matrix per wave");
+  constexpr int NS = 2;
+  constexpr int SHARED = 8192 + 512;        // operands + constants of both batch tiles
+  constexpr int PERW = NS * 1024 + 256;     // a wave's weights + scale/bias
+  constexpr int STAGE = SHARED + T * PERW;
+  constexpr int XPW = 8 / T;                // operand loads per wave (8 x 1 KiB per group)
+  constexpr int NDMA = NS + 1 + XPW + 1;    // weights, scale/bias, operands, one constant block
+  static_assert(P >= 3, "one stage is refilled while the next is in flight");
+  constexpr int NWAIT = (P - 2) * NDMA;
+  static_assert((size_t)P * STAGE <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) char smem[P * STAGE];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, q = lane >> 4;
+  const int G = a.n_in >> 6;
+  const int ntiles = (a.n_out + 31) >> 5;
+  const int tile = blockIdx.x * T + wave;
+  const int rtile = min(tile, ntiles - 1);  // a missing tile re-reads the last one; nothing is stored
+  const int r = blockIdx.y;
+  const int per = (G + KS - 1) / KS;
+  const int g0 = min(G, r * per), g1 = min(G, g0 + per);
+  const uint32_t smem_lds = lds_addr(smem);
+
+  const uint8_t* wsrc[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int row = 16 * st + j;
+    wsrc[st] = a.p0 + ((size_t)rtile * G << 11) + (q >> 1) * 1024 + row * 32 + (q & 1) * 16;
+  }
+  const uint32_t* ssrc =
+      reinterpret_cast<const uint32_t*>(a.p1) + ((size_t)rtile * G << 5) + 16 * min(lane >> 4, NS - 1) + j;
+  // this wave's share of the operands: loads XPW * wave .. of the 8 (tile bt = load / 4, operand load % 4)
+  const int x0 = XPW * wave;
+  const int cbt = wave & 1;  // constant block (waves 2.. load a copy of 0, 1's)
+
+  auto issue = [&](int g, int slot) {
+    char* sb = smem + slot * STAGE;
+    char* mine = sb + SHARED + wave * PERW;
+#pragma unroll
+    for (int st = 0; st < NS; ++st) dma16(wsrc[st] + ((size_t)g << 11), mine + st * 1024);
+    dma4(ssrc + ((size_t)g << 5), mine + NS * 1024);
+#pragma unroll
+    for (int i = 0; i < XPW; ++i) {
+      const int x = x0 + i, xbt = x >> 2, xi = x & 3;
+      dma16(XA + ((size_t)g * 2 + xbt) * 256 + xi * 64 + lane, sb + xbt * 4096 + xi * 1024);
+    }
+    dma4(CA + ((size_t)g * 2 + cbt) * 64 + lane, sb + 8192 + cbt * 256);
+  };
+
+  f4 Y[NS][NBT];
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int slot) {
+    const uint32_t base = smem_lds + slot * STAGE;
+    const uint32_t mine = base + SHARED + wave * PERW;
+    uint4 W[NS];
+    uint32_t S[NS];
+    uint4 X[NBT][4];
+    float4 CC[NBT][4];
+    StageReads<2, NS>::run(mine + 16 * lane, mine + NS * 1024 + 4 * j, base + 16 * lane, base + 8192 + 16 * q, W, S, X,
+                           CC);
+    float CPv[NBT][4], XSv[NBT][4];
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) {
+      CPv[bt][0] = CC[bt][0].x + CC[bt][1].x;
+      CPv[bt][1] = CC[bt][0].y + CC[bt][1].y;
+      CPv[bt][2] = CC[bt][0].z + CC[bt][1].z;
+      CPv[bt][3] = CC[bt][0].w + CC[bt][1].w;
+      XSv[bt][0] = CC[bt][2].x + CC[bt][3].x;
+      XSv[bt][1] = CC[bt][2].y + CC[bt][3].y;
+      XSv[bt][2] = CC[bt][2].z + CC[bt][3].z;
+      XSv[bt][3] = CC[bt][2].w + CC[bt][3].w;
+    }
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      const h8 b0 = codes8(W[st].x, W[st].y);
+      const h8 b1 = codes8(W[st].z, W[st].w);
+      const float sc = bf16_to_f32(S[st] & 0xffffu);
+      const float bi = bf16_to_f32(S[st] >> 16);
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        f4 Pm = {0.f, 0.f, 0.f, 0.f};
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][0]), b0, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][1]), b1, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][2]), b0, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][3]), b1, Pm, 0, 0, 0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          Y[st][bt][rr] = fmaf(bi, XSv[bt][rr], fmaf(sc, Pm[rr] + CPv[bt][rr], Y[st][bt][rr]));
+      }
+    }
+  };
+
+  // step i: wait for group g0 + i (P - 2 later groups stay in flight), publish
+  // it, refill the stage everyone finished at step i - 1, compute
+  if (g0 < g1) {
+#pragma unroll
+    for (int u = 0; u < P - 1; ++u) issue(min(g0 + u, g1 - 1), u);
+    int g = g0;
+    for (; g + P <= g1; g += P) {
+#pragma unroll
+      for (int u = 0; u < P; ++u) {
+        wait_vmcnt<NWAIT>();
+        __syncthreads();
+        issue(min(g + u + P - 1, g1 - 1), (u + P - 1) % P);
+        compute(u);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // tail: no more loads; the remaining stages arrive in order
+#pragma unroll
+    for (int u = 0; u < P - 1; ++u) {
+      if (g + u < g1) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        compute(u);
+      }
+    }
+  }
+  wait_vmcnt<0>();
+  if (tile >= ntiles) return;
+  // partial sums of range r: part[r][b][n]
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int n = tile * 32 + 16 * st + j;
+    if (n >= a.n_out) continue;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int b = 16 * bt + 4 * q + rr;
+        if (b < nb) part[((size_t)r * nb + b) * a.n_out + n] = Y[st][bt][rr];
+      }
+  }
+}
+
+// y[b][n] = (res[b][n] +) sum over ranges, in range order
+template <int EPI>
+__global__ __launch_bounds__(256) void a8_reduce_kernel(GemvArgs a, int nb, int ks, const float* __restrict__ part) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)nb * a.n_out) return;
+  const int b = (int)(i / a.n_out), n = (int)(i % a.n_out);
+  const size_t plane = (size_t)nb * a.n_out;
+  float y = part[i];
+  for (int r = 1; r < ks; ++r) y += part[(size_t)r * plane + i];
+  const size_t o = (size_t)b * a.ldy + n;
+  if constexpr (EPI == EPI_STORE) a.y[o] = y;
+  if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + y;
 }
 
 template <int MODE, int KS, int KP, int P, int MT, int EPI>
@@ -479,6 +664,17 @@ inline int split_ranges(const GemvArgs& a) {
   return tiles >= 512 ? 4 : tiles >= 256 ? 8 : 16;
 }
 
+template <int KS, int T, int P, int EPI>
+void launch_shared(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
+  static_assert(EPI != EPI_SWIGLU, "SwiGLU keeps the per-wave kernel");
+  const int tiles = (a.n_out + 31) / 32;
+  float* part = static_cast<float*>(gemv_scratch(s, (size_t)KS * nb * a.n_out * sizeof(float), 1));
+  hipLaunchKernelGGL((a8_mma_shared_kernel<KS, T, P, EPI>), dim3((tiles + T - 1) / T, KS), dim3(64 * T), 0, s, a, XA,
+                     CA, nb, part);
+  const size_t n = (size_t)nb * a.n_out;
+  hipLaunchKernelGGL((a8_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, nb, KS, part);
+}
+
 // one launch per chunk of up to 32 rows; the mode stages only the rows present
 // and picks waves per workgroup / ring depth within the LDS budget
 template <int KS, int EPI>
@@ -487,11 +683,14 @@ void launch_chunk_ks(const GemvArgs& a, const uint4* XA, const float* CA, int nb
   if (nb == 1) return launch_kernel<3, KS, KP8, 3, 1, EPI>(a, XA, CA, nb, s);
   if (nb <= 4) return launch_kernel<0, KS, KP8, 3, 1, EPI>(a, XA, CA, nb, s);
   if (nb <= 16) return launch_kernel<1, KS, KP4, 4, 1, EPI>(a, XA, CA, nb, s);
-  if constexpr (EPI != EPI_SWIGLU && KS <= 8) {
-    // wide matrices: two tiles per wave halve the activation traffic per weight byte
-    if ((a.n_out + 31) / 32 >= 256) return launch_kernel<2, KS, KP4, 3, 2, EPI>(a, XA, CA, nb, s);
+  if constexpr (EPI == EPI_SWIGLU) {
+    // gate + up already give each wave 2 KiB of weights per KiB of operands
+    launch_kernel<2, KS, KP4, 3, 1, EPI>(a, XA, CA, nb, s);
+  } else {
+    // one operand stage per workgroup of 4 (narrow) or 8 tiles
+    if constexpr (KS == 16) launch_shared<KS, 4, 3, EPI>(a, XA, CA, nb, s);
+    else launch_shared<KS, 8, 3, EPI>(a, XA, CA, nb, s);
   }
-  launch_kernel<2, KS, KP4, 3, 1, EPI>(a, XA, CA, nb, s);
 }
 
 template <int EPI>

@@ -348,11 +348,11 @@ __global__ void fill_kernel(float* out, size_t n, float v) {
 
 // ---------------------------------------------------------------------------
 namespace gemv {
-void* gemv_scratch(hipStream_t s, size_t bytes) {
+void* gemv_scratch(hipStream_t s, size_t bytes, int slot) {
   static std::mutex mu;
-  static std::map<hipStream_t, std::pair<void*, size_t>> bufs;
+  static std::map<std::pair<hipStream_t, int>, std::pair<void*, size_t>> bufs;
   std::lock_guard<std::mutex> lock(mu);
-  auto& e = bufs[s];
+  auto& e = bufs[{s, slot}];
   if (e.second < bytes) {
     if (e.first) {
       PGD_HIP(hipStreamSynchronize(s));
