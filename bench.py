@@ -9,9 +9,17 @@ the batch feeds its previous greedy token and gets its next one.
 
 value = aggregate decode tok/s at batch 32 (the batch-1 rate is reported as
 batch1_tok_s). roofline = the dominant kernel of that step (the fused
-gate/up SwiGLU A8 GEMV) timed with HIP events on the library's stream.
+gate/up SwiGLU A8 GEMV) timed with HIP events on the library's stream,
+cycling through 8 gate/up pairs (1.5 GB) so that each launch streams its
+weights from HBM as in the decode step, not from the 256 MB last-level
+cache; roofline.traffic comes from the committed rocprofv3 counter
+measurement of the same kernel (profiles/a8_swiglu_traffic.json).
 cpu_baseline = the C oracle (the CPU restatement used as the parity checker)
 on a bounded sample: one full-width 4-layer group, extrapolated per token.
+
+--roofline-only runs just the kernel timing (the command the counter runs
+profile); --copy-calib runs a plain device copy of known size for scaling
+the counters.
 """
 from __future__ import annotations
 
@@ -35,9 +43,8 @@ def log(*a):
 
 
 def gpu_bench(args):
-    from pagoda_amd import Device, Event, Matrix
+    from pagoda_amd import Device, Event
     from pagoda_amd.engine import QWEN35_27B, Model
-    from pagoda_amd.matrix import act_bytes, act_prep_dev
 
     dev = Device(os.environ.get("PAGODA_DEVICE", "hip"))
     batch = args.batch
@@ -60,17 +67,19 @@ def gpu_bench(args):
     for _ in range(args.warmup):
         ids, _ = model.step_ragged(sessions, [[int(t)] for t in ids])
     dev.sync()
-    e0 = Event(dev).record()
+    marks = [Event(dev).record()]
     t0 = time.perf_counter()
     for _ in range(args.steps):
         ids, _ = model.step_ragged(sessions, [[int(t)] for t in ids])
-    e1 = Event(dev).record()
+        marks.append(Event(dev).record())
     dev.sync()
     wall = time.perf_counter() - t0
-    gpu_ms = e0.elapsed_ms(e1)
+    per_step = np.array([marks[i].elapsed_ms(marks[i + 1]) for i in range(args.steps)])
+    gpu_ms = float(per_step.sum())
     ms_per_step = wall * 1e3 / args.steps
     tok_s = batch * args.steps / wall
-    log(f"batch {batch}: {ms_per_step:.2f} ms/step (events {gpu_ms / args.steps:.2f}), {tok_s:.1f} tok/s")
+    pct = {f"p{p}": round(float(np.percentile(per_step, p)), 3) for p in (10, 50, 90)}
+    log(f"batch {batch}: {ms_per_step:.2f} ms/step (events {gpu_ms / args.steps:.2f}; {pct}), {tok_s:.1f} tok/s")
     for s in sessions:
         s.free()
 
@@ -91,26 +100,44 @@ def gpu_bench(args):
     s.free()
     model.free()
 
-    # ---- dominant kernel: fused gate/up SwiGLU GEMV at the step's shape ----
-    # (the decode step feeds it activations prepared by the fused RMSNorm;
-    # here they are prepared once and only the GEMV kernel is timed)
+    roof = roofline(dev, cfg, batch)
+    return {
+        "tok_s": tok_s, "ms_per_step": ms_per_step, "batch1_tok_s": b1_tok_s, "step_ms_pct": pct,
+        "weight_gb": info["weight_bytes"] / 1e9, "algo_gb_per_step": info["algo_bytes_per_token"] / 1e9,
+        "roofline": roof,
+    }
+
+
+PAIRS = 8          # gate/up pairs cycled through (8 x 190 MB)
+LAUNCHES = 48      # timed launches per batch size
+
+
+def roofline(dev, cfg, batch):
+    """The fused gate/up SwiGLU A8 GEMV at the decode step's shape, fed
+    prepared activations as in the step; only the GEMV launches are timed,
+    with events on the library's stream."""
+    from pagoda_amd import Event, Matrix
+    from pagoda_amd.matrix import act_bytes, act_prep_dev
+
     H, I = cfg.hidden, cfg.intermediate
-    g = Matrix.synth(dev, 0, I, H, 2026, (0 << 8) | 12)
-    u = Matrix.synth(dev, 0, I, H, 2026, (0 << 8) | 13)
-    launches = 40
+    rng = np.random.default_rng(1)
+    pairs = [(Matrix.synth(dev, 0, I, H, 2026 + i, (i << 8) | 12), Matrix.synth(dev, 0, I, H, 2026 + i, (i << 8) | 13))
+             for i in range(PAIRS)]
 
     def time_swiglu(rows):
         x = dev.upload(rng.normal(0, 1, (rows, H)).astype(np.float32))
         act = dev.alloc(act_bytes(rows, H))
         mid = dev.alloc(rows * I * 4)
         act_prep_dev(dev, x, H, rows, H, act)
-        for _ in range(3):
+        for g, u in pairs[:2]:
             Matrix.gemv_swiglu_act_dev(g, u, act, rows, mid, I)
         e0 = Event(dev).record()
-        for _ in range(launches):
+        for i in range(LAUNCHES):
+            g, u = pairs[i % PAIRS]
             Matrix.gemv_swiglu_act_dev(g, u, act, rows, mid, I)
         e1 = Event(dev).record()
-        avg_ms = e0.elapsed_ms(e1) / launches
+        avg_ms = e0.elapsed_ms(e1) / LAUNCHES
+        g, u = pairs[0]
         algo = g.algo_bytes + u.algo_bytes + rows * H * 4 + rows * I * 4
         for p in (x, act, mid):
             dev.free(p)
@@ -121,17 +148,35 @@ def gpu_bench(args):
     avg1, algo1 = time_swiglu(1)
     log(f"swiglu GEMV kernel {batch} rows: {avg_ms * 1e3:.1f} us, {achieved:.0f} GB/s; 1 row: {avg1 * 1e3:.1f} us, "
         f"{algo1 / (avg1 * 1e-3) / 1e9:.0f} GB/s")
-    g.free()
-    u.free()
-    return {
-        "tok_s": tok_s, "ms_per_step": ms_per_step, "batch1_tok_s": b1_tok_s,
-        "weight_gb": info["weight_bytes"] / 1e9, "algo_gb_per_step": info["algo_bytes_per_token"] / 1e9,
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": f"a8_mma_kernel (fused gate/up SwiGLU A8 GEMV 5120->2x17408), {batch} rows",
-                     "algo_bytes_per_launch": algo, "avg_launch_us": avg_ms * 1e3,
-                     "batch1": {"achieved": algo1 / (avg1 * 1e-3) / 1e9, "avg_launch_us": avg1 * 1e3}},
-    }
+    for g, u in pairs:
+        g.free()
+        u.free()
+    traffic = None
+    tfile = ROOT / "profiles" / "a8_swiglu_traffic.json"
+    if tfile.exists():
+        t = json.loads(tfile.read_text())
+        if str(batch) in t.get("hbm_bytes_per_launch", {}):
+            traffic = t["hbm_bytes_per_launch"][str(batch)]
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+            "kernel": f"a8_mma_kernel (fused gate/up SwiGLU A8 GEMV 5120->2x17408), {batch} rows",
+            "algo_bytes_per_launch": algo, "avg_launch_us": avg_ms * 1e3,
+            "batch1": {"achieved": algo1 / (avg1 * 1e-3) / 1e9, "frac": algo1 / (avg1 * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                       "avg_launch_us": avg1 * 1e3, "algo_bytes_per_launch": algo1}}
+
+
+def copy_calib():
+    """A plain device-to-device copy kernel of known size (256 MiB read +
+    256 MiB written per launch) for scaling FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    n = 256 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(20):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 20}), flush=True)
 
 
 def cpu_baseline(args):
@@ -178,11 +223,22 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
+    if args.copy_calib:
+        copy_calib()
+        return
+    if args.roofline_only:
+        from pagoda_amd import Device
+        from pagoda_amd.engine import QWEN35_27B
+
+        print(json.dumps(roofline(Device(os.environ.get("PAGODA_DEVICE", "hip")), QWEN35_27B, args.batch)), flush=True)
+        return
     g = gpu_bench(args)
     cpu = None if args.no_cpu else cpu_baseline(args)
     out = {
@@ -202,6 +258,7 @@ def main():
                                "greedy decode", "batch": args.batch, "prompt_len": 19,
                    "weight_gb": round(g["weight_gb"], 3), "algo_weight_gb_per_step": round(g["algo_gb_per_step"], 3)},
         "batch1_tok_s": round(g["batch1_tok_s"], 2),
+        "step_ms_percentiles": g["step_ms_pct"],
         "roofline": g["roofline"],
         "cpu_baseline": cpu,
     }
