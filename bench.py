@@ -51,8 +51,8 @@ def gpu_bench(args):
     prompt_len = 19
     total = prompt_len + args.warmup + args.steps + 8
     cfg = QWEN35_27B
-    cfg.max_pos = max(256, total)
-    cfg.kv_blocks = (batch + 2) * ((total + cfg.kv_block - 1) // cfg.kv_block) + 16
+    cfg.max_pos = max(C5_TRUNK + C5_SUFFIX + C5_GEN + 64, total)
+    cfg.kv_blocks = (batch + 2) * ((total + cfg.kv_block - 1) // cfg.kv_block) + 16 + C5_PAGES
     t0 = time.time()
     model = Model.synth(dev, cfg, seed=2026)
     info = model.info()
@@ -98,14 +98,92 @@ def gpu_bench(args):
     b1_tok_s = n1 / wall1
     log(f"batch 1: {wall1 * 1e3 / n1:.2f} ms/token, {b1_tok_s:.1f} tok/s")
     s.free()
+    c5 = None if args.no_config5 else config5(model, cfg)
     model.free()
 
     roof = roofline(dev, cfg, batch)
     return {
-        "tok_s": tok_s, "ms_per_step": ms_per_step, "batch1_tok_s": b1_tok_s, "step_ms_pct": pct,
+        "tok_s": tok_s, "ms_per_step": ms_per_step, "batch1_tok_s": b1_tok_s, "step_ms_pct": pct, "config5": c5,
         "weight_gb": info["weight_bytes"] / 1e9, "algo_gb_per_step": info["algo_bytes_per_token"] / 1e9,
         "roofline": roof,
     }
+
+
+C5_REQ, C5_TRUNK, C5_SUFFIX, C5_GEN, C5_CHUNK = 64, 3968, 50, 32, 4
+C5_PAGES = (C5_TRUNK // 16 + 2) + 2 * C5_REQ * ((C5_SUFFIX + C5_GEN + C5_CHUNK) // 16 + 2)
+
+
+def config5(model, cfg):
+    """64 requests share one random 3968-token trunk
+    (prefilled once; its KV pages are shared copy-on-write by every fork),
+    each adds its own 50-token suffix and generates 32 greedy tokens.
+    Pass A decodes every request one token per step. Pass B restarts from the
+    same post-suffix states and packs decode rows (even requests) with 4-token
+    known-token verify chunks (odd requests, replaying pass A's tokens) into
+    one ragged batch per step; a verify chunk yields 4 tokens in one forward of
+    its request. Reports tok/s of both passes, the forwards saved and whether
+    every verified token equals pass A's."""
+    dev = model.dev
+    rng = np.random.default_rng(5)
+    trunk = rng.integers(0, cfg.vocab, C5_TRUNK)
+    root = model.new_session()
+    dev.sync()
+    t0 = time.perf_counter()
+    root.forward(trunk)
+    dev.sync()
+    t_trunk = time.perf_counter() - t0
+    reqs = [root.fork() for _ in range(C5_REQ)]
+    suffixes = [rng.integers(0, cfg.vocab, C5_SUFFIX) for _ in range(C5_REQ)]
+    t0 = time.perf_counter()
+    first, _ = model.step_ragged(reqs, suffixes)
+    dev.sync()
+    t_suffix = time.perf_counter() - t0
+    snap = [r.fork() for r in reqs]
+    # pass A: one decode row per request per step
+    streams = [[int(t)] for t in first]
+    t0 = time.perf_counter()
+    for _ in range(C5_GEN - 1):
+        ids, _ = model.step_ragged(reqs, [[s[-1]] for s in streams])
+        for s, t in zip(streams, ids):
+            s.append(int(t))
+    dev.sync()
+    t_a = time.perf_counter() - t0
+    # pass B: even requests decode, odd requests verify 4 known tokens per forward
+    pos = [1] * C5_REQ            # tokens of the stream produced so far (stream[0] came from the suffix)
+    fwd = [0] * C5_REQ            # forwards of each request
+    bad = 0
+    steps = 0
+    t0 = time.perf_counter()
+    while any(p < C5_GEN for p in pos):
+        sess, feeds, owners = [], [], []
+        for i in range(C5_REQ):
+            if pos[i] >= C5_GEN:
+                continue
+            n = 1 if i % 2 == 0 else min(C5_CHUNK, C5_GEN - pos[i])
+            feeds.append(streams[i][pos[i] - 1:pos[i] - 1 + n])
+            sess.append(snap[i])
+            owners.append((i, n))
+        ids, _ = model.step_ragged(sess, feeds, all_rows=True)
+        at = 0
+        for i, n in owners:
+            got = [int(t) for t in ids[at:at + n]]
+            bad += sum(1 for k in range(n) if got[k] != streams[i][pos[i] + k])
+            pos[i] += n
+            fwd[i] += 1
+            at += n
+        steps += 1
+    dev.sync()
+    t_b = time.perf_counter() - t0
+    produced = C5_REQ * (C5_GEN - 1)
+    saved = produced - sum(fwd)
+    for s in reqs + snap + [root]:
+        s.free()
+    out = {"requests": C5_REQ, "trunk": C5_TRUNK, "suffix": C5_SUFFIX, "gen": C5_GEN,
+           "trunk_prefill_s": round(t_trunk, 3), "suffix_prefill_s": round(t_suffix, 3),
+           "decode_tok_s": round(produced / t_a, 1), "mixed_tok_s": round(produced / t_b, 1),
+           "mixed_steps": steps, "forwards_saved": saved, "verify_mismatches": bad}
+    log(f"config 5: {out}")
+    return out
 
 
 PAIRS = 8          # gate/up pairs cycled through (8 x 190 MB)
@@ -225,6 +303,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--roofline-only", action="store_true")
     ap.add_argument("--copy-calib", action="store_true")
+    ap.add_argument("--no-config5", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -259,6 +338,7 @@ def main():
                    "weight_gb": round(g["weight_gb"], 3), "algo_weight_gb_per_step": round(g["algo_gb_per_step"], 3)},
         "batch1_tok_s": round(g["batch1_tok_s"], 2),
         "step_ms_percentiles": g["step_ms_pct"],
+        "config5": g["config5"],
         "roofline": g["roofline"],
         "cpu_baseline": cpu,
     }

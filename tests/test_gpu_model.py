@@ -196,3 +196,53 @@ def test_argument_errors_are_atomic(m35):
     assert s.context_len() == 3
     with pytest.raises(PagodaError):
         s.forward_verify([1, 2, 3, 4, 5])
+
+
+@pytest.mark.parametrize("which", ["m35", "m2"])
+def test_shared_trunk_mixed_decode_and_verify(which, request):
+    """Config-5 pattern at small size: requests fork one prefilled trunk
+    (KV pages shared copy-on-write), prefill distinct suffixes in one ragged
+    step, then decode; a second pass from the same post-suffix states packs
+    1-token decode rows with 4-token known-token verify chunks into one ragged
+    batch. Every verified id equals the decoded stream, and one request's
+    stream equals the oracle's greedy stream on the same tokens."""
+    model, oracle = request.getfixturevalue(which)
+    rng = np.random.default_rng(21)
+    trunk = rng.integers(0, model.cfg.vocab, 40)
+    nreq, gen = 6, 9
+    root = model.new_session()
+    root.forward(trunk)
+    reqs = [root.fork() for _ in range(nreq)]
+    suffixes = [rng.integers(0, model.cfg.vocab, 3 + i) for i in range(nreq)]
+    first, _ = model.step_ragged(reqs, suffixes)
+    snap = [r.fork() for r in reqs]
+    streams = [[int(t)] for t in first]
+    for _ in range(gen - 1):
+        ids, _ = model.step_ragged(reqs, [[s[-1]] for s in streams])
+        for s, t in zip(streams, ids):
+            s.append(int(t))
+    pos = [1] * nreq
+    while any(p < gen for p in pos):
+        sess, feeds, owners = [], [], []
+        for i in range(nreq):
+            if pos[i] >= gen:
+                continue
+            n = 1 if i % 2 == 0 else min(4, gen - pos[i])
+            feeds.append(streams[i][pos[i] - 1:pos[i] - 1 + n])
+            sess.append(snap[i])
+            owners.append((i, n))
+        ids, _ = model.step_ragged(sess, feeds, all_rows=True)
+        at = 0
+        for i, n in owners:
+            assert [int(t) for t in ids[at:at + n]] == streams[i][pos[i]:pos[i] + n], (i, pos[i])
+            pos[i] += n
+            at += n
+    # request 1 against the oracle: trunk + suffix, then its greedy stream
+    oc = oracle.new_cache()
+    ref = oracle.forward(np.concatenate([trunk, suffixes[1]]), oc)
+    for k in range(gen):
+        assert ora.argmax_first(ref) == streams[1][k], k
+        if k + 1 < gen:
+            ref = oracle.forward([streams[1][k]], oc)
+    for s in reqs + snap + [root]:
+        s.free()
