@@ -108,8 +108,8 @@ struct Q4K {
   static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t*, const uint8_t*,
                                   const GemvArgs& a, int row, int p) {
     W w;
-    w.q = *reinterpret_cast<const uint4*>(c0 + (size_t)row * a.nsb * 128 + ((size_t)p << 4));
-    w.hdr = reinterpret_cast<const uint4*>(c1)[(size_t)row * a.nsb + (p >> 3)];
+    w.q = *reinterpret_cast<const uint4*>(c0 + q4k_qs_off(row, p << 4, a.nsb));
+    w.hdr = *reinterpret_cast<const uint4*>(c1 + q4k_hdr_off(row, p >> 3, a.nsb));
     return w;
   }
   static __device__ inline void scale_min(const uint4& hdr, int is, float& sc, float& m) {
@@ -310,6 +310,9 @@ void launch_rows(GemvArgs a, int nrows, hipStream_t s) {
 // entry points of the instantiation files
 void run_q4k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 void run_q6k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
+// Q4K on the matrix cores (n_in % 64 == 0)
+bool q4k_mma_ok(const GemvArgs& a);
+void run_q4k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 // Per-stream device scratch for GEMV activation prep (grows, never shrinks;
 // growing drains the stream first).
 // per-stream device scratch that grows on demand (the stream is synchronized

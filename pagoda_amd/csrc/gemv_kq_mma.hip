@@ -1,0 +1,284 @@
+// gemv_kq_mma.hip — GGML Q4_K GEMV / skinny GEMM on the matrix cores.
+//
+// Q4_K (pagoda-hf/src/qwen2_gguf.rs:271-289 runs it through candle's
+// QMatMul): per 32-element sub-block s of a 256-element super-block,
+// w = d * sc[s] * q - dmin * m[s] with q a 4-bit code. Per sub-block:
+//   P[b, n] = sum_k (1024 + q[n,k]) * x[b,k]      v_mfma_f32_16x16x32_f16
+//   XS[b]   = sum_k x[b,k]                          (MFMA against a ones operand)
+//   Y[b, n] += d sc * P - (1024 d sc + dmin m) * XS
+// 1024 + q is exact in f16 and is what one byte permute makes of a nibble;
+// f32 activations enter as xh = f16(x), xl = f16(x - xh) (two MFMAs, ~22 bits
+// of x), f16 activations as themselves. The batch row is the MFMA's M index,
+// the weight row its N index, and the split of the groups depends on the
+// matrix shape only, so every batch row runs the same instruction sequence:
+// a batched call is bitwise equal to single-row calls.
+//
+// Weights are the tiled Q4K planes (quant.h): a 64-group of 32 rows is one
+// 1 KiB run of qs bytes (row-major, 32 B per row); a lane owning rows
+// j and 16 + j and k quarter q reads 8 bytes of each, whose low nibbles are
+// its 8 codes of sub-block 2 * (g % 4) and high nibbles those of the next.
+// Workgroups hold KS waves sharing one 32-row tile (KS from the shape) and
+// splitting its groups; each wave keeps PF groups of loads in flight; the
+// waves' partial sums meet in LDS in a fixed order.
+#include "common.h"
+#include "gemv_impl.h"
+#include "quant.h"
+
+namespace pgd {
+namespace gemv {
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// eight 4-bit codes (the low or high nibbles of 8 bytes) -> f16 1024 + q
+__device__ inline h8 nib8(uint32_t w0, uint32_t w1, int hi) {
+  const uint32_t a = hi ? (w0 >> 4) & 0x0F0F0F0Fu : w0 & 0x0F0F0F0Fu;
+  const uint32_t b = hi ? (w1 >> 4) & 0x0F0F0F0Fu : w1 & 0x0F0F0F0Fu;
+  // bytes [n, 0x64] form the f16 1024 + n
+  const uint32_t c0 = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
+  const uint32_t c1 = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
+  const uint32_t c2 = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+  const uint32_t c3 = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+  return __builtin_bit_cast(h8, make_uint4(c0, c1, c2, c3));
+}
+
+// 6-bit scale and min of sub-block is (0..7) from the 12 scale bytes
+__device__ inline void q4k_sc_m(const uint4& hdr, int is, float& sc, float& m) {
+  const uint4 s = make_uint4(hdr.y, hdr.z, hdr.w, 0u);
+  auto byte = [&](int i) -> uint32_t {
+    const uint32_t w = i < 4 ? s.x : (i < 8 ? s.y : s.z);
+    return (w >> (8 * (i & 3))) & 255u;
+  };
+  uint32_t a, b;
+  if (is < 4) {
+    a = byte(is) & 63u;
+    b = byte(is + 4) & 63u;
+  } else {
+    a = (byte(is + 4) & 0xFu) | ((byte(is - 4) >> 6) << 4);
+    b = (byte(is + 4) >> 4) | ((byte(is) >> 6) << 4);
+  }
+  sc = (float)a;
+  m = (float)b;
+}
+
+template <int NBT, int NS, bool XF16>
+struct Q4Raw {
+  uint2 w[NS];       // 8 qs bytes per 16-row subtile
+  uint4 hdr[NS];     // the subtile row's super-block header
+  uint4 x[2][NBT][XF16 ? 1 : 2];  // per sub-block half and batch tile: 8 activations (f16: 16 B, f32: 32 B)
+};
+
+template <int NBT, int KS, int PF, bool XF16, int EPI>
+__global__ __launch_bounds__(64 * KS) void q4k_mma_kernel(GemvArgs a, int nb) {
+  constexpr bool DUAL = EPI == EPI_SWIGLU;
+  constexpr int NS = DUAL ? 4 : 2;
+  __shared__ f4 red[KS > 1 ? KS - 1 : 1][NS][NBT][64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, q = lane >> 4;
+  const int G = a.n_in >> 6, nsb = a.nsb, G4 = 4 * nsb;
+  const int tile = blockIdx.x;
+
+  const uint8_t* wbase[NS];
+  const uint8_t* hbase[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const uint8_t* p = (DUAL && st >= 2) ? a.u0 : a.p0;
+    const uint8_t* ph = (DUAL && st >= 2) ? a.u1 : a.p1;
+    const int r = 16 * (st & 1) + j;
+    wbase[st] = p + (size_t)tile * G4 * 1024 + r * 32 + 8 * q;
+    hbase[st] = ph + (size_t)tile * nsb * 512 + r * 16;
+  }
+  // activation rows of this lane's A operand (rows past the batch re-read the
+  // last one; their MFMA rows only feed discarded outputs)
+  const uint8_t* xrow[NBT];
+#pragma unroll
+  for (int bt = 0; bt < NBT; ++bt) {
+    const int b = min(16 * bt + j, nb - 1);
+    xrow[bt] = reinterpret_cast<const uint8_t*>(a.x) + (size_t)b * a.ldx * (XF16 ? 2 : 4);
+  }
+
+  auto load = [&](int g, Q4Raw<NBT, NS, XF16>& R) {
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      R.w[st] = *reinterpret_cast<const uint2*>(wbase[st] + (size_t)g * 1024);
+      R.hdr[st] = *reinterpret_cast<const uint4*>(hbase[st] + (size_t)(g >> 2) * 512);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const int k0 = 64 * g + 32 * h + 8 * q;
+        if constexpr (XF16) {
+          R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 2);
+        } else {
+          R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4);
+          R.x[h][bt][1] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4 + 16);
+        }
+      }
+  };
+
+  f4 Y[NS][NBT];
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+  const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+
+  auto compute = [&](int g, const Q4Raw<NBT, NS, XF16>& R) {
+    // A operands and sub-block sums
+    h8 xh[2][NBT], xl[2][NBT];
+    f4 XS[2][NBT];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        if constexpr (XF16) {
+          xh[h][bt] = __builtin_bit_cast(h8, R.x[h][bt][0]);
+          XS[h][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[h][bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        } else {
+          const float v[8] = {__builtin_bit_cast(float, R.x[h][bt][0].x), __builtin_bit_cast(float, R.x[h][bt][0].y),
+                              __builtin_bit_cast(float, R.x[h][bt][0].z), __builtin_bit_cast(float, R.x[h][bt][0].w),
+                              __builtin_bit_cast(float, R.x[h][bt][1].x), __builtin_bit_cast(float, R.x[h][bt][1].y),
+                              __builtin_bit_cast(float, R.x[h][bt][1].z), __builtin_bit_cast(float, R.x[h][bt][1].w)};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const _Float16 hv = (_Float16)v[e];
+            xh[h][bt][e] = hv;
+            xl[h][bt][e] = (_Float16)(v[e] - (float)hv);
+          }
+          f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[h][bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          XS[h][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[h][bt], ones, t, 0, 0, 0);
+        }
+      }
+    const int js = 2 * (g & 3);  // sub-blocks js, js + 1 of the super-block
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      const float d = f16_to_f32(R.hdr[st].x & 0xffffu), dmin = f16_to_f32(R.hdr[st].x >> 16);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float sc, m;
+        q4k_sc_m(R.hdr[st], js + h, sc, m);
+        const float ca = d * sc;
+        const float cb = fmaf(1024.0f, ca, dmin * m);
+        const h8 bq = nib8(R.w[st].x, R.w[st].y, h);
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+          f4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[h][bt], bq, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          if constexpr (!XF16) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[h][bt], bq, P, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(ca, P[r], fmaf(-cb, XS[h][bt][r], Y[st][bt][r]));
+        }
+      }
+    }
+  };
+
+  const int per = (G + KS - 1) / KS;
+  const int g0 = wave * per, g1 = min(G, g0 + per);
+  Q4Raw<NBT, NS, XF16> buf[PF];
+#pragma unroll
+  for (int u = 0; u < PF; ++u)
+    if (g0 + u < g1) load(g0 + u, buf[u]);
+  for (int g = g0; g < g1; g += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      if (g + u < g1) {
+        compute(g + u, buf[u]);
+        if (g + u + PF < g1) load(g + u + PF, buf[u]);
+      }
+    }
+  }
+
+  // ---- split-K reduction (fixed order: wave 0 + 1 + ... + KS-1) ----
+  if constexpr (KS > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) red[wave - 1][st][bt][lane] = Y[st][bt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 0; w < KS - 1; ++w)
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[w][st][bt][lane];
+  }
+  // ---- epilogue: lane holds weight row n for batch rows 16bt + 4q + r ----
+#pragma unroll
+  for (int st = 0; st < (DUAL ? 2 : NS); ++st) {
+    const int n = tile * 32 + 16 * (st & 1) + j;
+    if (n >= a.n_out) continue;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int b = 16 * bt + 4 * q + r;
+        if (b >= nb) continue;
+        const size_t o = (size_t)b * a.ldy + n;
+        if constexpr (EPI == EPI_STORE) a.y[o] = Y[st][bt][r];
+        if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];
+        if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(Y[st][bt][r]) * Y[2 + st][bt][r];
+      }
+  }
+}
+
+// split of the groups: depends on the matrix shape only
+inline int q4k_split(const GemvArgs& a) {
+  const int tiles = (a.n_out + 31) / 32, G = a.n_in / 64;
+  int ks = 1;
+  while (ks < 8 && tiles * ks < 1024 && G / (2 * ks) >= 2) ks *= 2;
+  return ks;
+}
+
+template <int NBT, int KS, bool XF16, int EPI>
+void q4k_launch(const GemvArgs& a, int nb, hipStream_t s) {
+  hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI>), dim3((a.n_out + 31) / 32), dim3(64 * KS), 0, s, a, nb);
+}
+
+template <int NBT, bool XF16, int EPI>
+void q4k_launch_ks(const GemvArgs& a, int nb, hipStream_t s) {
+  switch (q4k_split(a)) {
+    case 1: return q4k_launch<NBT, 1, XF16, EPI>(a, nb, s);
+    case 2: return q4k_launch<NBT, 2, XF16, EPI>(a, nb, s);
+    case 4: return q4k_launch<NBT, 4, XF16, EPI>(a, nb, s);
+    default: return q4k_launch<NBT, 8, XF16, EPI>(a, nb, s);
+  }
+}
+
+template <bool XF16, int EPI>
+void q4k_rows(GemvArgs a, int nrows, hipStream_t s) {
+  const size_t xel = XF16 ? 2 : 4;
+  while (nrows > 0) {
+    const int nb = nrows < 32 ? nrows : 32;
+    if (nb > 16) q4k_launch_ks<2, XF16, EPI>(a, nb, s);
+    else q4k_launch_ks<1, XF16, EPI>(a, nb, s);
+    PGD_HIP(hipGetLastError());
+    nrows -= nb;
+    a.x = reinterpret_cast<const uint8_t*>(a.x) + (size_t)nb * a.ldx * xel;
+    a.y += (size_t)nb * a.ldy;
+    if (a.res) a.res += (size_t)nb * a.ldres;
+  }
+}
+
+}  // namespace
+
+bool q4k_mma_ok(const GemvArgs& a) { return a.n_in % 64 == 0; }
+
+void run_q4k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s) {
+  if (x_f16) {
+    if (epi == EPI_SWIGLU) q4k_rows<true, EPI_SWIGLU>(a, nrows, s);
+    else if (epi == EPI_RES) q4k_rows<true, EPI_RES>(a, nrows, s);
+    else q4k_rows<true, EPI_STORE>(a, nrows, s);
+  } else {
+    if (epi == EPI_SWIGLU) q4k_rows<false, EPI_SWIGLU>(a, nrows, s);
+    else if (epi == EPI_RES) q4k_rows<false, EPI_RES>(a, nrows, s);
+    else q4k_rows<false, EPI_STORE>(a, nrows, s);
+  }
+}
+
+}  // namespace gemv
+}  // namespace pgd

@@ -50,6 +50,17 @@ __host__ __device__ inline size_t a8_sb_off(int row, int g, int G) {
   return (((size_t)(row >> 5) * G + g) << 5) + (size_t)(row & 31);
 }
 
+// Q4K tiled addressing: the GGML block bytes, reordered so that the 32 bytes
+// of one 64-group of 32 consecutive rows are one 1 KiB run. qs byte i
+// (0 <= i < 128 nsb; 64-group g = i / 32) of row r, and the 16-byte header
+// (d, dmin, 12 scale bytes) of super-block sb of row r.
+__host__ __device__ inline size_t q4k_qs_off(int row, int i, int nsb) {
+  return ((size_t)(row >> 5) * (4 * (size_t)nsb) + (size_t)(i >> 5)) * 1024 + (size_t)(row & 31) * 32 + (size_t)(i & 31);
+}
+__host__ __device__ inline size_t q4k_hdr_off(int row, int sb, int nsb) {
+  return ((size_t)(row >> 5) * nsb + (size_t)sb) * 512 + (size_t)(row & 31) * 16;
+}
+
 // algorithmic bytes of the weights (what a GEMV must stream at least once;
 // unpadded n_in as the measurement plan defines it)
 double qmat_algo_bytes(const QMat& m);

@@ -24,7 +24,10 @@ void run_fmt(const QMat& m, const GemvArgs& a, int nrows, int x_f16, int epi, hi
       run_a8_mma(a, act, epi, s);
       break;
     }
-    case FMT_Q4K: run_q4k(a, nrows, x_f16, epi, s); break;
+    case FMT_Q4K:
+      if (q4k_mma_ok(a)) run_q4k_mma(a, nrows, x_f16, epi, s);
+      else run_q4k(a, nrows, x_f16, epi, s);
+      break;
     case FMT_Q6K: run_q6k(a, nrows, x_f16, epi, s); break;
     default: throw Error{kErrFormat, "unknown matrix format"};
   }
@@ -69,8 +72,8 @@ __global__ void dequant_q4k_kernel(const uint8_t* qs, const uint4* hdr, int n_in
   int r = (int)(t / runs), p = (int)(t % runs);
   int row = ids ? (int)ids[r] : row0 + r;
   int sb = p >> 3, part = p & 7, j = part >> 1, h = part & 1;
-  uint4 q = *reinterpret_cast<const uint4*>(qs + (size_t)row * nsb * 128 + (size_t)p * 16);
-  uint4 hd = hdr[(size_t)row * nsb + sb];
+  uint4 q = *reinterpret_cast<const uint4*>(qs + q4k_qs_off(row, p * 16, nsb));
+  uint4 hd = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(hdr) + q4k_hdr_off(row, sb, nsb));
   float d = f16_to_f32(hd.x & 0xffffu), dmin = f16_to_f32(hd.x >> 16);
   float sc0, m0, sc1, m1;
   Q4K::scale_min(hd, 2 * j, sc0, m0);
@@ -267,8 +270,8 @@ __global__ void synth_q4k_kernel(uint8_t* qs, uint4* hdr, int n_out, int n_in, i
   for (int i = 0; i < 3; ++i)
     sw[i] = (uint32_t)sc[4 * i] | ((uint32_t)sc[4 * i + 1] << 8) | ((uint32_t)sc[4 * i + 2] << 16) |
             ((uint32_t)sc[4 * i + 3] << 24);
-  hdr[t] = make_uint4((uint32_t)dh | ((uint32_t)mh << 16), sw[0], sw[1], sw[2]);
-  uint8_t* q = qs + t * 128;
+  *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(hdr) + q4k_hdr_off((int)r, b, nsb)) =
+      make_uint4((uint32_t)dh | ((uint32_t)mh << 16), sw[0], sw[1], sw[2]);
   for (int grp = 0; grp < 4; ++grp) {
     int j0 = 2 * grp, j1 = 2 * grp + 1;
     float ds0 = d * (float)scq[j0], dm0 = dmin * (float)mq[j0];
@@ -283,7 +286,7 @@ __global__ void synth_q4k_kernel(uint8_t* qs, uint4* hdr, int n_out, int n_in, i
         float q1 = ds1 > 0.0f ? clampf(rintf((v1 + dm1) / ds1), 0.0f, 15.0f) : 0.0f;
         word |= ((uint32_t)q0 | ((uint32_t)q1 << 4)) << (8 * e);
       }
-      *reinterpret_cast<uint32_t*>(q + 32 * grp + l4) = word;
+      *reinterpret_cast<uint32_t*>(qs + q4k_qs_off((int)r, b * 128 + 32 * grp + l4, nsb)) = word;
     }
   }
 }
@@ -400,8 +403,9 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s) {
     place(1, tiles * (n_in / 64) * 128);
   } else if (fmt == FMT_Q4K) {
     PGD_CHECK(n_in % 32 == 0, kErrShape, "Q4K n_in must be a multiple of 32");
-    place(0, rows * m.nsb * 128);
-    place(1, rows * m.nsb * 16);
+    size_t tiles = (rows + 31) / 32;
+    place(0, tiles * 4 * m.nsb * 1024);
+    place(1, tiles * m.nsb * 512);
   } else if (fmt == FMT_Q6K) {
     PGD_CHECK(n_in % 32 == 0, kErrShape, "Q6K n_in must be a multiple of 32");
     place(0, rows * m.nsb * 128);
@@ -422,7 +426,7 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s) {
   m.p3 = fmt == FMT_Q6K ? m.base + off[3] : nullptr;
   // zero the padding rows of the last tile, ordered before the writes that
   // follow on the same stream
-  if (fmt == FMT_A8) PGD_HIP(hipMemsetAsync(m.base, 0, total, s));
+  if (fmt == FMT_A8 || fmt == FMT_Q4K) PGD_HIP(hipMemsetAsync(m.base, 0, total, s));
 }
 
 void qmat_free(QMat& m) {
@@ -452,12 +456,16 @@ void qmat_upload_a8(QMat& m, const uint32_t* packed, const uint16_t* scales, con
 void qmat_upload_kq(QMat& m, const uint8_t* blocks, hipStream_t s) {
   size_t nb = (size_t)m.n_out * m.nsb;
   if (m.fmt == FMT_Q4K) {
-    std::vector<uint8_t> qs(nb * 128), hdr(nb * 16);
-    for (size_t i = 0; i < nb; ++i) {
-      const uint8_t* b = blocks + i * 144;
-      std::copy(b, b + 16, hdr.data() + i * 16);
-      std::copy(b + 16, b + 144, qs.data() + i * 128);
-    }
+    // GGML blocks (row-major, 144 B each) -> tiled planes (same bytes, permuted)
+    const size_t tiles = ((size_t)m.n_out + 31) / 32;
+    std::vector<uint8_t> qs(tiles * 4 * m.nsb * 1024, 0), hdr(tiles * m.nsb * 512, 0);
+    for (int r = 0; r < m.n_out; ++r)
+      for (int sb = 0; sb < m.nsb; ++sb) {
+        const uint8_t* b = blocks + ((size_t)r * m.nsb + sb) * 144;
+        std::copy(b, b + 16, hdr.data() + q4k_hdr_off(r, sb, m.nsb));
+        for (int g = 0; g < 4; ++g)
+          std::copy(b + 16 + 32 * g, b + 48 + 32 * g, qs.data() + q4k_qs_off(r, sb * 128 + 32 * g, m.nsb));
+      }
     PGD_HIP(hipMemcpyAsync(m.p0, qs.data(), qs.size(), hipMemcpyHostToDevice, s));
     PGD_HIP(hipMemcpyAsync(m.p1, hdr.data(), hdr.size(), hipMemcpyHostToDevice, s));
     PGD_HIP(hipStreamSynchronize(s));
