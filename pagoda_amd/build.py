@@ -34,13 +34,21 @@ COMMON = [
 ]
 
 
+# per-file extra flags
+EXTRA = {
+    # keep the stream-K GEMV's register prefetch ring in registers (LLVM would
+    # otherwise move the private array into LDS, serializing every load)
+    "gemv_sk.hip": ["-mllvm", "-disable-promote-alloca-to-lds"],
+}
+
+
 def sources() -> list[Path]:
     return sorted(p for p in CSRC.iterdir() if p.suffix in (".hip", ".cpp"))
 
 
 def _compile(src: Path) -> Path:
     obj = OUT_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -321,6 +321,10 @@ void run_q4k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s
 void* gemv_scratch(hipStream_t s, size_t bytes, int slot = 0);
 // A8 on the matrix cores (f32 activations)
 void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s);
+// Stream-K A8 kernel: whether a matrix takes it for 5..32-row launches, and
+// one launch of 5..32 rows (operand chunk XA / CA of the prepared activations)
+bool a8_sk_wanted(const GemvArgs& a, int epi);
+void run_a8_sk_chunk(const GemvArgs& a, const uint4* XA, const float* CA, int nb, int epi, hipStream_t s);
 
 }  // namespace gemv
 }  // namespace pgd

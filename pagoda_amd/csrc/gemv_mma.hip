@@ -708,11 +708,13 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   const int G = a.n_in / 64;
   const uint4* XA = reinterpret_cast<const uint4*>(act.XA);
   int rows = act.rows;
+  const bool sk = a8_sk_wanted(a, EPI);
   for (int c = 0; rows > 0; ++c) {
     const int nb = rows < 32 ? rows : 32;
     const uint4* xa = XA + (size_t)c * G * 2 * 256;
     const float* ca = act.CA + (size_t)c * G * 2 * 64;
-    launch_chunk<EPI>(a, xa, ca, nb, s);
+    if (sk && nb >= 5) run_a8_sk_chunk(a, xa, ca, nb, EPI, s);
+    else launch_chunk<EPI>(a, xa, ca, nb, s);
     PGD_HIP(hipGetLastError());
     rows -= nb;
     if (a.y) a.y += (size_t)nb * a.ldy;

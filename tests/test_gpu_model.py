@@ -92,23 +92,40 @@ def test_prefill_then_greedy_decode_matches_oracle(which, request):
 
 @pytest.mark.parametrize("which", ["m35", "m2"])
 def test_ragged_batch_bitwise_equals_serial(which, request):
-    """Batched step == per-session forwards (pagoda/tests/batch_tests.rs:217-242);
-    every kernel computes rows independently, so the logits are bitwise equal."""
+    """Batched step == per-session forwards (pagoda/tests/batch_tests.rs:217-242).
+    Every kernel computes rows independently. A row's logits are bitwise equal
+    whenever the GEMV launches holding it have the same size class (1..4 or
+    5..32 rows: the fused SwiGLU and the >= 2048-tile lm_head switch kernels
+    between them), else within 1e-5 with the same greedy id; a permuted batch
+    is bitwise equal to the original."""
     model, _ = request.getfixturevalue(which)
     rng = np.random.default_rng(4)
     prompts = [rng.integers(0, model.cfg.vocab, n) for n in (5, 9, 1, 17)]
     serial = [model.new_session() for _ in prompts]
     batched = [model.new_session() for _ in prompts]
+    permuted = [model.new_session() for _ in prompts]
+    order = [2, 0, 3, 1]
+
+    def check(bl, ser, feeds):
+        for i in range(len(feeds)):
+            same_class = (len(feeds[i]) <= 4) == (sum(len(f) for f in feeds) <= 4)
+            if same_class:
+                np.testing.assert_array_equal(bl[i].view(np.uint32), ser[i].view(np.uint32))
+            else:
+                assert rel(bl[i], ser[i]) < 1e-5
+                assert int(np.argmax(bl[i])) == int(np.argmax(ser[i]))
+
     ser_logits = [s.forward(p) for s, p in zip(serial, prompts)]
     _, bl = model.step_ragged(batched, prompts, want_logits=True)
-    for i in range(len(prompts)):
-        np.testing.assert_array_equal(bl[i].view(np.uint32), ser_logits[i].view(np.uint32))
+    check(bl, ser_logits, prompts)
+    _, pl = model.step_ragged([permuted[i] for i in order], [prompts[i] for i in order], want_logits=True)
+    for k, i in enumerate(order):
+        np.testing.assert_array_equal(pl[k].view(np.uint32), bl[i].view(np.uint32))
     # mixed decode rows and 4-token chunks in one step
     feeds = [[int(np.argmax(ser_logits[0]))], rng.integers(0, model.cfg.vocab, 4), [7], rng.integers(0, 100, 3)]
     ser = [s.forward(f) for s, f in zip(serial, feeds)]
     _, bl = model.step_ragged(batched, feeds, want_logits=True)
-    for i in range(len(feeds)):
-        np.testing.assert_array_equal(bl[i].view(np.uint32), ser[i].view(np.uint32))
+    check(bl, ser, feeds)
     assert [s.context_len() for s in batched] == [s.context_len() for s in serial]
 
 

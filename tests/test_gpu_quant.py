@@ -2,7 +2,10 @@
 
 Bars: dequantized weights bit-exact to the oracle; GEMV within 1e-3 of an
 fp64 dot over the oracle-dequantized weights (max error relative to max
-|y|), batched rows bitwise equal to single-row calls.
+|y|); batched rows bitwise equal to single-row calls, except that the fused
+SwiGLU GEMV and matrices of >= 2048 row tiles run 5..32-row launches on the
+stream-K kernel (bitwise equal among themselves, within 1e-5 of 1..4-row
+launches).
 """
 import numpy as np
 import pytest
@@ -228,3 +231,61 @@ def test_a8_two_tile_waves_large_matrix(dev, n_out, rows):
     assert rel_err(y, ref) < GEMV_TOL
     for i in (0, 7, rows - 1):
         np.testing.assert_array_equal(m.gemv(x[i]).view(np.uint32), y[i].view(np.uint32))
+
+
+def _class_checks(full, sub7, sub13, single, ref):
+    """Stream-K launches (5..32 rows) compute every row alike: a row's output
+    is bitwise the same in any 5..32-row launch; 1..4-row launches use the
+    split-K kernel and agree to fp32 rounding."""
+    assert rel_err(full, ref) < GEMV_TOL
+    np.testing.assert_array_equal(sub7.view(np.uint32), full[:7].view(np.uint32))
+    np.testing.assert_array_equal(sub13.view(np.uint32), full[32:45].view(np.uint32))
+    scale = np.abs(full[3]).max()
+    assert np.abs(single.astype(np.float64) - full[3]).max() <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("n_out,n_in", [(65536 + 40, 128), (66000, 320)])
+def test_a8_stream_k_tall_matrix(dev, n_out, n_in):
+    """Matrices of >= 2048 row tiles (lm_head) take the stream-K kernel for
+    5..32-row launches (two tiles per wave, partial runs added by the fix-up
+    kernel); a 45-row call is one 32-row and one 13-row launch."""
+    from pagoda_amd import Matrix
+
+    m = Matrix.synth(dev, 0, n_out, n_in, 5, 3, 0.02)
+    deq = m.dequant().astype(np.float64)
+    rng = np.random.default_rng(n_out)
+    x = rng.normal(0, 1, (45, n_in)).astype(np.float32)
+    full = m.gemv(x)
+    ref = x.astype(np.float64) @ deq.T
+    _class_checks(full, m.gemv(x[:7]), m.gemv(x[32:45]), m.gemv(x[3]), ref)
+
+
+@pytest.mark.parametrize("n_out,n_in", [(1000, 512), (2000, 5120)])
+def test_a8_stream_k_swiglu(dev, n_out, n_in):
+    """The fused gate/up SwiGLU GEMV takes the stream-K kernel for 5..32 rows:
+    silu(x Wg^T) * (x Wu^T) against fp64 over the dequantized weights; ragged
+    last tile (n_out % 32 != 0) and blocks cut into many runs (K = 5120 with
+    few tiles)."""
+    from pagoda_amd import Matrix
+
+    g = Matrix.synth(dev, 0, n_out, n_in, 11, 1, 0.02)
+    u = Matrix.synth(dev, 0, n_out, n_in, 11, 2, 0.02)
+    dg, du = g.dequant().astype(np.float64), u.dequant().astype(np.float64)
+    rng = np.random.default_rng(n_out + n_in)
+    x = rng.normal(0, 1, (45, n_in)).astype(np.float32)
+
+    def run(xs):
+        rows = xs.shape[0]
+        xd = dev.upload(np.ascontiguousarray(xs))
+        md = dev.alloc(rows * n_out * 4)
+        Matrix.gemv_swiglu_dev(g, u, xd, n_in, rows, md, n_out)
+        out = dev.download(md, (rows, n_out), np.float32)
+        dev.free(xd)
+        dev.free(md)
+        return out
+
+    full = run(x)
+    x64 = x.astype(np.float64)
+    a, b = x64 @ dg.T, x64 @ du.T
+    ref = a / (1.0 + np.exp(-a)) * b
+    _class_checks(full, run(x[:7]), run(x[32:45]), run(x[3:4])[0], ref)
