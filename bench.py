@@ -237,7 +237,8 @@ def roofline(dev, cfg, batch):
             traffic = t["hbm_bytes_per_launch"][str(batch)]
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-            "kernel": f"a8_mma_kernel (fused gate/up SwiGLU A8 GEMV 5120->2x17408), {batch} rows",
+            "kernel": (f"fused gate/up SwiGLU A8 GEMV 5120->2x17408, {batch} rows: a8_sk_kernel<2,2,2> (stream-K) "
+                       f"+ a8_sk_fix_kernel<2,2> (cut blocks); 1 row: a8_mma_kernel<3,4,4,3,1,2>"),
             "algo_bytes_per_launch": algo, "avg_launch_us": avg_ms * 1e3,
             "batch1": {"achieved": algo1 / (avg1 * 1e-3) / 1e9, "frac": algo1 / (avg1 * 1e-3) / 1e9 / HBM_PEAK_GBS,
                        "avg_launch_us": avg1 * 1e3, "algo_bytes_per_launch": algo1}}

@@ -226,40 +226,33 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
   };
   zero_y();
 
+  // batch tile outer, subtile inner: one batch tile's operands are live at a
+  // time (the byte permutes of the codes are redone per batch tile, cheaper
+  // than the registers holding them)
   auto compute = [&](const WR& r, int slot) {
     const char* sb = smem + slot * Gm::SLOT;
     const u4* sx = reinterpret_cast<const u4*>(sb);
     const f4* sc = reinterpret_cast<const f4*>(sb + Gm::XU4 * 16);
-    u4 X[NBT][4];
-    float CPv[NBT][4], XSv[NBT][4];
-    // operands [bt][i][lane]; constants [bt][-1024 XSP | XS][16]
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) {
+      // operands [bt][i][lane]; constants [bt][-1024 XSP | XS][16]
+      u4 X[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) X[bt][i] = sx[bt * 256 + i * 64 + lane];
+      for (int i = 0; i < 4; ++i) X[i] = sx[bt * 256 + i * 64 + lane];
       const f4 cp = sc[bt * 8 + q], xs = sc[bt * 8 + 4 + q];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        CPv[bt][rr] = cp[rr];
-        XSv[bt][rr] = xs[rr];
-      }
-    }
-#pragma unroll
-    for (int st = 0; st < NS; ++st) {
-      const h8 b0 = codes8(r.w[st].x, r.w[st].y);
-      const h8 b1 = codes8(r.w[st].z, r.w[st].w);
-      const float sc = bf16_to_f32(r.s[st] & 0xffffu);
-      const float bi = bf16_to_f32(r.s[st] >> 16);
-#pragma unroll
-      for (int bt = 0; bt < NBT; ++bt) {
+      for (int st = 0; st < NS; ++st) {
+        const h8 b0 = codes8(r.w[st].x, r.w[st].y);
+        const h8 b1 = codes8(r.w[st].z, r.w[st].w);
+        const float sc = bf16_to_f32(r.s[st] & 0xffffu);
+        const float bi = bf16_to_f32(r.s[st] >> 16);
         f4 Pm = {0.f, 0.f, 0.f, 0.f};
-        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][0]), b0, Pm, 0, 0, 0);
-        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][1]), b1, Pm, 0, 0, 0);
-        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][2]), b0, Pm, 0, 0, 0);
-        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][3]), b1, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[0]), b0, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[1]), b1, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[2]), b0, Pm, 0, 0, 0);
+        Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[3]), b1, Pm, 0, 0, 0);
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          Y[st][bt][rr] = fmaf(bi, XSv[bt][rr], fmaf(sc, Pm[rr] + CPv[bt][rr], Y[st][bt][rr]));
+        for (int rr = 0; rr < 4; ++rr) Y[st][bt][rr] = fmaf(bi, xs[rr], fmaf(sc, Pm[rr] + cp[rr], Y[st][bt][rr]));
       }
     }
   };
@@ -329,14 +322,14 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
 }
 
 // Cut blocks: add the runs' partial sums in run order, then the epilogue.
-// One workgroup per block, wave w on tile 8 * block + w.
+// One single-wave workgroup per (block, wave of the streaming kernel), so the
+// few blocks of a matrix still spread over many compute units.
 template <int MODE, int EPI>
-__global__ __launch_bounds__(64 * kWaves) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArgs k) {
+__global__ __launch_bounds__(64) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArgs k) {
   using Gm = Geo<MODE, EPI == EPI_SWIGLU>;
   constexpr int NS = Gm::NS, NBT = Gm::NBT, NF = Gm::NF;
-  __shared__ __attribute__((aligned(16))) char smem[Gm::HB > 0 ? Gm::HB : 16];
-  const int blk = blockIdx.x, lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ __attribute__((aligned(16))) char smem[Gm::HB > 0 ? Gm::HB / kWaves : 16];
+  const int blk = blockIdx.x / kWaves, wave = blockIdx.x % kWaves, lane = threadIdx.x;
   const long long b0 = (long long)blk * k.G;
   const int r0 = run_of(k.U, k.nwg, b0), r1 = run_of(k.U, k.nwg, b0 + k.G - 1);
   if (r0 == r1 || (blk * kWaves + wave) * Gm::TPW >= k.ntiles) return;  // whole in one run: done in place
@@ -366,7 +359,7 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_fix_kernel(GemvArgs a, int 
         for (int bt = 0; bt < NBT; ++bt) V[st][bt] = r + t == r0 ? P[t][st][bt] : V[st][bt] + P[t][st][bt];
     }
   }
-  wave_epilogue<MODE, EPI>(a, nb, blk, wave, V, reinterpret_cast<float*>(smem) + wave * 32 * 33);
+  wave_epilogue<MODE, EPI>(a, nb, blk, wave, V, reinterpret_cast<float*>(smem));
 }
 
 // ---- host side ----
@@ -395,7 +388,7 @@ void launch_sk(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipS
   k.nwg = (int)std::min<long long>(cu_count(), k.U);
   k.part = static_cast<f4*>(gemv_scratch(s, (size_t)k.nwg * 2 * kWaves * Gm::NF * 64 * sizeof(f4), 3));
   hipLaunchKernelGGL((a8_sk_kernel<MODE, EPI, D>), dim3(k.nwg), dim3(64 * kWaves), 0, s, a, XA, CA, nb, k);
-  hipLaunchKernelGGL((a8_sk_fix_kernel<MODE, EPI>), dim3(k.nblocks), dim3(64 * kWaves), 0, s, a, nb, k);
+  hipLaunchKernelGGL((a8_sk_fix_kernel<MODE, EPI>), dim3(k.nblocks * kWaves), dim3(64), 0, s, a, nb, k);
 }
 
 template <int EPI>
