@@ -1,0 +1,442 @@
+// attn.hip — paged GQA decode attention on the matrix cores, by page chunks.
+//
+// Counterpart of FullAttn::forward's softmax attention (pagoda-hf/src/
+// qwen3_5.rs:1433-1475), full_attn_heads (qwen3_fuse.rs:384-440) and the
+// Qwen2 attention core (qwen2_gguf.rs:252-266): row r attends to positions
+// [0, pos_of_row[r]] of its sequence, softmax(q k^T / sqrt(hd)) v per head,
+// GQA group = heads / kv_heads query heads per KV head; the hybrid model then
+// multiplies by sigmoid(gate).
+//
+// Work split (the plan, built on the host from the block tables). A row's
+// context is cut into chunks of kChunkPages pages. Rows whose chunk holds the
+// same physical pages — requests forked from one trunk, the rows of one
+// sequence in a prefill or verify chunk — share one work item, so the chunk's
+// K/V is read once for all of them. An item holds at most 64 query vectors
+// (rows x group heads); each 16 of them are one wave.
+//
+// Item kernel, per page of the chunk (16 positions), per wave (the four waves
+// of an item take every fourth page and are combined in LDS):
+//   S[p][n] = sum_d K[p][d] Q[n][d]        64 x v_mfma_f32_16x16x4_f32 (hd 256)
+//   block softmax update per query n (positions past the row's length masked)
+//   O[n][d] += sum_p P[n][p] V[p][d]       64 x v_mfma_f32_16x16x4_f32
+// in fp32 like the reference. The score registers of the first product are
+// the A operand of the second as they stand: lane (n, kq) holds positions
+// 4 kq + r, which is the k index the second product assigns to it. The
+// item writes per query its running max m, sum l and unnormalized O.
+// Merge kernel, per (row, kv head): the row's chunk partials in chunk order,
+// O / l, then gate and output (or the o projection's prepared operands).
+// When every row of a launch has a single chunk, the item kernel does this
+// last step itself and the merge is skipped (one launch for short contexts).
+// A row's result depends only on its own chunks, never on which rows shared
+// an item, so batched rows equal single-row calls bit for bit.
+#include <unordered_map>
+#include <vector>
+
+#include "a8_act.h"
+#include "common.h"
+#include "gemv_impl.h"
+#include "ops.h"
+
+namespace pgd {
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kItemFields = 5;  // page_off, npages, row_off, nrows, chunk index
+
+// ---------------------------------------------------------------------------
+// item kernel
+// ---------------------------------------------------------------------------
+// Workgroup (item, kv head), 4 waves. The item's query vectors (query
+// qi = row k * G + head g) are taken 16 at a time (a tile); for each tile, wave
+// w runs the chunk's pages w, w + 4, ... (a page subset fixed by the page's
+// place in the chunk, whatever the item's rows) and the four subsets' states
+// are combined in LDS in subset order. Lane (j, kq) = (lane % 16, lane / 16).
+// DIRECT: every row of the launch has one chunk; the item normalizes and
+// writes the final output (gate, out / prepared operands) itself.
+constexpr int kSubsets = 4;
+
+template <int HD>
+struct ItemLds {
+  float o[kSubsets][16][HD];  // subset states: unnormalized O per query
+  float m[kSubsets][16], l[kSubsets][16];
+};
+
+template <int HD, bool DIRECT>
+__global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict__ q, const float* __restrict__ gate,
+                                                        float* __restrict__ out, AttnLayout L, RowMeta m,
+                                                        AttnPlan plan, int G, float* __restrict__ part_o,
+                                                        float* __restrict__ part_ml, a8act::Dst act) {
+  constexpr int T = HD / 4;    // QK k-steps; lane (i, kq) holds d = T kq + t
+  constexpr int NT = HD / 16;  // PV n-tiles; lane (j, kq) holds d = NT j + nt
+  __shared__ __attribute__((aligned(16))) ItemLds<HD> sh;
+  const int item = blockIdx.x, kvh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, kq = lane >> 4;
+  const int* it = plan.items + (size_t)item * kItemFields;
+  const int page_off = it[0], npages = it[1], row_off = it[2], nrows = it[3], chunk = it[4];
+  const int nq = nrows * G;
+  const int chunk_pos0 = chunk * kChunkPages * L.block;
+  const float inv_scale = 1.0f / sqrtf((float)HD);
+  // this wave's pages: w, w + 4, ... (none when the chunk has fewer pages)
+  const int my_pages = npages > wave ? (npages - wave + kSubsets - 1) / kSubsets : 0;
+  auto page_base = [&](int k) {  // k-th page of this wave, clamped to its last one
+    const int pi = wave + kSubsets * min(k, max(my_pages - 1, 0));
+    const int page = plan.pages[page_off + min(pi, npages - 1)];
+    return ((size_t)page * L.kv_heads + kvh) * L.block * HD;
+  };
+
+  for (int t0 = 0; t0 < nq; t0 += 16) {
+    // this lane's query vector n = j: Q[n][T kq + t] (zero past the item's queries)
+    const int qi = t0 + j;
+    const bool qlive = qi < nq;
+    const int krow = qlive ? qi / G : 0, g = qlive ? qi % G : 0;
+    const int row = plan.item_rows[row_off + krow];
+    const int len = m.pos_of_row[row] + 1;  // positions [0, len) are visible
+    float Q[T];
+    {
+      const float* qp = q + ((size_t)row * L.heads + kvh * G + g) * HD + T * kq;
+#pragma unroll
+      for (int t = 0; t < T; t += 4) {
+        const float4 v = qlive ? *reinterpret_cast<const float4*>(qp + t) : make_float4(0.f, 0.f, 0.f, 0.f);
+        Q[t] = v.x;
+        Q[t + 1] = v.y;
+        Q[t + 2] = v.z;
+        Q[t + 3] = v.w;
+      }
+    }
+    float mx = -INFINITY, lsum = 0.0f;  // of query j (replicated over kq)
+    f4 O[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) O[nt] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    // K and V of a page in registers: lane (j, kq) holds K[p = j][T kq + t] and
+    // V[4 kq + s][NT j + nt]. Software pipeline: the next page's K is issued
+    // once this page's scores are done, its V once this page's P V is done
+    // (the last page re-reads itself, an L2 hit): no load waits behind a branch.
+    float Kr[T], Vr[4][NT];
+    auto load_k = [&](size_t base) {
+      const float* kp = L.k_pool + base + (size_t)j * HD + T * kq;
+#pragma unroll
+      for (int e = 0; e < T; e += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(kp + e);
+        Kr[e] = v.x;
+        Kr[e + 1] = v.y;
+        Kr[e + 2] = v.z;
+        Kr[e + 3] = v.w;
+      }
+    };
+    auto load_v = [&](size_t base) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float* vp = L.v_pool + base + (size_t)(4 * kq + s) * HD + NT * j;
+#pragma unroll
+        for (int e = 0; e < NT; e += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(vp + e);
+          Vr[s][e] = v.x;
+          Vr[s][e + 1] = v.y;
+          Vr[s][e + 2] = v.z;
+          Vr[s][e + 3] = v.w;
+        }
+      }
+    };
+    load_k(page_base(0));
+    load_v(page_base(0));
+    for (int k = 0; k < my_pages; ++k) {
+      // ---- S = K Q^T: A = K[p = j][T kq + t], B = Q[n = j][T kq + t]; four
+      // independent accumulators (t mod 4), added pairwise ----
+      f4 Sa[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int t = 0; t < T; ++t) Sa[t & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(Kr[t], Q[t], Sa[t & 3], 0, 0, 0);
+      const f4 S = (Sa[0] + Sa[1]) + (Sa[2] + Sa[3]);
+      load_k(page_base(k + 1));
+      // lane (j, kq) holds S[p = 4 kq + r][n = j]
+      const int pos0 = chunk_pos0 + (wave + kSubsets * k) * L.block + 4 * kq;
+      float sc[4];
+      float pm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[r] = pos0 + r < len ? S[r] * inv_scale : -INFINITY;
+        pm = fmaxf(pm, sc[r]);
+      }
+      pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
+      pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+      // a page past a live query's length (its last page is w's, not this one)
+      // leaves the state as it is
+      const float mn = fmaxf(mx, pm);
+      const float alpha = mn == -INFINITY ? 1.0f : expf(mx - mn);
+      float ps = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[r] = (qlive && sc[r] != -INFINITY) ? expf(sc[r] - mn) : 0.0f;
+        ps += sc[r];
+      }
+      ps += __shfl_xor(ps, 16, 64);
+      ps += __shfl_xor(ps, 32, 64);
+      lsum = lsum * alpha + ps;
+      mx = mn;
+      // O rows of this lane are queries 4 kq + r; their alphas live in lanes 4 kq + r
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float al = __shfl(alpha, 4 * kq + r, 64);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) O[nt][r] *= al;
+      }
+      // ---- O += P V: A = P[n = j][p = 4 kq + s] (= sc[s]), B = V[4 kq + s][NT j + nt] ----
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) O[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[s], Vr[s][nt], O[nt], 0, 0, 0);
+      load_v(page_base(k + 1));
+    }
+    // ---- subset state to LDS: lane (j, kq) holds O[query 4 kq + r][NT j + nt] ----
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int e = 0; e < NT; e += 4)
+        *reinterpret_cast<float4*>(&sh.o[wave][4 * kq + r][NT * j + e]) =
+            make_float4(O[e][r], O[e + 1][r], O[e + 2][r], O[e + 3][r]);
+    if (kq == 0) {
+      sh.m[wave][j] = mx;
+      sh.l[wave][j] = lsum;
+    }
+    __syncthreads();
+    // ---- combine the subsets in order; thread = (query n, 16 dims) ----
+    constexpr int SL = HD / 16;  // 16-dim slices per query
+    for (int u = tid; u < 16 * SL; u += 256) {
+      const int n = u / SL, d0 = (u % SL) * 16;
+      const int qo = t0 + n;
+      const bool live = qo < nq;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kSubsets; ++w) M = fmaxf(M, sh.m[w][n]);
+      float lt = 0.0f, v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kSubsets; ++w) {
+        if (sh.m[w][n] == -INFINITY) continue;  // no visible position in this subset
+        const float wt = expf(sh.m[w][n] - M);
+        lt += sh.l[w][n] * wt;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] += sh.o[w][n][d0 + e] * wt;
+      }
+      const int orow = plan.item_rows[row_off + (live ? qo / G : 0)], head = kvh * G + (live ? qo % G : 0);
+      if constexpr (DIRECT) {
+        const size_t oo = ((size_t)orow * L.heads + head) * HD + d0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          v[e] = v[e] / lt;
+          if (gate && live) v[e] *= 1.0f / (1.0f + expf(-gate[oo + e]));
+        }
+        if (out && live) {
+#pragma unroll
+          for (int e = 0; e < 16; e += 4)
+            *reinterpret_cast<float4*>(out + oo + e) = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
+        }
+        if (act.XA) {
+          // one 16-dim slice of the o projection's input; thread u ^ 1 holds the
+          // neighbouring slice of the same 64-wide group (HD >= 64, SL even)
+          const int col = head * HD + d0;
+          a8act::emit_slice(act, orow, col >> 6, (col >> 4) & 3, v, live);
+        }
+      } else if (live) {
+        const int slot = row_off + qo / G, go = qo % G;
+        float* po = part_o + (((size_t)slot * L.kv_heads + kvh) * G + go) * HD + d0;
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) *reinterpret_cast<float4*>(po + e) = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
+        if (d0 == 0) {
+          float* pml = part_ml + (((size_t)slot * L.kv_heads + kvh) * G + go) * 2;
+          pml[0] = M;
+          pml[1] = lt;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// merge kernel: workgroup (row, kv head), 256 threads over the G x HD outputs
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ gate, float* __restrict__ out,
+                                                         AttnLayout L, AttnPlan plan, int G,
+                                                         const float* __restrict__ part_o,
+                                                         const float* __restrict__ part_ml, a8act::Dst act) {
+  extern __shared__ __attribute__((aligned(16))) float obuf[];  // [G * HD]
+  const int r = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+  const int s0 = plan.row_slot_off[r], ns = plan.row_slot_off[r + 1] - s0;
+  for (int e = tid; e < G * HD; e += 256) {
+    const int g = e / HD;
+    float M = -INFINITY;
+    for (int i = 0; i < ns; ++i) {
+      const int slot = plan.row_slots[s0 + i];
+      M = fmaxf(M, part_ml[(((size_t)slot * L.kv_heads + kvh) * G + g) * 2]);
+    }
+    float lt = 0.0f, o = 0.0f;
+    for (int i = 0; i < ns; ++i) {
+      const int slot = plan.row_slots[s0 + i];
+      const float* ml = part_ml + (((size_t)slot * L.kv_heads + kvh) * G + g) * 2;
+      const float w = expf(ml[0] - M);
+      lt += ml[1] * w;
+      o += part_o[((size_t)slot * L.kv_heads + kvh) * G * HD + e] * w;
+    }
+    float res = o / lt;
+    const size_t oo = ((size_t)r * L.heads + kvh * G) * HD + e;
+    if (gate) res *= 1.0f / (1.0f + expf(-gate[oo]));
+    if (out) out[oo] = res;
+    if (act.XA) obuf[e] = res;
+  }
+  if (act.XA) {
+    // the group's G heads are whole groups of the o projection's input
+    __syncthreads();
+    const int SL = G * HD / 16;
+    for (int u0 = 0; u0 < SL; u0 += 256) {
+      const int u = u0 + tid;
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = u < SL ? obuf[16 * u + e] : 0.0f;
+      const int col = kvh * G * HD + 16 * u;
+      a8act::emit_slice(act, r, col >> 6, (col >> 4) & 3, v, u < SL);
+    }
+  }
+}
+
+template <int HD>
+void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m,
+             const AttnPlan& plan, int rows, hipStream_t s, const a8act::Dst& act) {
+  const int G = L.heads / L.kv_heads;
+  const size_t o_floats = (size_t)plan.n_slots * L.kv_heads * G * HD;
+  const size_t ml_floats = (size_t)plan.n_slots * L.kv_heads * G * 2;
+  // one chunk per row (n_slots == rows): the items finish the rows themselves
+  if (plan.n_slots == rows) {
+    hipLaunchKernelGGL((attn_item_kernel<HD, true>), dim3(plan.n_items, L.kv_heads), dim3(256), 0, s, q, gate, out,
+                       L, m, plan, G, nullptr, nullptr, act);
+    return;
+  }
+  float* ws = static_cast<float*>(gemv::gemv_scratch(s, (o_floats + ml_floats) * sizeof(float), 4));
+  hipLaunchKernelGGL((attn_item_kernel<HD, false>), dim3(plan.n_items, L.kv_heads), dim3(256), 0, s, q, gate, out,
+                     L, m, plan, G, ws, ws + o_floats, act);
+  hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(rows, L.kv_heads), dim3(256), (size_t)G * HD * sizeof(float), s,
+                     gate, out, L, plan, G, ws, ws + o_floats, act);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// host: plan
+// ---------------------------------------------------------------------------
+void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, const int* block_tables,
+                     int max_blocks, int block, int group, std::vector<int>& out) {
+  PGD_CHECK(group > 0 && group <= 64 && block == 16, kErrShape, "attention plan: group <= 64 heads, pages of 16");
+  const int max_rows = 64 / group;  // query vectors per item <= 64
+  struct Key {
+    int chunk;
+    std::vector<int> pages;
+    bool operator==(const Key& o) const { return chunk == o.chunk && pages == o.pages; }
+  };
+  struct KeyHash {
+    size_t operator()(const Key& k) const {
+      size_t h = std::hash<int>()(k.chunk) * 0x9e3779b97f4a7c15ull;
+      for (int p : k.pages) h = (h ^ (size_t)(unsigned)p) * 0x100000001b3ull;
+      return h;
+    }
+  };
+  std::unordered_map<Key, int, KeyHash> index;  // key -> group id
+  std::vector<Key> keys;
+  std::vector<std::vector<int>> members;        // rows of each group, in row order
+  std::vector<std::vector<int>> row_chunk_group(rows);
+  for (int r = 0; r < rows; ++r) {
+    const int npages = pos_of_row[r] / block + 1;
+    PGD_CHECK(npages <= max_blocks, kErrShape, "attention plan: position past the block table");
+    const int* bt = block_tables + (size_t)seq_of_row[r] * max_blocks;
+    const int nch = (npages + kChunkPages - 1) / kChunkPages;
+    for (int c = 0; c < nch; ++c) {
+      Key k{c, std::vector<int>(bt + c * kChunkPages, bt + std::min(npages, (c + 1) * kChunkPages))};
+      auto f = index.find(k);
+      int gid;
+      if (f == index.end()) {
+        gid = (int)keys.size();
+        index.emplace(k, gid);
+        keys.push_back(std::move(k));
+        members.emplace_back();
+      } else {
+        gid = f->second;
+      }
+      members[gid].push_back(r);
+      row_chunk_group[r].push_back(gid);
+    }
+  }
+  // items: each group's rows in runs of max_rows
+  std::vector<int> items, pages, item_rows;
+  std::vector<std::vector<int>> group_slot0(keys.size());  // slot of each member
+  for (size_t gi = 0; gi < keys.size(); ++gi) {
+    const int page_off = (int)pages.size();
+    pages.insert(pages.end(), keys[gi].pages.begin(), keys[gi].pages.end());
+    const auto& mem = members[gi];
+    for (size_t k0 = 0; k0 < mem.size(); k0 += max_rows) {
+      const int nr = (int)std::min<size_t>(max_rows, mem.size() - k0);
+      items.insert(items.end(), {page_off, (int)keys[gi].pages.size(), (int)item_rows.size(), nr, keys[gi].chunk});
+      for (int k = 0; k < nr; ++k) {
+        group_slot0[gi].push_back((int)item_rows.size());
+        item_rows.push_back(mem[k0 + k]);
+      }
+    }
+  }
+  // row -> slots in chunk order
+  std::vector<int> row_slot_off(rows + 1), row_slots;
+  std::vector<size_t> cursor(keys.size(), 0);
+  for (int r = 0; r < rows; ++r) {
+    row_slot_off[r] = (int)row_slots.size();
+    for (int gid : row_chunk_group[r]) row_slots.push_back(group_slot0[gid][cursor[gid]++]);
+  }
+  row_slot_off[rows] = (int)row_slots.size();
+  // layout: header {n_items, n_slots, off_items, off_pages, off_item_rows, off_row_slot_off, off_row_slots}
+  const int hdr = 8;
+  out.assign(hdr, 0);
+  out[0] = (int)(items.size() / kItemFields);
+  out[1] = (int)item_rows.size();
+  auto put = [&](int field, const std::vector<int>& v) {
+    out[field] = (int)out.size();
+    out.insert(out.end(), v.begin(), v.end());
+  };
+  put(2, items);
+  put(3, pages);
+  put(4, item_rows);
+  put(5, row_slot_off);
+  put(6, row_slots);
+}
+
+AttnPlan attn_plan_view(const int* host, const int* dev) {
+  AttnPlan p;
+  p.n_items = host[0];
+  p.n_slots = host[1];
+  p.items = dev + host[2];
+  p.pages = dev + host[3];
+  p.item_rows = dev + host[4];
+  p.row_slot_off = dev + host[5];
+  p.row_slots = dev + host[6];
+  return p;
+}
+
+void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m,
+                 const AttnPlan& plan, int rows, hipStream_t s, const a8act::Dst* act) {
+  PGD_CHECK(L.kv_heads > 0 && L.heads % L.kv_heads == 0, kErrShape, "heads must be a multiple of kv_heads");
+  PGD_CHECK(L.heads / L.kv_heads <= 64, kErrShape, "GQA group of at most 64 heads");
+  PGD_CHECK(L.block == 16, kErrShape, "attention pages hold 16 positions");
+  PGD_CHECK(out || act, kErrArg, "attention needs an output");
+  if (rows <= 0) return;
+  const a8act::Dst d = act ? *act : a8act::Dst{nullptr, nullptr, 0, 0};
+  if (act) PGD_CHECK(act->G * 64 == L.heads * L.head_dim && act->rows == rows, kErrShape, "prepared attention output");
+  switch (L.head_dim) {
+    case 64: attn_hd<64>(q, gate, out, L, m, plan, rows, s, d); break;
+    case 128: attn_hd<128>(q, gate, out, L, m, plan, rows, s, d); break;
+    case 256: attn_hd<256>(q, gate, out, L, m, plan, rows, s, d); break;
+    default: throw Error{kErrShape, "attention head_dim must be 64, 128 or 256"};
+  }
+  PGD_HIP(hipGetLastError());
+}
+
+}  // namespace pgd

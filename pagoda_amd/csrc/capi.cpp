@@ -1,6 +1,7 @@
 // capi.cpp — extern "C" surface: devices, matrices and the error channel.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -322,7 +323,26 @@ int pgd_attn_decode_dev(pgd_dev* dev, int heads, int kv_heads, int head_dim, int
     DeviceScope scope(dev);
     AttnLayout L{heads, kv_heads, head_dim, head_dim, block, const_cast<float*>(k_pool), const_cast<float*>(v_pool)};
     RowMeta m{seq_of_row, pos_of_row, block_tables, max_blocks, nullptr, nullptr};
-    attn_decode(q, gate, out, L, m, rows, dev->stream);
+    if (rows == 0) return;
+    PGD_CHECK(kv_heads > 0 && heads % kv_heads == 0, kErrShape, "heads must be a multiple of kv_heads");
+    // the plan is built from the row metadata on the host
+    std::vector<int> h_seq(rows), h_pos(rows);
+    PGD_HIP(hipStreamSynchronize(dev->stream));
+    PGD_HIP(hipMemcpy(h_seq.data(), seq_of_row, rows * sizeof(int), hipMemcpyDeviceToHost));
+    PGD_HIP(hipMemcpy(h_pos.data(), pos_of_row, rows * sizeof(int), hipMemcpyDeviceToHost));
+    int nseq = 0;
+    for (int v : h_seq) {
+      PGD_CHECK(v >= 0, kErrArg, "negative sequence index");
+      nseq = std::max(nseq, v + 1);
+    }
+    std::vector<int> h_bt((size_t)nseq * max_blocks);
+    PGD_HIP(hipMemcpy(h_bt.data(), block_tables, h_bt.size() * sizeof(int), hipMemcpyDeviceToHost));
+    std::vector<int> plan;
+    build_attn_plan(h_seq.data(), h_pos.data(), rows, h_bt.data(), max_blocks, block, heads / kv_heads, plan);
+    DevBuf d_plan(plan.size() * sizeof(int));
+    PGD_HIP(hipMemcpy(d_plan.p, plan.data(), plan.size() * sizeof(int), hipMemcpyHostToDevice));
+    attn_decode(q, gate, out, L, m, attn_plan_view(plan.data(), d_plan.as<int>()), rows, dev->stream);
+    PGD_HIP(hipStreamSynchronize(dev->stream));
   });
 }
 

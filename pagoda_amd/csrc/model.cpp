@@ -354,6 +354,27 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   }
   m.ensure_rope(max_pos);
   const int rd = c.rotary_dim;
+  // ---- attention plan (same for every full-attention layer) ----
+  std::vector<int>& plan = m.plan_host;
+  {
+    std::vector<int>& p_seq = m.plan_seq;
+    std::vector<int>& p_pos = m.plan_pos;
+    std::vector<int>& p_bt = m.plan_bt;
+    p_seq.resize(rows);
+    p_pos.resize(rows);
+    p_bt.assign((size_t)nseq * max_blocks, 0);
+    int r = 0;
+    for (int i = 0; i < nseq; ++i) {
+      const Session* ss = sess[i];
+      for (size_t b = 0; b < ss->blocks.size(); ++b) p_bt[i * max_blocks + b] = ss->blocks[b];
+      for (int t = 0; t < n[i]; ++t, ++r) {
+        p_seq[r] = i;
+        p_pos[r] = ss->len + t;
+      }
+    }
+    build_attn_plan(p_seq.data(), p_pos.data(), rows, p_bt.data(), (int)max_blocks, c.kv_block, c.heads / c.kv_heads,
+                    plan);
+  }
   // ---- host metadata, one upload ----
   size_t off_seq = 0;
   size_t off_pos = align_up(off_seq + rows * 4, 256);
@@ -365,7 +386,8 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   size_t off_sb = align_up(off_tok + rows * 4, 256);
   size_t off_cos = align_up(off_sb + nseq * 8, 256);
   size_t off_sin = align_up(off_cos + (size_t)rows * rd * 4, 256);
-  size_t meta_bytes = align_up(off_sin + (size_t)rows * rd * 4, 256);
+  size_t off_plan = align_up(off_sin + (size_t)rows * rd * 4, 256);
+  size_t meta_bytes = align_up(off_plan + plan.size() * 4, 256);
   if (m.meta_host_cap < meta_bytes) {
     if (m.meta_host) {
       PGD_HIP(hipStreamSynchronize(st));
@@ -391,6 +413,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   float** h_sb = (float**)(hb + off_sb);
   float* h_cos = (float*)(hb + off_cos);
   float* h_sin = (float*)(hb + off_sin);
+  memcpy(hb + off_plan, plan.data(), plan.size() * 4);
   {
     int r = 0, lr = 0;
     for (int i = 0; i < nseq; ++i) {
@@ -420,6 +443,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   float* const* d_sb = (float* const*)(db + off_sb);
   RowMeta rm{d_seq, d_pos, (const int*)(db + off_bt), (int)max_blocks, (const float*)(db + off_cos),
              (const float*)(db + off_sin)};
+  const AttnPlan ap = attn_plan_view(plan.data(), (const int*)(db + off_plan));
 
   // ---- forward ----
   Ws w = carve_ws(m, rows, lrows);
@@ -504,10 +528,10 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
         // attention writes the o projection's operands itself
         const A8Act act = a8_act_view(w.act, rows, c.heads * c.head_dim);
         const a8act::Dst dst = a8_act_dst(act);
-        attn_decode(w.D, w.F, nullptr, al, rm, rows, st, &dst);
+        attn_decode(w.D, w.F, nullptr, al, rm, ap, rows, st, &dst);
         qmat_gemv_a8(L.o, act, w.x, H, w.x, H, st);
       } else {
-        attn_decode(w.D, nullptr, w.E, al, rm, rows, st);
+        attn_decode(w.D, nullptr, w.E, al, rm, ap, rows, st);
         qmat_gemv(L.o, w.E, 0, c.heads * c.head_dim, rows, w.x, H, w.x, H, st);
       }
     }

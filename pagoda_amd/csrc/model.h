@@ -72,6 +72,7 @@ struct Model {
   size_t meta_cap = 0;
   void* meta_host = nullptr;  // pinned
   size_t meta_host_cap = 0;
+  std::vector<int> plan_host, plan_seq, plan_pos, plan_bt;  // attention plan of the current step
   DevBuf out_dev;  // ids / values / non-finite counts
   size_t out_cap = 0;
   void* out_host = nullptr;

@@ -4,6 +4,7 @@
 // `rows` token rows that belong to `nseq` sequences, sequence s owning rows
 // [row_start[s], row_start[s] + row_count[s]) in feed order.
 #pragma once
+#include <vector>
 
 #include "a8_act.h"
 #include <hip/hip_runtime.h>
@@ -99,9 +100,25 @@ void qkv_prep(const QkvPrep& p, const AttnLayout& L, const RowMeta& m, int rows,
 
 // Paged GQA decode attention: row r attends to positions [0, pos_of_row[r]]
 // of its sequence. out [rows, heads, hd]; gate (nullable) multiplies by
-// sigmoid(gate) (qwen3_5.rs:1433-1475; qwen2_gguf.rs:252-266).
-void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
-                 hipStream_t s, const a8act::Dst* act = nullptr);
+// sigmoid(gate) (qwen3_5.rs:1433-1475; qwen2_gguf.rs:252-266). Work is cut
+// into chunks of kChunkPages pages; rows whose chunk holds the same physical
+// pages share one work item (the plan), so shared pages are read once.
+constexpr int kChunkPages = 16;
+struct AttnPlan {
+  int n_items, n_slots;
+  const int* items;         // [n_items][5]: page_off, npages, row_off, nrows, chunk
+  const int* pages;         // page ids of the items' chunks
+  const int* item_rows;     // rows of the items; index = partial slot
+  const int* row_slot_off;  // [rows + 1]
+  const int* row_slots;     // each row's slots in chunk order
+};
+// Plan of one step as one int array (header + sections); the same array is
+// uploaded as is, and attn_plan_view maps the host header onto its device copy.
+void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, const int* block_tables,
+                     int max_blocks, int block, int group, std::vector<int>& out);
+AttnPlan attn_plan_view(const int* host, const int* dev);
+void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m,
+                 const AttnPlan& plan, int rows, hipStream_t s, const a8act::Dst* act = nullptr);
 
 // Row-wise argmax over finite values. last_max = 0: first index among equal
 // maxima (pagoda/src/sampler.rs:59-69); 1: last (Iterator::max_by,

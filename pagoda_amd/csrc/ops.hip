@@ -1,5 +1,5 @@
 // ops.hip — RMSNorm, causal conv step, Gated-DeltaNet recurrence, q/k/v
-// preparation with paged KV writes, paged GQA decode attention and argmax.
+// preparation with paged KV writes and argmax (attention: attn.hip).
 #include "common.h"
 #include "ops.h"
 #include "gemv_impl.h"
@@ -268,114 +268,6 @@ __global__ __launch_bounds__(64) void qkv_prep_kernel(QkvPrep p, AttnLayout L, R
   }
 }
 
-// ---------------------------------------------------------------------------
-// paged GQA decode attention
-// ---------------------------------------------------------------------------
-// Workgroup (kv head, row), 4 waves. A position is LP = hd/4 lanes (float4
-// each); a wave covers PPW = 64/LP positions per step. Each lane group keeps
-// an online softmax per q head of the GQA group; groups are merged in LDS.
-template <int HD, int G>
-__global__ __launch_bounds__(256) void attn_kernel(const float* __restrict__ q, const float* __restrict__ gate,
-                                                   float* __restrict__ out, AttnLayout L, RowMeta m, a8act::Dst act) {
-  constexpr int LP = HD / 4;
-  constexpr int PPW = 64 / LP;
-  constexpr int NG = 4 * PPW;  // position groups per workgroup
-  __shared__ float s_m[NG][G], s_l[NG][G];
-  __shared__ float4 s_acc[NG][G][LP];
-  __shared__ __attribute__((aligned(16))) float obuf[G * HD];
-  const int kvh = blockIdx.x, r = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int grp = wave * PPW + lane / LP;  // position group
-  const int sub = lane % LP;               // float4 slot within the head
-  const int seq = m.seq_of_row[r];
-  const int len = m.pos_of_row[r] + 1;
-  const int* bt = m.block_tables + (size_t)seq * m.max_blocks;
-  const float scale = sqrtf((float)HD);
-  float4 qv[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-    qv[g] = *reinterpret_cast<const float4*>(q + ((size_t)r * L.heads + kvh * G + g) * HD + 4 * sub);
-  float mx[G], l[G];
-  float4 acc[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    mx[g] = -INFINITY;
-    l[g] = 0.0f;
-    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  for (int p0 = grp; p0 < len; p0 += NG) {
-    const int blk = bt[p0 / L.block];
-    const size_t off = (((size_t)blk * L.kv_heads + kvh) * L.block + (p0 % L.block)) * HD + 4 * sub;
-    const float4 kk = *reinterpret_cast<const float4*>(L.k_pool + off);
-    const float4 vv = *reinterpret_cast<const float4*>(L.v_pool + off);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float d = qv[g].x * kk.x + qv[g].y * kk.y + qv[g].z * kk.z + qv[g].w * kk.w;
-      d = group_sum(d, LP);
-      const float sc = d / scale;
-      const float mn = fmaxf(mx[g], sc);
-      const float al = expf(mx[g] - mn);
-      const float e = expf(sc - mn);
-      l[g] = l[g] * al + e;
-      acc[g].x = acc[g].x * al + e * vv.x;
-      acc[g].y = acc[g].y * al + e * vv.y;
-      acc[g].z = acc[g].z * al + e * vv.z;
-      acc[g].w = acc[g].w * al + e * vv.w;
-      mx[g] = mn;
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (sub == 0) {
-      s_m[grp][g] = mx[g];
-      s_l[grp][g] = l[g];
-    }
-    s_acc[grp][g][sub] = acc[g];
-  }
-  __syncthreads();
-  for (int i = tid; i < G * LP; i += 256) {
-    const int g = i / LP, sl = i % LP;
-    float M = -INFINITY;
-    for (int k = 0; k < NG; ++k) M = fmaxf(M, s_m[k][g]);
-    float Lsum = 0.0f;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = 0; k < NG; ++k) {
-      if (s_l[k][g] == 0.0f) continue;
-      const float w = expf(s_m[k][g] - M);
-      Lsum += s_l[k][g] * w;
-      const float4 a = s_acc[k][g][sl];
-      o.x += a.x * w;
-      o.y += a.y * w;
-      o.z += a.z * w;
-      o.w += a.w * w;
-    }
-    const int head = kvh * G + g;
-    const size_t oo = ((size_t)r * L.heads + head) * HD + 4 * sl;
-    float4 res = make_float4(o.x / Lsum, o.y / Lsum, o.z / Lsum, o.w / Lsum);
-    if (gate) {
-      const float4 gg = *reinterpret_cast<const float4*>(gate + oo);
-      res.x *= 1.0f / (1.0f + expf(-gg.x));
-      res.y *= 1.0f / (1.0f + expf(-gg.y));
-      res.z *= 1.0f / (1.0f + expf(-gg.z));
-      res.w *= 1.0f / (1.0f + expf(-gg.w));
-    }
-    if (out) *reinterpret_cast<float4*>(out + oo) = res;
-    if (act.XA) *reinterpret_cast<float4*>(&obuf[g * HD + 4 * sl]) = res;
-  }
-  if (act.XA) {
-    // the group's G heads are whole groups of the o projection's input
-    __syncthreads();
-    constexpr int SL = G * HD / 16;
-    for (int u0 = 0; u0 < SL; u0 += 256) {
-      const int u = u0 + tid;
-      float v[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = u < SL ? obuf[16 * u + e] : 0.0f;
-      const int col = kvh * G * HD + 16 * u;
-      a8act::emit_slice(act, r, col >> 6, (col >> 4) & 3, v, u < SL);
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // argmax
@@ -494,38 +386,6 @@ void qkv_prep(const QkvPrep& p, const AttnLayout& L, const RowMeta& m, int rows,
   PGD_CHECK(L.rotary_dim % 2 == 0 && L.rotary_dim <= L.head_dim, kErrShape, "rotary_dim");
   if (rows <= 0) return;
   hipLaunchKernelGGL(qkv_prep_kernel, dim3(L.heads + L.kv_heads, rows), dim3(64), 0, s, p, L, m);
-  PGD_HIP(hipGetLastError());
-}
-
-template <int HD>
-static void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
-                    hipStream_t s, const a8act::Dst& act) {
-  const int G = L.heads / L.kv_heads;
-  dim3 grid(L.kv_heads, rows);
-  switch (G) {
-    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
-    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
-    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
-    case 6: hipLaunchKernelGGL((attn_kernel<HD, 6>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
-    case 7: hipLaunchKernelGGL((attn_kernel<HD, 7>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
-    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, s, q, gate, out, L, m, act); break;
-    default: throw Error{kErrShape, "unsupported GQA group size " + std::to_string(G)};
-  }
-}
-
-void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m, int rows,
-                 hipStream_t s, const a8act::Dst* act) {
-  PGD_CHECK(L.kv_heads > 0 && L.heads % L.kv_heads == 0, kErrShape, "heads must be a multiple of kv_heads");
-  PGD_CHECK(out || act, kErrArg, "attention needs an output");
-  if (rows <= 0) return;
-  const a8act::Dst d = act ? *act : a8act::Dst{nullptr, nullptr, 0, 0};
-  if (act) PGD_CHECK(act->G * 64 == L.heads * L.head_dim && act->rows == rows, kErrShape, "prepared attention output");
-  switch (L.head_dim) {
-    case 64: attn_hd<64>(q, gate, out, L, m, rows, s, d); break;
-    case 128: attn_hd<128>(q, gate, out, L, m, rows, s, d); break;
-    case 256: attn_hd<256>(q, gate, out, L, m, rows, s, d); break;
-    default: throw Error{kErrShape, "attention head_dim must be 64, 128 or 256"};
-  }
   PGD_HIP(hipGetLastError());
 }
 

@@ -157,3 +157,70 @@ def test_paged_attention_ragged(dev, heads, kvh, hd):
         assert rel(out[r], ref) < TOL, (r, rel(out[r], ref))
     for p in bufs + [d_out]:
         dev.free(p)
+
+
+@pytest.mark.parametrize("heads,kvh,hd", [(24, 4, 256), (14, 2, 64)])
+def test_paged_attention_shared_trunk(dev, heads, kvh, hd):
+    """Forked sequences over one shared trunk (the block tables hold the same
+    page ids, as after Session::fork / the radix cache) plus private suffix
+    pages, with 4-token verify rows: rows sharing a chunk's pages share one
+    work item (more rows than one item holds), and every row equals the
+    oracle and, bitwise, the same row attended alone."""
+    from pagoda_amd._lib import call
+    import ctypes as C
+
+    rng = np.random.default_rng(hd + 3)
+    block, trunk = 16, 40  # 640 trunk positions: chunks 0, 1 and part of 2
+    nseq = 13
+    total_pages = trunk + nseq * 3 + 5
+    kpool = rng.normal(0, 1, (total_pages, kvh, block, hd)).astype(np.float32)
+    vpool = rng.normal(0, 1, (total_pages, kvh, block, hd)).astype(np.float32)
+    free = list(rng.permutation(np.arange(trunk, total_pages)))
+    trunk_pages = list(rng.permutation(trunk))
+    tables, seq_of_row, pos_of_row = [], [], []
+    for i in range(nseq):
+        extra = 1 + i % 3  # private pages after the trunk
+        tables.append(trunk_pages + [int(free.pop()) for _ in range(extra)])
+        last = trunk * block + extra * block - 1 - (i % 7)
+        # a decode row, or a 4-token verify chunk for every third sequence
+        for t in (range(4) if i % 3 == 0 else range(1)):
+            seq_of_row.append(i)
+            pos_of_row.append(last - 3 + t if i % 3 == 0 else last)
+    seq_of_row.append(2)  # a row inside the trunk
+    pos_of_row.append(300)
+    rows = len(seq_of_row)
+    max_blocks = max(len(t) for t in tables)
+    bt = np.zeros((nseq, max_blocks), np.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = t
+    q = rng.normal(0, 1, (rows, heads, hd)).astype(np.float32)
+    gate = rng.normal(0, 1, (rows, heads, hd)).astype(np.float32)
+    pools = [dev.upload(kpool), dev.upload(vpool), dev.upload(bt)]
+
+    def run(rsel):
+        qs, gs = np.ascontiguousarray(q[rsel]), np.ascontiguousarray(gate[rsel])
+        bufs = [dev.upload(qs), dev.upload(gs), pools[0], pools[1],
+                dev.upload(np.asarray([seq_of_row[r] for r in rsel], np.int32)),
+                dev.upload(np.asarray([pos_of_row[r] for r in rsel], np.int32)), pools[2]]
+        d_out = dev.alloc(len(rsel) * heads * hd * 4)
+        call("pgd_attn_decode_dev", dev.handle, heads, kvh, hd, block, *[C.c_void_p(p) for p in bufs], max_blocks,
+             len(rsel), C.c_void_p(d_out))
+        got = dev.download(d_out, (len(rsel), heads, hd), np.float32)
+        for p in [bufs[0], bufs[1], bufs[4], bufs[5], d_out]:
+            dev.free(p)
+        return got
+
+    out = run(list(range(rows)))
+    for r in range(rows):
+        s, L = seq_of_row[r], pos_of_row[r] + 1
+        kc = np.zeros((L, kvh, hd), np.float32)
+        vc = np.zeros((L, kvh, hd), np.float32)
+        for p in range(L):
+            kc[p] = kpool[tables[s][p // block], :, p % block]
+            vc[p] = vpool[tables[s][p // block], :, p % block]
+        ref = ora.attn_decode(q[r], kc, vc, L, heads, kvh, hd, gate[r])
+        assert rel(out[r], ref) < TOL, (r, rel(out[r], ref))
+    for r in (0, 5, rows - 1):
+        np.testing.assert_array_equal(run([r])[0].view(np.uint32), out[r].view(np.uint32))
+    for p in pools:
+        dev.free(p)
