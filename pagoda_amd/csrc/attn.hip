@@ -11,8 +11,9 @@
 // context is cut into chunks of kChunkPages pages. Rows whose chunk holds the
 // same physical pages — requests forked from one trunk, the rows of one
 // sequence in a prefill or verify chunk — share one work item, so the chunk's
-// K/V is read once for all of them. An item holds at most 64 query vectors
-// (rows x group heads); each 16 of them are one wave.
+// K/V is read once for all of them (once per item of up to 16 query
+// vectors = rows x group heads; more sharers make more items, which the
+// chunk's K/V then feeds from L2).
 //
 // Item kernel, per page of the chunk (16 positions), per wave (the four waves
 // of an item take every fourth page and are combined in LDS):
@@ -29,6 +30,7 @@
 // last step itself and the merge is skipped (one launch for short contexts).
 // A row's result depends only on its own chunks, never on which rows shared
 // an item, so batched rows equal single-row calls bit for bit.
+#include <algorithm>
 #include <unordered_map>
 #include <vector>
 
@@ -260,46 +262,60 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // merge kernel: workgroup (row, kv head), 256 threads over the G x HD outputs
 // ---------------------------------------------------------------------------
+constexpr int kMergeMax = 1024;  // chunk slots per row, staged in LDS
+
+// Workgroup (row, kv head, group head g), thread = one of the head's HD dims.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ gate, float* __restrict__ out,
-                                                         AttnLayout L, AttnPlan plan, int G,
-                                                         const float* __restrict__ part_o,
-                                                         const float* __restrict__ part_ml, a8act::Dst act) {
-  extern __shared__ __attribute__((aligned(16))) float obuf[];  // [G * HD]
-  const int r = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+__global__ __launch_bounds__(HD) void attn_merge_kernel(const float* __restrict__ gate, float* __restrict__ out,
+                                                        AttnLayout L, AttnPlan plan, int G,
+                                                        const float* __restrict__ part_o,
+                                                        const float* __restrict__ part_ml, a8act::Dst act) {
+  __shared__ float s_w[kMergeMax];  // per slot: m, then exp(m - M)
+  __shared__ float s_l[kMergeMax];
+  __shared__ int s_slot[kMergeMax];
+  __shared__ float s_lt;
+  __shared__ __attribute__((aligned(16))) float obuf[HD];
+  const int r = blockIdx.x, kvh = blockIdx.y, g = blockIdx.z, d = threadIdx.x;
   const int s0 = plan.row_slot_off[r], ns = plan.row_slot_off[r + 1] - s0;
-  for (int e = tid; e < G * HD; e += 256) {
-    const int g = e / HD;
-    float M = -INFINITY;
-    for (int i = 0; i < ns; ++i) {
-      const int slot = plan.row_slots[s0 + i];
-      M = fmaxf(M, part_ml[(((size_t)slot * L.kv_heads + kvh) * G + g) * 2]);
-    }
-    float lt = 0.0f, o = 0.0f;
-    for (int i = 0; i < ns; ++i) {
-      const int slot = plan.row_slots[s0 + i];
-      const float* ml = part_ml + (((size_t)slot * L.kv_heads + kvh) * G + g) * 2;
-      const float w = expf(ml[0] - M);
-      lt += ml[1] * w;
-      o += part_o[((size_t)slot * L.kv_heads + kvh) * G * HD + e] * w;
-    }
-    float res = o / lt;
-    const size_t oo = ((size_t)r * L.heads + kvh * G) * HD + e;
-    if (gate) res *= 1.0f / (1.0f + expf(-gate[oo]));
-    if (out) out[oo] = res;
-    if (act.XA) obuf[e] = res;
+  // every slot's (m, l) in one round of loads
+  for (int i = d; i < ns; i += HD) {
+    const int slot = plan.row_slots[s0 + i];
+    s_slot[i] = slot;
+    const float* ml = part_ml + (((size_t)slot * L.kv_heads + kvh) * G + g) * 2;
+    s_w[i] = ml[0];
+    s_l[i] = ml[1];
   }
+  __syncthreads();
+  // in chunk order: M = max m, weights exp(m - M), l = sum l * weight
+  if (d == 0) {
+    float M = -INFINITY;
+    for (int i = 0; i < ns; ++i) M = fmaxf(M, s_w[i]);
+    float lt = 0.0f;
+    for (int i = 0; i < ns; ++i) {
+      const float w = expf(s_w[i] - M);
+      s_w[i] = w;
+      lt += s_l[i] * w;
+    }
+    s_lt = lt;
+  }
+  __syncthreads();
+  float o = 0.0f;
+#pragma unroll 8
+  for (int i = 0; i < ns; ++i) o += part_o[(((size_t)s_slot[i] * L.kv_heads + kvh) * G + g) * HD + d] * s_w[i];
+  float res = o / s_lt;
+  const size_t oo = ((size_t)r * L.heads + kvh * G + g) * HD + d;
+  if (gate) res *= 1.0f / (1.0f + expf(-gate[oo]));
+  if (out) out[oo] = res;
   if (act.XA) {
-    // the group's G heads are whole groups of the o projection's input
+    // the head's HD dims are whole 64-wide groups of the o projection's input
+    obuf[d] = res;
     __syncthreads();
-    const int SL = G * HD / 16;
-    for (int u0 = 0; u0 < SL; u0 += 256) {
-      const int u = u0 + tid;
+    if (d < HD / 16) {
       float v[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = u < SL ? obuf[16 * u + e] : 0.0f;
-      const int col = kvh * G * HD + 16 * u;
-      a8act::emit_slice(act, r, col >> 6, (col >> 4) & 3, v, u < SL);
+      for (int e = 0; e < 16; ++e) v[e] = obuf[16 * d + e];
+      const int col = (kvh * G + g) * HD + 16 * d;
+      a8act::emit_slice(act, r, col >> 6, (col >> 4) & 3, v, true);
     }
   }
 }
@@ -316,10 +332,11 @@ void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L,
                        L, m, plan, G, nullptr, nullptr, act);
     return;
   }
+  PGD_CHECK(plan.max_row_slots <= kMergeMax, kErrShape, "attention context too long for the merge");
   float* ws = static_cast<float*>(gemv::gemv_scratch(s, (o_floats + ml_floats) * sizeof(float), 4));
   hipLaunchKernelGGL((attn_item_kernel<HD, false>), dim3(plan.n_items, L.kv_heads), dim3(256), 0, s, q, gate, out,
                      L, m, plan, G, ws, ws + o_floats, act);
-  hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(rows, L.kv_heads), dim3(256), (size_t)G * HD * sizeof(float), s,
+  hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(rows, L.kv_heads, G), dim3(HD), 0, s,
                      gate, out, L, plan, G, ws, ws + o_floats, act);
 }
 
@@ -331,7 +348,9 @@ void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L,
 void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, const int* block_tables,
                      int max_blocks, int block, int group, std::vector<int>& out) {
   PGD_CHECK(group > 0 && group <= 64 && block == 16, kErrShape, "attention plan: group <= 64 heads, pages of 16");
-  const int max_rows = 64 / group;  // query vectors per item <= 64
+  // rows per item: one 16-query tile (a tile's result does not depend on the
+  // item's size, so this only trades shared K/V reads for parallelism)
+  const int max_rows = std::max(1, 16 / group);
   struct Key {
     int chunk;
     std::vector<int> pages;
@@ -398,6 +417,9 @@ void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, con
   out.assign(hdr, 0);
   out[0] = (int)(items.size() / kItemFields);
   out[1] = (int)item_rows.size();
+  int max_slots = 0;
+  for (int r = 0; r < rows; ++r) max_slots = std::max(max_slots, row_slot_off[r + 1] - row_slot_off[r]);
+  out[7] = max_slots;
   auto put = [&](int field, const std::vector<int>& v) {
     out[field] = (int)out.size();
     out.insert(out.end(), v.begin(), v.end());
@@ -418,6 +440,7 @@ AttnPlan attn_plan_view(const int* host, const int* dev) {
   p.item_rows = dev + host[4];
   p.row_slot_off = dev + host[5];
   p.row_slots = dev + host[6];
+  p.max_row_slots = host[7];
   return p;
 }
 

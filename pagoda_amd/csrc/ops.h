@@ -105,7 +105,7 @@ void qkv_prep(const QkvPrep& p, const AttnLayout& L, const RowMeta& m, int rows,
 // pages share one work item (the plan), so shared pages are read once.
 constexpr int kChunkPages = 16;
 struct AttnPlan {
-  int n_items, n_slots;
+  int n_items, n_slots, max_row_slots;
   const int* items;         // [n_items][5]: page_off, npages, row_off, nrows, chunk
   const int* pages;         // page ids of the items' chunks
   const int* item_rows;     // rows of the items; index = partial slot
