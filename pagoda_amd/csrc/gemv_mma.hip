@@ -93,8 +93,10 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
 
 // Fused RMSNorm (rms_zero, pagoda-hf/src/qwen3_5.rs:1736-1745) + activation
 // prep: one workgroup per output row; thread t owns 16-wide slices t, t+256,
-// ... (slice u = 4g + q), kept in registers between the two passes.
+// ... (slice u = 4g + q), kept in registers between the two passes together
+// with their norm weights, which are loaded with the row (one round trip).
 constexpr int kNormMaxSlices = 8;  // n <= 256 * 16 * 8
+template <int NSL>
 __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restrict__ x, int ldx,
                                                            const int* __restrict__ rows_idx, int rows, int n,
                                                            const float* __restrict__ w, float eps, float* y, int ldy,
@@ -103,21 +105,26 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
   const int r = blockIdx.x, tid = threadIdx.x;
   const int src = rows_idx ? rows_idx[r] : r;
   const float* xr = x + (size_t)src * ldx;
-  const int slices = n >> 4, G = n >> 6;
-  float v[kNormMaxSlices][16];
+  const int slices = n >> 4;
+  float v[NSL][16], wv[NSL][16];
   float ss = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kNormMaxSlices; ++i) {
+  for (int i = 0; i < NSL; ++i) {
     const int u = tid + 256 * i;
     if (u < slices) {
       const float4* p = reinterpret_cast<const float4*>(xr + 16 * u);
+      const float4* wp = reinterpret_cast<const float4*>(w + 16 * u);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float4 f = p[e];
+        const float4 f = p[e], g = wp[e];
         v[i][4 * e] = f.x;
         v[i][4 * e + 1] = f.y;
         v[i][4 * e + 2] = f.z;
         v[i][4 * e + 3] = f.w;
+        wv[i][4 * e] = g.x;
+        wv[i][4 * e + 1] = g.y;
+        wv[i][4 * e + 2] = g.z;
+        wv[i][4 * e + 3] = g.w;
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) ss += v[i][e] * v[i][e];
@@ -128,19 +135,12 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
   __syncthreads();
   const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)n + eps);
 #pragma unroll
-  for (int i = 0; i < kNormMaxSlices; ++i) {
+  for (int i = 0; i < NSL; ++i) {
     const int u = tid + 256 * i;
     const bool live = u < slices;  // uniform per group of four lanes (slices % 4 == 0)
     if (live) {
-      const float4* wp = reinterpret_cast<const float4*>(w + 16 * u);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float4 f = wp[e];
-        v[i][4 * e] = v[i][4 * e] * inv * f.x;
-        v[i][4 * e + 1] = v[i][4 * e + 1] * inv * f.y;
-        v[i][4 * e + 2] = v[i][4 * e + 2] * inv * f.z;
-        v[i][4 * e + 3] = v[i][4 * e + 3] * inv * f.w;
-      }
+      for (int e = 0; e < 16; ++e) v[i][e] = v[i][e] * inv * wv[i][e];
       if (y) {
         float4* yp = reinterpret_cast<float4*>(y + (size_t)r * ldy + 16 * u);
 #pragma unroll
@@ -765,8 +765,12 @@ A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n
   PGD_CHECK(n % 64 == 0 && n <= 256 * 16 * gemv::kNormMaxSlices && ldx % 4 == 0, kErrShape, "norm prep width");
   A8Act a = a8_act_view(buf, rows, n);
   if (rows <= 0) return a;
-  hipLaunchKernelGGL(gemv::a8_norm_prep_kernel, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx, rows, n, w, eps, y,
-                     ldy, a8_act_dst(a));
+  if (n <= 256 * 16 * 2)
+    hipLaunchKernelGGL(gemv::a8_norm_prep_kernel<2>, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx, rows, n, w, eps, y,
+                       ldy, a8_act_dst(a));
+  else
+    hipLaunchKernelGGL(gemv::a8_norm_prep_kernel<gemv::kNormMaxSlices>, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx,
+                       rows, n, w, eps, y, ldy, a8_act_dst(a));
   PGD_HIP(hipGetLastError());
   return a;
 }

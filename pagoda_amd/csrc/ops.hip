@@ -223,11 +223,16 @@ __global__ __launch_bounds__(64) void qkv_prep_kernel(QkvPrep p, AttnLayout L, R
     bias = p.variant == 1 ? p.k_bias + (size_t)h * hd : nullptr;
     nw = p.variant == 0 ? p.k_norm : nullptr;
   }
-  float v[4];
+  float v[4], cs_v[4], sn_v[4];
   float ss = 0.0f;
+  // the RoPE table entries are loaded with the row (one round trip)
+  const float* cs = m.cos + (size_t)r * rd;
+  const float* sn = m.sin + (size_t)r * rd;
   for (int e = 0; e < E; ++e) {
     const int d = lane + 64 * e;
     v[e] = src[d];
+    cs_v[e] = d < rd ? cs[d] : 0.0f;
+    sn_v[e] = d < rd ? sn[d] : 0.0f;
     if (bias) v[e] = v[e] + bias[d];
     ss += v[e] * v[e];
   }
@@ -238,13 +243,11 @@ __global__ __launch_bounds__(64) void qkv_prep_kernel(QkvPrep p, AttnLayout L, R
   }
   for (int e = 0; e < E; ++e) buf[lane + 64 * e] = v[e];
   __syncthreads();
-  const float* cs = m.cos + (size_t)r * rd;
-  const float* sn = m.sin + (size_t)r * rd;
   for (int e = 0; e < E; ++e) {
     const int d = lane + 64 * e;
     if (d < rd) {
       const float rot = d < half ? -buf[d + half] : buf[d - half];
-      v[e] = buf[d] * cs[d] + rot * sn[d];
+      v[e] = buf[d] * cs_v[e] + rot * sn_v[e];
     }
   }
   if (is_q) {
