@@ -110,9 +110,14 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
   const float a_log = p.a_log[h], dtb = p.dt_bias[h];
   const float qscale = sqrtf((float)D);
   const int r0 = row_start[s], n = row_count[s];
+  // the gate input z and the norm weight are loaded with the step's other
+  // inputs, not after the reductions that need them
+  const float nw = tid < D ? p.norm[tid] : 0.0f;
   for (int t = 0; t < n; ++t) {
     const int row = r0 + t;
     const float* cv = p.conv_out + (size_t)row * p.ld_conv;
+    const float zg = tid < D ? p.z[(size_t)row * p.ld_z + h * D + tid] : 0.0f;
+    const float vv = tid < D ? cv[2 * key_dim + h * D + tid] : 0.0f;
     // q (threads 0..127) and k (128..255), L2-normalized per head
     float v = tid < D ? cv[kh * D + tid] : cv[key_dim + kh * D + (tid - D)];
     float ss = wave_sum(v * v);
@@ -147,7 +152,6 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
       float mem = 0.0f;
 #pragma unroll
       for (int q = 0; q < 8; ++q) mem += red[q][tid];
-      const float vv = cv[2 * key_dim + h * D + tid];
       delta[tid] = (vv - mem) * beta;
     }
     __syncthreads();
@@ -179,8 +183,7 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
     __syncthreads();
     if (tid < D) {
       const float inv = 1.0f / sqrtf((part[0] + part[1]) / (float)D + 1e-6f);
-      const float zg = p.z[(size_t)row * p.ld_z + h * D + tid];
-      const float val = o * inv * p.norm[tid] * (zg / (1.0f + expf(-zg)));
+      const float val = o * inv * nw * (zg / (1.0f + expf(-zg)));
       if (p.out) p.out[(size_t)row * p.ld_out + h * D + tid] = val;
       obuf[tid] = val;
     }
