@@ -244,6 +244,52 @@ def roofline(dev, cfg, batch):
                        "avg_launch_us": avg1 * 1e3, "algo_bytes_per_launch": algo1}}
 
 
+def config5_only():
+    from pagoda_amd import Device
+    from pagoda_amd.engine import QWEN35_27B, Model
+
+    dev = Device(os.environ.get("PAGODA_DEVICE", "hip"))
+    cfg = QWEN35_27B
+    cfg.max_pos = C5_TRUNK + C5_SUFFIX + C5_GEN + 64
+    cfg.kv_blocks = C5_PAGES + 16
+    model = Model.synth(dev, cfg, seed=2026)
+    out = config5(model, cfg)
+    model.free()
+    return out
+
+
+def attn_scan():
+    """Paged GQA decode attention alone (config-4 heads: 24 q / 4 kv, head_dim
+    256), 1 and 32 rows, contexts of 40..4096 positions, 5 calls each through
+    pgd_attn_decode_dev; every row reads its own pages."""
+    import ctypes as C
+
+    from pagoda_amd import Device
+    from pagoda_amd._lib import call
+
+    dev = Device(os.environ.get("PAGODA_DEVICE", "hip"))
+    heads, kvh, hd, block = 24, 4, 256, 16
+    rng = np.random.default_rng(0)
+    for rows in (1, 32):
+        for L in (40, 256, 1024, 4096):
+            nb = (L + block - 1) // block
+            pages = rows * nb + 1
+            bufs = [dev.upload(rng.normal(0, 1, (rows, heads, hd)).astype(np.float32)),
+                    dev.upload(rng.normal(0, 1, (rows, heads, hd)).astype(np.float32)),
+                    dev.upload(rng.normal(0, 1, (pages, kvh, block, hd)).astype(np.float32)),
+                    dev.upload(rng.normal(0, 1, (pages, kvh, block, hd)).astype(np.float32)),
+                    dev.upload(np.arange(rows, dtype=np.int32)),
+                    dev.upload(np.full(rows, L - 1, np.int32)),
+                    dev.upload(np.arange(rows * nb, dtype=np.int32).reshape(rows, nb))]
+            out = dev.alloc(rows * heads * hd * 4)
+            for _ in range(5):
+                call("pgd_attn_decode_dev", dev.handle, heads, kvh, hd, block, *[C.c_void_p(p) for p in bufs], nb,
+                     rows, C.c_void_p(out))
+            log(f"attn scan: rows={rows} positions={L}")
+            for p in bufs + [out]:
+                dev.free(p)
+
+
 def copy_calib():
     """A plain device-to-device copy kernel of known size (256 MiB read +
     256 MiB written per launch) for scaling FETCH_SIZE / WRITE_SIZE."""
@@ -305,6 +351,10 @@ def main():
     ap.add_argument("--roofline-only", action="store_true")
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--no-config5", action="store_true")
+    ap.add_argument("--config5-only", action="store_true",
+                    help="run only the config-5 passes (for kernel traces of that workload)")
+    ap.add_argument("--attn-scan", action="store_true",
+                    help="time the paged attention alone over context lengths (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -312,6 +362,12 @@ def main():
         sys.exit(2)
     if args.copy_calib:
         copy_calib()
+        return
+    if args.config5_only:
+        print(json.dumps({"config5": config5_only()}), flush=True)
+        return
+    if args.attn_scan:
+        attn_scan()
         return
     if args.roofline_only:
         from pagoda_amd import Device
