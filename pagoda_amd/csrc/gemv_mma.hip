@@ -636,18 +636,38 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
   }
 }
 
-// y[b][n] = (res[b][n] +) sum over ranges, in range order
-template <int EPI>
-__global__ __launch_bounds__(256) void a8_reduce_kernel(GemvArgs a, int nb, int ks, const float* __restrict__ part) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (size_t)nb * a.n_out) return;
-  const int b = (int)(i / a.n_out), n = (int)(i % a.n_out);
-  const size_t plane = (size_t)nb * a.n_out;
-  float y = part[i];
-  for (int r = 1; r < ks; ++r) y += part[(size_t)r * plane + i];
+// y[b][n] = (res[b][n] +) sum over ranges, in range order; each thread sums 4
+// consecutive outputs of one row with all KS loads issued before the adds
+template <int KS, int EPI>
+__global__ __launch_bounds__(256) void a8_reduce_kernel(GemvArgs a, int nb, const float* __restrict__ part) {
+  const int n4 = a.n_out >> 2;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= nb * n4) return;
+  const int b = i / n4, n = (i - b * n4) * 4;
+  const size_t plane = (size_t)nb * a.n_out, e = (size_t)b * a.n_out + n;
+  float4 v[KS];
+#pragma unroll
+  for (int r = 0; r < KS; ++r) v[r] = *reinterpret_cast<const float4*>(part + r * plane + e);
+  float4 y = v[0];
+#pragma unroll
+  for (int r = 1; r < KS; ++r) {
+    y.x += v[r].x;
+    y.y += v[r].y;
+    y.z += v[r].z;
+    y.w += v[r].w;
+  }
   const size_t o = (size_t)b * a.ldy + n;
-  if constexpr (EPI == EPI_STORE) a.y[o] = y;
-  if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + y;
+  if constexpr (EPI == EPI_RES) {
+    const float* rs = a.res + (size_t)b * a.ldres + n;
+    y.x = rs[0] + y.x;
+    y.y = rs[1] + y.y;
+    y.z = rs[2] + y.z;
+    y.w = rs[3] + y.w;
+  }
+  a.y[o] = y.x;
+  a.y[o + 1] = y.y;
+  a.y[o + 2] = y.z;
+  a.y[o + 3] = y.w;
 }
 
 template <int MODE, int KS, int KP, int P, int MT, int EPI>
@@ -671,8 +691,8 @@ void launch_shared(const GemvArgs& a, const uint4* XA, const float* CA, int nb, 
   float* part = static_cast<float*>(gemv_scratch(s, (size_t)KS * nb * a.n_out * sizeof(float), 1));
   hipLaunchKernelGGL((a8_mma_shared_kernel<KS, T, P, EPI>), dim3((tiles + T - 1) / T, KS), dim3(64 * T), 0, s, a, XA,
                      CA, nb, part);
-  const size_t n = (size_t)nb * a.n_out;
-  hipLaunchKernelGGL((a8_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, nb, KS, part);
+  const int n4 = nb * (a.n_out / 4);
+  hipLaunchKernelGGL((a8_reduce_kernel<KS, EPI>), dim3((n4 + 255) / 256), dim3(256), 0, s, a, nb, part);
 }
 
 // one launch per chunk of up to 32 rows; the mode stages only the rows present
@@ -685,6 +705,8 @@ void launch_chunk_ks(const GemvArgs& a, const uint4* XA, const float* CA, int nb
   if (nb <= 16) return launch_kernel<1, KS, KP4, 4, 1, EPI>(a, XA, CA, nb, s);
   if constexpr (EPI == EPI_SWIGLU) {
     // gate + up already give each wave 2 KiB of weights per KiB of operands
+    launch_kernel<2, KS, KP4, 3, 1, EPI>(a, XA, CA, nb, s);
+  } else if (a.n_out % 4 != 0) {
     launch_kernel<2, KS, KP4, 3, 1, EPI>(a, XA, CA, nb, s);
   } else {
     // one operand stage per workgroup of 4 (narrow) or 8 tiles

@@ -74,7 +74,7 @@ def test_synth_on_device_matches_cpu_quantizer(dev, fmt, shape):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("shape", [(64, 256), (333, 896), (77, 4864), (1152, 896)])
-@pytest.mark.parametrize("rows", [1, 3, 8, 13])
+@pytest.mark.parametrize("rows", [1, 3, 8, 13, 30])
 def test_gemv_matches_fp64(dev, fmt, shape, rows):
     n_out, n_in = shape
     if fmt == 0 and n_in % 64:
@@ -89,14 +89,17 @@ def test_gemv_matches_fp64(dev, fmt, shape, rows):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_batched_rows_bitwise_equal_serial(dev, fmt):
-    """qwen3_gemv.rs:1115-1167: a batched step equals per-row GEMVs exactly."""
+@pytest.mark.parametrize("n_out", [200, 203])
+def test_batched_rows_bitwise_equal_serial(dev, fmt, n_out):
+    """qwen3_gemv.rs:1115-1167: a batched step equals per-row GEMVs exactly
+    (203 outputs: 17..32-row A8 launches take the per-wave kernel, not the
+    shared-operand kernel + vector reduction)."""
     rng = np.random.default_rng(9)
-    w = rng.normal(0, 0.02, (200, 1024)).astype(np.float32)
+    w = rng.normal(0, 0.02, (n_out, 1024)).astype(np.float32)
     m, _ = make(dev, fmt, w)
-    x = rng.normal(0, 1, (21, 1024)).astype(np.float32)
-    serial = np.stack([m.gemv(x[i]) for i in range(21)])
-    for rows in (2, 4, 8, 13, 21):
+    x = rng.normal(0, 1, (32, 1024)).astype(np.float32)
+    serial = np.stack([m.gemv(x[i]) for i in range(32)])
+    for rows in (2, 4, 8, 13, 21, 32):
         got = m.gemv(x[:rows])
         np.testing.assert_array_equal(got.view(np.uint32), serial[:rows].view(np.uint32))
 
