@@ -244,6 +244,99 @@ def roofline(dev, cfg, batch):
                        "avg_launch_us": avg1 * 1e3, "algo_bytes_per_launch": algo1}}
 
 
+KQ_SHAPES = [(896, 4864), (4864, 896), (896, 1152), (896, 151936)]  # K x N
+KQ_ROWS = [1, 4, 8, 16, 32, 64]
+
+
+def kernel_sweeps():
+    """Config 2 (Q4_K / Q6_K GEMV over K x N shapes and ragged row counts,
+    f16 activations) and config 3 (Gated-DeltaNet decode step, B sequences of
+    32 value heads with 128 x 128 f32 state, plus 4-token chunks), timed with
+    HIP events on the library's stream. Every launch reads weights or state
+    that the previous launches did not touch (copies cycled through past the
+    last-level cache), so the figures are HBM figures."""
+    import ctypes as C
+    from pagoda_amd import Device, Event, Matrix
+    from pagoda_amd.matrix import FMT_Q4K, FMT_Q6K
+    from pagoda_amd._lib import call
+
+    dev = Device(os.environ.get("PAGODA_DEVICE", "hip"))
+    rng = np.random.default_rng(3)
+    out = {"kquant": [], "gdn": []}
+    for fmt, fname in ((FMT_Q4K, "q4k"), (FMT_Q6K, "q6k")):
+        for K, N in KQ_SHAPES:
+            probe = Matrix.synth(dev, fmt, N, K, 11, 1)
+            per = probe.algo_bytes
+            ncopy = max(2, int(1.2e9 // probe.dev_bytes) + 1)
+            ms = [probe] + [Matrix.synth(dev, fmt, N, K, 11, 2 + i) for i in range(ncopy - 1)]
+            for rows in KQ_ROWS:
+                x = dev.upload(rng.normal(0, 1, (rows, K)).astype(np.float16))
+                y = dev.alloc(rows * N * 4)
+                for m in ms[:2]:
+                    m.gemv_dev(x, K, rows, y, N, x_f16=True)
+                L = max(32, 2 * ncopy)
+                e0 = Event(dev).record()
+                for i in range(L):
+                    ms[i % ncopy].gemv_dev(x, K, rows, y, N, x_f16=True)
+                e1 = Event(dev).record()
+                us = e0.elapsed_ms(e1) / L * 1e3
+                algo = per + rows * K * 2 + rows * N * 4
+                gbs = algo / (us * 1e-6) / 1e9
+                log(f"{fname} K={K:5d} N={N:6d} rows={rows:2d}: {us:8.2f} us {gbs:7.0f} GB/s {100 * gbs / HBM_PEAK_GBS:5.1f}%")
+                out["kquant"].append({"fmt": fname, "K": K, "N": N, "rows": rows, "us": round(us, 3),
+                                      "algo_bytes": algo, "gbs": round(gbs, 1),
+                                      "frac": round(gbs / HBM_PEAK_GBS, 4)})
+                dev.free(x)
+                dev.free(y)
+            for m in ms:
+                m.free()
+    # config 3: 16 key heads, 32 value heads, d = 128
+    kh, vh, d = 16, 32, 128
+    state_bytes = vh * d * d * 4
+    for B, toks in ((1, 1), (8, 1), (32, 1), (64, 1), (8, 4), (32, 4)):
+        rows = B * toks
+        conv = dev.upload(rng.normal(0, 1, (rows, 2 * kh * d + vh * d)).astype(np.float32))
+        a = dev.upload(rng.normal(0, 1, (rows, vh)).astype(np.float32))
+        b = dev.upload(rng.normal(0, 1, (rows, vh)).astype(np.float32))
+        z = dev.upload(rng.normal(0, 1, (rows, vh * d)).astype(np.float32))
+        a_log = dev.upload(np.log(rng.uniform(1, 16, vh)).astype(np.float32))
+        dtb = dev.upload(np.zeros(vh, np.float32))
+        norm = dev.upload(rng.uniform(0.5, 1.5, d).astype(np.float32))
+        sets = max(2, int(1.2e9 // (B * state_bytes)) + 1)
+        sbuf = dev.alloc(sets * B * state_bytes)
+        init = (rng.normal(0, 1, (B, vh, d, d)) * 0.1).astype(np.float32)
+        for k in range(sets):
+            call("pgd_device_memcpy", dev.handle, C.c_void_p(sbuf + k * B * state_bytes), init.ctypes.data_as(C.c_void_p),
+                 C.c_size_t(init.nbytes), 0)
+        ptrs = [dev.upload(np.array([sbuf + (k * B + i) * state_bytes for i in range(B)], np.uint64))
+                for k in range(sets)]
+        rs = dev.upload((np.arange(B) * toks).astype(np.int32))
+        rc = dev.upload(np.full(B, toks, np.int32))
+        o = dev.alloc(rows * vh * d * 4)
+
+        def step(k):
+            call("pgd_gdn_step_dev", dev.handle, kh, vh, *[C.c_void_p(p) for p in (conv, a, b, z, a_log, dtb, norm)],
+                 C.c_void_p(ptrs[k]), C.c_void_p(rs), C.c_void_p(rc), B, C.c_void_p(o))
+
+        for k in range(sets):
+            step(k)
+        L = max(32, 2 * sets)
+        e0 = Event(dev).record()
+        for i in range(L):
+            step(i % sets)
+        e1 = Event(dev).record()
+        us = e0.elapsed_ms(e1) / L * 1e3
+        algo = 2 * B * state_bytes + rows * (2 * kh * d + vh * d + 2 * vh + vh * d + vh * d) * 4
+        gbs = algo / (us * 1e-6) / 1e9
+        log(f"gdn B={B:2d} tokens={toks}: {us:8.2f} us {gbs:7.0f} GB/s {100 * gbs / HBM_PEAK_GBS:5.1f}%")
+        out["gdn"].append({"B": B, "tokens": toks, "us": round(us, 3), "algo_bytes": algo, "gbs": round(gbs, 1),
+                           "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        for p in [conv, a, b, z, a_log, dtb, norm, sbuf, rs, rc, o] + ptrs:
+            dev.free(p)
+    dev.close()
+    return out
+
+
 def config5_only():
     from pagoda_amd import Device
     from pagoda_amd.engine import QWEN35_27B, Model
@@ -355,6 +448,8 @@ def main():
                     help="run only the config-5 passes (for kernel traces of that workload)")
     ap.add_argument("--attn-scan", action="store_true",
                     help="time the paged attention alone over context lengths (for kernel traces)")
+    ap.add_argument("--kernel-sweeps", action="store_true",
+                    help="config 2 (Q4_K/Q6_K GEMV sweep) and config 3 (GDN step) kernel timings")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -368,6 +463,9 @@ def main():
         return
     if args.attn_scan:
         attn_scan()
+        return
+    if args.kernel_sweeps:
+        print(json.dumps(kernel_sweeps()), flush=True)
         return
     if args.roofline_only:
         from pagoda_amd import Device

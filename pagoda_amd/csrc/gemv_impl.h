@@ -172,12 +172,20 @@ struct Q6K {
                                   const GemvArgs& a, int row, int p) {
     int sb = p >> 3, part = p & 7, n = part >> 2, c = part & 3;
     W w;
-    w.ql = *reinterpret_cast<const uint4*>(c0 + (size_t)row * a.nsb * 128 + ((size_t)p << 4));
-    w.qh = *reinterpret_cast<const uint4*>(c1 + (size_t)row * a.nsb * 64 + sb * 64 + 32 * n + 16 * (c & 1));
-    const int8_t* sc = reinterpret_cast<const int8_t*>(c2) + (size_t)row * a.nsb * 16 + sb * 16 + 8 * n + c;
-    float d = f16_to_f32(reinterpret_cast<const uint16_t*>(c3)[(size_t)row * a.nsb + sb]);
-    w.s_lo = d * (float)sc[0];
-    w.s_hi = d * (float)sc[4];
+    // tiled planes (quant.h): the 16-byte runs arrive one dword at a time
+    uint32_t l[4], h[4];
+    const int hq = sb * 64 + 32 * n + 16 * (c & 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      l[k] = *reinterpret_cast<const uint32_t*>(c0 + q6k_ql_off(row, 16 * p + 4 * k, a.nsb));
+      h[k] = *reinterpret_cast<const uint32_t*>(c1 + q6k_qh_off(row, hq + 4 * k, a.nsb));
+    }
+    w.ql = make_uint4(l[0], l[1], l[2], l[3]);
+    w.qh = make_uint4(h[0], h[1], h[2], h[3]);
+    const int8_t* sc = reinterpret_cast<const int8_t*>(c2);
+    float d = f16_to_f32(reinterpret_cast<const uint16_t*>(c3)[q6k_d_off(row, sb, a.nsb)]);
+    w.s_lo = d * (float)sc[q6k_sc_off(row, sb * 16 + 8 * n + c, a.nsb)];
+    w.s_hi = d * (float)sc[q6k_sc_off(row, sb * 16 + 8 * n + c + 4, a.nsb)];
     return w;
   }
   static __device__ inline float acc(float r, const W& w, const float* xl, const float* xh, float sl, float sh,
@@ -313,6 +321,8 @@ void run_q6k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 // Q4K on the matrix cores (n_in % 64 == 0)
 bool q4k_mma_ok(const GemvArgs& a);
 void run_q4k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
+bool q6k_mma_ok(const GemvArgs& a, int epi);
+void run_q6k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 // Per-stream device scratch for GEMV activation prep (grows, never shrinks;
 // growing drains the stream first).
 // per-stream device scratch that grows on demand (the stream is synchronized

@@ -20,6 +20,8 @@
 // Workgroups hold KS waves sharing one 32-row tile (KS from the shape) and
 // splitting its groups; each wave keeps PF groups of loads in flight; the
 // waves' partial sums meet in LDS in a fixed order.
+#include <type_traits>
+
 #include "common.h"
 #include "gemv_impl.h"
 #include "quant.h"
@@ -31,6 +33,7 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // eight 4-bit codes (the low or high nibbles of 8 bytes) -> f16 1024 + q
@@ -264,9 +267,245 @@ void q4k_rows(GemvArgs a, int nrows, hipStream_t s) {
   }
 }
 
+
+// ---- Q6_K -----------------------------------------------------------------
+// GGML block_q6_K (pagoda-hf/src/qwen2_gguf.rs:271-289 via candle's QMatMul):
+// per 128-element half of a super-block, element e (0..127) has code
+// q = (ql[e % 64] nibble e / 64) | ((qh[e % 32] >> 2 (e / 32)) & 3) << 4 and
+// weight d * sc[e / 16] * (q - 32). The scale changes every 16 elements, so
+// one v_mfma_f32_16x16x16_f16 covers one 16-element sub-block s:
+//   P[b, n] = sum (1024 + q) x,  XS[b] = sum x  (MFMA against ones)
+//   Y += d sc P - 1056 d sc XS
+// Lane (j, quarter q) holds elements 16 s + 4 q .. + 3 of every sub-block:
+// ql bytes 16 (s % 4) + 4 q (nibble s / 4) and qh bytes 16 (s % 2) + 4 q
+// (shift 2 (s / 2)): four ql dwords and two qh dwords per half and row,
+// which the tiled planes (quant.h q6k_*_off) hold as 16 + 8 contiguous
+// bytes; padding rows are zeros.
+
+// four 6-bit codes (ql nibbles + qh bit pairs of 4 bytes) -> f16 1024 + q
+__device__ inline h4 q6_codes(uint32_t ql, uint32_t qh, int hi_nib, int sh) {
+  const uint32_t lo = hi_nib ? (ql >> 4) & 0x0F0F0F0Fu : ql & 0x0F0F0F0Fu;
+  const uint32_t q = lo | (((qh >> sh) & 0x03030303u) << 4);
+  const uint32_t c0 = __builtin_amdgcn_perm(0x64646464u, q, 0x04010400u);
+  const uint32_t c1 = __builtin_amdgcn_perm(0x64646464u, q, 0x04030402u);
+  return __builtin_bit_cast(h4, make_uint2(c0, c1));
+}
+
+template <int NBT, bool XF16>
+struct Q6Raw {
+  using XT = typename std::conditional<XF16, uint2, uint4>::type;  // 4 activations
+  uint32_t ql[2][4];
+  uint32_t qh[2][2];
+  uint2 sc[2];   // the half's 8 int8 sub-block scales
+  uint32_t d[2]; // f16 super-block scale (low half)
+  XT x[8][NBT];
+};
+
+template <int NBT, int KS, bool XF16, int EPI>
+__global__ __launch_bounds__(64 * KS) void q6k_mma_kernel(GemvArgs a, int nb) {
+  static_assert(EPI != EPI_SWIGLU, "one matrix per wave");
+  constexpr int NS = 2;
+  __shared__ f4 red[KS > 1 ? KS - 1 : 1][NS][NBT][64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, q = lane >> 4;
+  const int H = a.n_in >> 7, nsb = a.nsb;
+  const int tile = blockIdx.x;
+
+  // per half u: block tile * 2 nsb + u of each plane
+  const size_t blk0 = (size_t)tile * 2 * nsb;
+  const uint8_t* qlb[NS];
+  const uint8_t* qhb[NS];
+  const uint8_t* scb[NS];
+  const uint16_t* db[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int ln = (4 * st + q) * 16 + j;
+    qlb[st] = a.p0 + (blk0 << 11) + ln * 16;
+    qhb[st] = a.p1 + (blk0 << 10) + ln * 8;
+    scb[st] = a.p2 + (blk0 << 8) + (16 * st + j) * 8;
+    db[st] = reinterpret_cast<const uint16_t*>(a.p3) + (size_t)tile * nsb * 32 + 16 * st + j;
+  }
+  const uint8_t* xrow[NBT];
+#pragma unroll
+  for (int bt = 0; bt < NBT; ++bt) {
+    const int b = min(16 * bt + j, nb - 1);
+    xrow[bt] = reinterpret_cast<const uint8_t*>(a.x) + ((size_t)b * a.ldx + 4 * q) * (XF16 ? 2 : 4);
+  }
+  using Raw = Q6Raw<NBT, XF16>;
+  using XT = typename Raw::XT;
+
+  auto load = [&](int u, Raw& R) {
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      const uint4 l = *reinterpret_cast<const uint4*>(qlb[st] + ((size_t)u << 11));
+      const uint2 h = *reinterpret_cast<const uint2*>(qhb[st] + ((size_t)u << 10));
+      R.ql[st][0] = l.x;
+      R.ql[st][1] = l.y;
+      R.ql[st][2] = l.z;
+      R.ql[st][3] = l.w;
+      R.qh[st][0] = h.x;
+      R.qh[st][1] = h.y;
+      R.sc[st] = *reinterpret_cast<const uint2*>(scb[st] + ((size_t)u << 8));
+      R.d[st] = db[st][(u >> 1) * 32];
+    }
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb)
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt)
+        R.x[sb][bt] = *reinterpret_cast<const XT*>(xrow[bt] + (size_t)(128 * u + 16 * sb) * (XF16 ? 2 : 4));
+  };
+
+  f4 Y[NS][NBT];
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+  const h4 ones = {1, 1, 1, 1};
+
+  auto compute = [&](const Raw& R) {
+    float dv[NS];
+#pragma unroll
+    for (int st = 0; st < NS; ++st) dv[st] = f16_to_f32(R.d[st] & 0xffffu);
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+      h4 xh[NBT], xl[NBT];
+      f4 XS[NBT];
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        if constexpr (XF16) {
+          xh[bt] = __builtin_bit_cast(h4, R.x[sb][bt]);
+          XS[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        } else {
+          const float v[4] = {__builtin_bit_cast(float, R.x[sb][bt].x), __builtin_bit_cast(float, R.x[sb][bt].y),
+                              __builtin_bit_cast(float, R.x[sb][bt].z), __builtin_bit_cast(float, R.x[sb][bt].w)};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const _Float16 hv = (_Float16)v[e];
+            xh[bt][e] = hv;
+            xl[bt][e] = (_Float16)(v[e] - (float)hv);
+          }
+          f4 t = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          XS[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xl[bt], ones, t, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        const uint32_t scw = sb < 4 ? R.sc[st].x : R.sc[st].y;
+        const float sc = (float)(int8_t)((scw >> (8 * (sb & 3))) & 255u);
+        const float ca = dv[st] * sc;
+        const float cb = 1056.0f * ca;
+        const h4 bq = q6_codes(R.ql[st][sb & 3], R.qh[st][sb & 1], sb >> 2, 2 * (sb >> 1));
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+          f4 P = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], bq, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          if constexpr (!XF16) P = __builtin_amdgcn_mfma_f32_16x16x16f16(xl[bt], bq, P, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(ca, P[r], fmaf(-cb, XS[bt][r], Y[st][bt][r]));
+        }
+      }
+      // one sub-block at a time: keeps the operands of the others out of registers
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // double buffer: the next half's loads are in flight during this one's MFMAs
+  const int per = (H + KS - 1) / KS;
+  const int u0 = min(H, wave * per), u1 = min(H, u0 + per);
+  Raw cur, nxt;
+  if (u0 < u1) load(u0, cur);
+  for (int u = u0; u < u1; ++u) {
+    if (u + 1 < u1) load(u + 1, nxt);
+    compute(cur);
+    cur = nxt;
+  }
+
+  // ---- split-K reduction (fixed order: wave 0 + 1 + ... + KS-1) ----
+  if constexpr (KS > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) red[wave - 1][st][bt][lane] = Y[st][bt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 0; w < KS - 1; ++w)
+#pragma unroll
+      for (int st = 0; st < NS; ++st)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[w][st][bt][lane];
+  }
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int n = tile * 32 + 16 * st + j;
+    if (n >= a.n_out) continue;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int b = 16 * bt + 4 * q + r;
+        if (b >= nb) continue;
+        const size_t o = (size_t)b * a.ldy + n;
+        if constexpr (EPI == EPI_STORE) a.y[o] = Y[st][bt][r];
+        if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];
+      }
+  }
+}
+
+// split of the 128-element halves: depends on the matrix shape only
+inline int q6k_split(const GemvArgs& a) {
+  const int tiles = (a.n_out + 31) / 32, H = a.n_in / 128;
+  int ks = 1;
+  while (ks < 8 && tiles * ks < 1024 && H / (2 * ks) >= 2) ks *= 2;
+  return ks;
+}
+
+template <int NBT, int KS, bool XF16, int EPI>
+void q6k_launch(const GemvArgs& a, int nb, hipStream_t s) {
+  hipLaunchKernelGGL((q6k_mma_kernel<NBT, KS, XF16, EPI>), dim3((a.n_out + 31) / 32), dim3(64 * KS), 0, s, a, nb);
+}
+
+template <int NBT, bool XF16, int EPI>
+void q6k_launch_ks(const GemvArgs& a, int nb, hipStream_t s) {
+  switch (q6k_split(a)) {
+    case 1: return q6k_launch<NBT, 1, XF16, EPI>(a, nb, s);
+    case 2: return q6k_launch<NBT, 2, XF16, EPI>(a, nb, s);
+    case 4: return q6k_launch<NBT, 4, XF16, EPI>(a, nb, s);
+    default: return q6k_launch<NBT, 8, XF16, EPI>(a, nb, s);
+  }
+}
+
+template <bool XF16, int EPI>
+void q6k_rows(GemvArgs a, int nrows, hipStream_t s) {
+  const size_t xel = XF16 ? 2 : 4;
+  while (nrows > 0) {
+    const int nb = nrows < 32 ? nrows : 32;
+    if (nb > 16) q6k_launch_ks<2, XF16, EPI>(a, nb, s);
+    else q6k_launch_ks<1, XF16, EPI>(a, nb, s);
+    PGD_HIP(hipGetLastError());
+    nrows -= nb;
+    a.x = reinterpret_cast<const uint8_t*>(a.x) + (size_t)nb * a.ldx * xel;
+    a.y += (size_t)nb * a.ldy;
+    if (a.res) a.res += (size_t)nb * a.ldres;
+  }
+}
+
 }  // namespace
 
 bool q4k_mma_ok(const GemvArgs& a) { return a.n_in % 64 == 0; }
+
+// whole 128-element halves and 16-byte aligned activation rows
+bool q6k_mma_ok(const GemvArgs& a, int epi) { return a.n_in % 128 == 0 && a.ldx % 4 == 0 && epi != EPI_SWIGLU; }
+
+void run_q6k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s) {
+  if (x_f16) {
+    if (epi == EPI_RES) q6k_rows<true, EPI_RES>(a, nrows, s);
+    else q6k_rows<true, EPI_STORE>(a, nrows, s);
+  } else {
+    if (epi == EPI_RES) q6k_rows<false, EPI_RES>(a, nrows, s);
+    else q6k_rows<false, EPI_STORE>(a, nrows, s);
+  }
+}
 
 void run_q4k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s) {
   if (x_f16) {

@@ -11,10 +11,8 @@
 //                                rows are padded to a multiple of 32 with zeros
 //   Q4K (GGML block_q4_K):       qs    u8 [n_out][nsb*128]      the 128 nibble bytes of each block
 //                                hdr   16B [n_out][nsb]         d, dmin (f16) + 12 packed scale bytes
-//   Q6K (GGML block_q6_K):       ql    u8 [n_out][nsb*128]
-//                                qh    u8 [n_out][nsb*64]
-//                                sc    i8 [n_out][nsb*16]
-//                                d     f16 [n_out][nsb]
+//   Q6K (GGML block_q6_K):       ql, qh, sc, d planes, tiled by 32 rows
+//                                (q6k_*_off below); rows padded with zeros
 //
 // The planes hold exactly the bytes of the source blocks (144 B / 210 B per
 // 256 weights; 1.0625 B per A8 weight), only regrouped.
@@ -59,6 +57,36 @@ __host__ __device__ inline size_t q4k_qs_off(int row, int i, int nsb) {
 }
 __host__ __device__ inline size_t q4k_hdr_off(int row, int sb, int nsb) {
   return ((size_t)(row >> 5) * nsb + (size_t)sb) * 512 + (size_t)(row & 31) * 16;
+}
+
+// Q6K tiled addressing. For each 32-row tile and 128-element half u of the
+// rows (2 nsb halves): a 2 KiB ql block (64 B per row), a 1 KiB qh block
+// (32 B per row) and a 256 B scale block (8 int8 per row); per tile and
+// super-block 32 f16 d. Inside the ql / qh blocks, dword k of a row's
+// 16-byte runs (bytes 4k..4k+3 of each run) of row 16 h + j lives at
+// [4 h + k][j][run]: the four ql dwords (two qh dwords) a matrix-core lane
+// needs for one half are 16 (8) contiguous bytes, and 64 lanes read 1 KiB
+// (512 B) contiguously. ql byte i of a row (0 <= i < 128 nsb), qh byte i
+// (0 <= i < 64 nsb), scale i (0 <= i < 16 nsb), d of super-block sb (in f16
+// elements):
+__host__ __device__ inline size_t q6k_ql_off(int row, int i, int nsb) {
+  const int u = i >> 6, w = i & 63;
+  const size_t blk = (size_t)(row >> 5) * 2 * nsb + u;
+  const int lane = ((((row & 31) >> 4) << 2) + ((w & 15) >> 2)) * 16 + (row & 15);
+  return (blk << 11) + (size_t)lane * 16 + (w >> 4) * 4 + (w & 3);
+}
+__host__ __device__ inline size_t q6k_qh_off(int row, int i, int nsb) {
+  const int u = i >> 5, w = i & 31;
+  const size_t blk = (size_t)(row >> 5) * 2 * nsb + u;
+  const int lane = ((((row & 31) >> 4) << 2) + ((w & 15) >> 2)) * 16 + (row & 15);
+  return (blk << 10) + (size_t)lane * 8 + (w >> 4) * 4 + (w & 3);
+}
+__host__ __device__ inline size_t q6k_sc_off(int row, int i, int nsb) {
+  const size_t blk = (size_t)(row >> 5) * 2 * nsb + (i >> 3);
+  return (blk << 8) + (size_t)(row & 31) * 8 + (i & 7);
+}
+__host__ __device__ inline size_t q6k_d_off(int row, int sb, int nsb) {
+  return ((size_t)(row >> 5) * nsb + sb) * 32 + (row & 31);
 }
 
 // algorithmic bytes of the weights (what a GEMV must stream at least once;

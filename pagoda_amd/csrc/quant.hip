@@ -28,7 +28,10 @@ void run_fmt(const QMat& m, const GemvArgs& a, int nrows, int x_f16, int epi, hi
       if (q4k_mma_ok(a)) run_q4k_mma(a, nrows, x_f16, epi, s);
       else run_q4k(a, nrows, x_f16, epi, s);
       break;
-    case FMT_Q6K: run_q6k(a, nrows, x_f16, epi, s); break;
+    case FMT_Q6K:
+      if (q6k_mma_ok(a, epi)) run_q6k_mma(a, nrows, x_f16, epi, s);
+      else run_q6k(a, nrows, x_f16, epi, s);
+      break;
     default: throw Error{kErrFormat, "unknown matrix format"};
   }
 }
@@ -98,11 +101,19 @@ __global__ void dequant_q6k_kernel(const uint8_t* qlp, const uint8_t* qhp, const
   int r = (int)(t / runs), p = (int)(t % runs);
   int row = ids ? (int)ids[r] : row0 + r;
   int sb = p >> 3, part = p & 7, n = part >> 2, c = part & 3;
-  uint4 ql = *reinterpret_cast<const uint4*>(qlp + (size_t)row * nsb * 128 + (size_t)p * 16);
-  uint4 qh = *reinterpret_cast<const uint4*>(qhp + (size_t)row * nsb * 64 + sb * 64 + 32 * n + 16 * (c & 1));
-  const int8_t* sc = scp + (size_t)row * nsb * 16 + sb * 16 + 8 * n + c;
-  float d = f16_to_f32(dp[(size_t)row * nsb + sb]);
-  float slo = (float)sc[0], shi = (float)sc[4];
+  // ql bytes 16p.., qh bytes 64 sb + 32 n + 16 (c & 1).., one dword at a time
+  uint32_t qlw[4], qhw[4];
+  const int hq = sb * 64 + 32 * n + 16 * (c & 1);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    qlw[k] = *reinterpret_cast<const uint32_t*>(qlp + q6k_ql_off(row, 16 * p + 4 * k, nsb));
+    qhw[k] = *reinterpret_cast<const uint32_t*>(qhp + q6k_qh_off(row, hq + 4 * k, nsb));
+  }
+  const uint4 ql = make_uint4(qlw[0], qlw[1], qlw[2], qlw[3]);
+  const uint4 qh = make_uint4(qhw[0], qhw[1], qhw[2], qhw[3]);
+  float d = f16_to_f32(dp[q6k_d_off(row, sb, nsb)]);
+  float slo = (float)scp[q6k_sc_off(row, sb * 16 + 8 * n + c, nsb)];
+  float shi = (float)scp[q6k_sc_off(row, sb * 16 + 8 * n + c + 4, nsb)];
   int shl = 2 * (c >> 1), shh = 4 + 2 * (c >> 1);
   int lo = sb * 256 + 128 * n + 16 * c, hi = lo + 64;
   float* o = out + (size_t)r * ldo;
@@ -310,14 +321,13 @@ __global__ void synth_q6k_kernel(uint8_t* qlp, uint8_t* qhp, int8_t* scp, uint16
   }
   uint16_t dh = f32_to_f16(maxs / 127.0f);
   float d = f16_to_f32(dh);
-  dp[t] = dh;
+  const int row = (int)r;
+  dp[q6k_d_off(row, b, nsb)] = dh;
   int8_t scq[16];
   for (int j = 0; j < 16; ++j) {
     scq[j] = d > 0.0f ? (int8_t)clampf(rintf(scale[j] / d), 0.0f, 127.0f) : 0;
-    scp[t * 16 + j] = scq[j];
+    scp[q6k_sc_off(row, b * 16 + j, nsb)] = scq[j];
   }
-  uint8_t* ql = qlp + t * 128;
-  uint8_t* qh = qhp + t * 64;
   for (int n = 0; n < 2; ++n) {
     for (int l = 0; l < 32; ++l) {
       uint32_t c[4];
@@ -329,9 +339,10 @@ __global__ void synth_q6k_kernel(uint8_t* qlp, uint8_t* qhp, int8_t* scp, uint16
         float q = ds > 0.0f ? clampf(rintf(v / ds), -32.0f, 31.0f) : 0.0f;
         c[u] = (uint32_t)((int)q + 32);
       }
-      ql[64 * n + l] = (uint8_t)((c[0] & 0xF) | ((c[2] & 0xF) << 4));
-      ql[64 * n + l + 32] = (uint8_t)((c[1] & 0xF) | ((c[3] & 0xF) << 4));
-      qh[32 * n + l] = (uint8_t)((c[0] >> 4) | ((c[1] >> 4) << 2) | ((c[2] >> 4) << 4) | ((c[3] >> 4) << 6));
+      qlp[q6k_ql_off(row, b * 128 + 64 * n + l, nsb)] = (uint8_t)((c[0] & 0xF) | ((c[2] & 0xF) << 4));
+      qlp[q6k_ql_off(row, b * 128 + 64 * n + l + 32, nsb)] = (uint8_t)((c[1] & 0xF) | ((c[3] & 0xF) << 4));
+      qhp[q6k_qh_off(row, b * 64 + 32 * n + l, nsb)] =
+          (uint8_t)((c[0] >> 4) | ((c[1] >> 4) << 2) | ((c[2] >> 4) << 4) | ((c[3] >> 4) << 6));
     }
   }
 }
@@ -408,10 +419,11 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s) {
     place(1, tiles * m.nsb * 512);
   } else if (fmt == FMT_Q6K) {
     PGD_CHECK(n_in % 32 == 0, kErrShape, "Q6K n_in must be a multiple of 32");
-    place(0, rows * m.nsb * 128);
-    place(1, rows * m.nsb * 64);
-    place(2, rows * m.nsb * 16);
-    place(3, rows * m.nsb * 2);
+    size_t tiles = (rows + 31) / 32;
+    place(0, tiles * m.nsb * 4096);
+    place(1, tiles * m.nsb * 2048);
+    place(2, tiles * m.nsb * 512);
+    place(3, tiles * m.nsb * 64);
   } else {
     throw Error{kErrFormat, "unknown matrix format"};
   }
@@ -426,7 +438,7 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s) {
   m.p3 = fmt == FMT_Q6K ? m.base + off[3] : nullptr;
   // zero the padding rows of the last tile, ordered before the writes that
   // follow on the same stream
-  if (fmt == FMT_A8 || fmt == FMT_Q4K) PGD_HIP(hipMemsetAsync(m.base, 0, total, s));
+  PGD_HIP(hipMemsetAsync(m.base, 0, total, s));
 }
 
 void qmat_free(QMat& m) {
@@ -470,18 +482,24 @@ void qmat_upload_kq(QMat& m, const uint8_t* blocks, hipStream_t s) {
     PGD_HIP(hipMemcpyAsync(m.p1, hdr.data(), hdr.size(), hipMemcpyHostToDevice, s));
     PGD_HIP(hipStreamSynchronize(s));
   } else if (m.fmt == FMT_Q6K) {
-    std::vector<uint8_t> ql(nb * 128), qh(nb * 64), sc(nb * 16), d(nb * 2);
-    for (size_t i = 0; i < nb; ++i) {
-      const uint8_t* b = blocks + i * 210;
-      std::copy(b, b + 128, ql.data() + i * 128);
-      std::copy(b + 128, b + 192, qh.data() + i * 64);
-      std::copy(b + 192, b + 208, sc.data() + i * 16);
-      std::copy(b + 208, b + 210, d.data() + i * 2);
-    }
+    // GGML blocks (row-major, 210 B each) -> tiled planes (same bytes, permuted)
+    const size_t tiles = ((size_t)m.n_out + 31) / 32;
+    const int nsb = m.nsb;
+    std::vector<uint8_t> ql(tiles * nsb * 4096, 0), qh(tiles * nsb * 2048, 0), sc(tiles * nsb * 512, 0);
+    std::vector<uint16_t> d(tiles * nsb * 32, 0);
+    for (int r = 0; r < m.n_out; ++r)
+      for (int sb = 0; sb < nsb; ++sb) {
+        const uint8_t* b = blocks + ((size_t)r * nsb + sb) * 210;
+        for (int i = 0; i < 128; i += 4) std::copy(b + i, b + i + 4, ql.data() + q6k_ql_off(r, sb * 128 + i, nsb));
+        for (int i = 0; i < 64; i += 4)
+          std::copy(b + 128 + i, b + 132 + i, qh.data() + q6k_qh_off(r, sb * 64 + i, nsb));
+        for (int i = 0; i < 16; ++i) sc[q6k_sc_off(r, sb * 16 + i, nsb)] = b[192 + i];
+        d[q6k_d_off(r, sb, nsb)] = (uint16_t)(b[208] | (b[209] << 8));
+      }
     PGD_HIP(hipMemcpyAsync(m.p0, ql.data(), ql.size(), hipMemcpyHostToDevice, s));
     PGD_HIP(hipMemcpyAsync(m.p1, qh.data(), qh.size(), hipMemcpyHostToDevice, s));
     PGD_HIP(hipMemcpyAsync(m.p2, sc.data(), sc.size(), hipMemcpyHostToDevice, s));
-    PGD_HIP(hipMemcpyAsync(m.p3, d.data(), d.size(), hipMemcpyHostToDevice, s));
+    PGD_HIP(hipMemcpyAsync(m.p3, d.data(), d.size() * 2, hipMemcpyHostToDevice, s));
     PGD_HIP(hipStreamSynchronize(s));
   } else {
     throw Error{kErrFormat, "k-quant upload on a non k-quant matrix"};
