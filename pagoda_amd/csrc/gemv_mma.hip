@@ -92,16 +92,17 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
 }
 
 // Fused RMSNorm (rms_zero, pagoda-hf/src/qwen3_5.rs:1736-1745) + activation
-// prep: one workgroup per output row; thread t owns 16-wide slices t, t+256,
-// ... (slice u = 4g + q), kept in registers between the two passes together
+// prep: one workgroup of NT threads per output row; thread t owns 16-wide
+// slices t, t+NT, ... (slice u = 4g + q), kept in registers between the two passes together
 // with their norm weights, which are loaded with the row (one round trip).
-constexpr int kNormMaxSlices = 8;  // n <= 256 * 16 * 8
-template <int NSL>
-__global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restrict__ x, int ldx,
-                                                           const int* __restrict__ rows_idx, int rows, int n,
-                                                           const float* __restrict__ w, float eps, float* y, int ldy,
-                                                           a8act::Dst d) {
-  __shared__ float red[4];
+constexpr int kNormMaxSlices = 8;  // n <= 256 * 16 * 8 (wide rows: 256 threads)
+template <int NSL, int NT>
+__global__ __launch_bounds__(NT) void a8_norm_prep_kernel(const float* __restrict__ x, int ldx,
+                                                          const int* __restrict__ rows_idx, int rows, int n,
+                                                          const float* __restrict__ w, float eps, float* y, int ldy,
+                                                          a8act::Dst d) {
+  constexpr int NW = NT / 64;
+  __shared__ float red[NW];
   const int r = blockIdx.x, tid = threadIdx.x;
   const int src = rows_idx ? rows_idx[r] : r;
   const float* xr = x + (size_t)src * ldx;
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < NSL; ++i) {
-    const int u = tid + 256 * i;
+    const int u = tid + NT * i;
     if (u < slices) {
       const float4* p = reinterpret_cast<const float4*>(xr + 16 * u);
       const float4* wp = reinterpret_cast<const float4*>(w + 16 * u);
@@ -133,10 +134,13 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
-  const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)n + eps);
+  float tot = red[0];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) tot += red[k];
+  const float inv = 1.0f / sqrtf(tot / (float)n + eps);
 #pragma unroll
   for (int i = 0; i < NSL; ++i) {
-    const int u = tid + 256 * i;
+    const int u = tid + NT * i;
     const bool live = u < slices;  // uniform per group of four lanes (slices % 4 == 0)
     if (live) {
 #pragma unroll
@@ -148,7 +152,7 @@ __global__ __launch_bounds__(256) void a8_norm_prep_kernel(const float* __restri
       }
     }
     // slice u = 4 g + q: quarter partners are adjacent lanes
-    if (i * 256 < slices) a8act::emit_slice(d, r, u >> 2, u & 3, v[i], live);
+    if (i * NT < slices) a8act::emit_slice(d, r, u >> 2, u & 3, v[i], live);
   }
 }
 
@@ -331,7 +335,8 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
       const float bi = bf16_to_f32(S[st] >> 16);
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) {
-        f4 Pm = {0.f, 0.f, 0.f, 0.f};
+        // the MFMA adds the codes' dot product to -1024 XSP (the 1024 + c offset)
+        f4 Pm = {CPv[bt][0], CPv[bt][1], CPv[bt][2], CPv[bt][3]};
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][0]), b0, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][1]), b1, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][2]), b0, Pm, 0, 0, 0);
@@ -340,7 +345,7 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
         // never stored)
 #pragma unroll
         for (int r = 0; r < (MODE == 3 ? 1 : 4); ++r)
-          Y[st][bt][r] = fmaf(bi, XSv[bt][r], fmaf(sc, Pm[r] + CPv[bt][r], Y[st][bt][r]));
+          Y[st][bt][r] = fmaf(bi, XSv[bt][r], fmaf(sc, Pm[r], Y[st][bt][r]));
       }
     }
   };
@@ -581,14 +586,15 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
       const float bi = bf16_to_f32(S[st] >> 16);
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) {
-        f4 Pm = {0.f, 0.f, 0.f, 0.f};
+        // the MFMA adds the codes' dot product to -1024 XSP (the 1024 + c offset)
+        f4 Pm = {CPv[bt][0], CPv[bt][1], CPv[bt][2], CPv[bt][3]};
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][0]), b0, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][1]), b1, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][2]), b0, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][3]), b1, Pm, 0, 0, 0);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
-          Y[st][bt][rr] = fmaf(bi, XSv[bt][rr], fmaf(sc, Pm[rr] + CPv[bt][rr], Y[st][bt][rr]));
+          Y[st][bt][rr] = fmaf(bi, XSv[bt][rr], fmaf(sc, Pm[rr], Y[st][bt][rr]));
       }
     }
   };
@@ -787,12 +793,13 @@ A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n
   PGD_CHECK(n % 64 == 0 && n <= 256 * 16 * gemv::kNormMaxSlices && ldx % 4 == 0, kErrShape, "norm prep width");
   A8Act a = a8_act_view(buf, rows, n);
   if (rows <= 0) return a;
-  if (n <= 256 * 16 * 2)
-    hipLaunchKernelGGL(gemv::a8_norm_prep_kernel<2>, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx, rows, n, w, eps, y,
-                       ldy, a8_act_dst(a));
+  // one 16-wide slice per thread up to 8192 wide
+  if (n <= 512 * 16)
+    hipLaunchKernelGGL((gemv::a8_norm_prep_kernel<1, 512>), dim3(rows), dim3(512), 0, s, x, ldx, rows_idx, rows, n, w,
+                       eps, y, ldy, a8_act_dst(a));
   else
-    hipLaunchKernelGGL(gemv::a8_norm_prep_kernel<gemv::kNormMaxSlices>, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx,
-                       rows, n, w, eps, y, ldy, a8_act_dst(a));
+    hipLaunchKernelGGL((gemv::a8_norm_prep_kernel<gemv::kNormMaxSlices, 256>), dim3(rows), dim3(256), 0, s, x, ldx,
+                       rows_idx, rows, n, w, eps, y, ldy, a8_act_dst(a));
   PGD_HIP(hipGetLastError());
   return a;
 }

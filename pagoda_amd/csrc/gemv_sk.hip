@@ -246,13 +246,14 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
         const h8 b1 = codes8(r.w[st].z, r.w[st].w);
         const float sc = bf16_to_f32(r.s[st] & 0xffffu);
         const float bi = bf16_to_f32(r.s[st] >> 16);
-        f4 Pm = {0.f, 0.f, 0.f, 0.f};
+        // the MFMA adds the codes' dot product to -1024 XSP (the 1024 + c offset)
+        f4 Pm = cp;
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[0]), b0, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[1]), b1, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[2]), b0, Pm, 0, 0, 0);
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[3]), b1, Pm, 0, 0, 0);
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) Y[st][bt][rr] = fmaf(bi, xs[rr], fmaf(sc, Pm[rr] + cp[rr], Y[st][bt][rr]));
+        for (int rr = 0; rr < 4; ++rr) Y[st][bt][rr] = fmaf(bi, xs[rr], fmaf(sc, Pm[rr], Y[st][bt][rr]));
       }
     }
   };
