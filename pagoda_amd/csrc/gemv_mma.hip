@@ -686,8 +686,9 @@ void launch_kernel(const GemvArgs& a, const uint4* XA, const float* CA, int nb, 
 // split of the groups: enough ranges that every matrix puts ~2000+ waves' worth
 // of work on the GPU. Depends on the shape only.
 inline int split_ranges(const GemvArgs& a) {
-  const int tiles = (a.n_out + 31) / 32;
-  return tiles >= 512 ? 4 : tiles >= 256 ? 8 : 16;
+  const int tiles = (a.n_out + 31) / 32, G = a.n_in / 64;
+  // 16 ranges only where each still streams >= 16 groups (measured on MI355X)
+  return tiles >= 512 ? 4 : (tiles >= 256 || G < 256) ? 8 : 16;
 }
 
 template <int KS, int T, int P, int EPI>
