@@ -709,7 +709,10 @@ void launch_chunk_ks(const GemvArgs& a, const uint4* XA, const float* CA, int nb
   constexpr int KP4 = KS < 4 ? KS : 4, KP8 = KS < 8 ? KS : 8;
   if (nb == 1) return launch_kernel<3, KS, KP8, 3, 1, EPI>(a, XA, CA, nb, s);
   if (nb <= 4) return launch_kernel<0, KS, KP8, 3, 1, EPI>(a, XA, CA, nb, s);
-  if (nb <= 16) return launch_kernel<1, KS, KP4, 4, 1, EPI>(a, XA, CA, nb, s);
+  // 5..16 rows: the per-wave kernel, except for matrices large enough that one
+  // operand stage shared by a workgroup's tiles streams faster (same sums)
+  if (nb <= 16 && (EPI == EPI_SWIGLU || a.n_out % 4 != 0 || ((a.n_out + 31) / 32 < 256 && a.n_in / 64 < 256)))
+    return launch_kernel<1, KS, KP4, 4, 1, EPI>(a, XA, CA, nb, s);
   if constexpr (EPI == EPI_SWIGLU) {
     // gate + up already give each wave 2 KiB of weights per KiB of operands
     launch_kernel<2, KS, KP4, 3, 1, EPI>(a, XA, CA, nb, s);

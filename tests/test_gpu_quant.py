@@ -216,7 +216,7 @@ def test_prepared_activations_shared_across_matrices(dev):
 
 
 @pytest.mark.parametrize("n_out", [8200, 8192 + 64])
-@pytest.mark.parametrize("rows", [19, 32, 45])
+@pytest.mark.parametrize("rows", [9, 19, 32, 45])
 def test_a8_two_tile_waves_large_matrix(dev, n_out, rows):
     """Matrices of 256+ row tiles run two tiles per wave when a launch holds
     17-32 rows; an odd tile count leaves the last wave with one real tile.
@@ -233,6 +233,25 @@ def test_a8_two_tile_waves_large_matrix(dev, n_out, rows):
     ref = x.astype(np.float64) @ deq.astype(np.float64).T
     assert rel_err(y, ref) < GEMV_TOL
     for i in (0, 7, rows - 1):
+        np.testing.assert_array_equal(m.gemv(x[i]).view(np.uint32), y[i].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows", [6, 16, 29])
+def test_a8_wide_matrix_shared_stage(dev, rows):
+    """A narrow matrix with K >= 16384 (256+ groups) runs 5..32-row launches
+    through the shared-operand kernel + range reduction; every row is bitwise
+    its one-row GEMV."""
+    from pagoda_amd import Matrix
+
+    n_out, K = 300, 16384
+    m = Matrix.synth(dev, 0, n_out, K, 41, 9, 0.02)
+    deq = m.dequant()
+    rng = np.random.default_rng(rows)
+    x = rng.normal(0, 1, (rows, K)).astype(np.float32)
+    y = m.gemv(x)
+    ref = x.astype(np.float64) @ deq.astype(np.float64).T
+    assert rel_err(y, ref) < GEMV_TOL
+    for i in (0, rows // 2, rows - 1):
         np.testing.assert_array_equal(m.gemv(x[i]).view(np.uint32), y[i].view(np.uint32))
 
 
