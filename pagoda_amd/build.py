@@ -27,6 +27,8 @@ COMMON = [
     "-ffp-contract=off",
     # No packed FP32 math (v_pk_*_f32) anywhere in this library.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: no v_accvgpr moves around every MFMA chain
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-result",
     "-Wno-unused-variable",

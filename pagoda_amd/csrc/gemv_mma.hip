@@ -496,18 +496,24 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
 // part[r][row][n]; a8_reduce_kernel adds the KS ranges in order 0, 1, ...
 // (the order of the in-workgroup reduction above), so results equal the
 // other modes bit for bit.
-template <int KS, int T, int P, int EPI>
+// NC = activation chunks of 32 rows per launch (2: a 64-row launch streams
+// the weights once for both; the second chunk must hold more than 4 rows,
+// i.e. use the full operand layout).
+template <int KS, int T, int P, int EPI, int NC>
 __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const uint4* __restrict__ XA,
                                                                const float* __restrict__ CA, int nb,
                                                                float* __restrict__ part) {
   static_assert(T == 2 || T == 4 || T == 8, "operand quarters per wave");
-  constexpr int NBT = 2;
+  static_assert(NC == 1 || NC == 2, "one or two chunks");
+  static_assert(T >= 2 * NC, "one constant block per wave");
+  constexpr int NBT = 2 * NC;
   static_assert(EPI != EPI_SWIGLU, "one matrix per wave");
   constexpr int NS = 2;
-  constexpr int SHARED = 8192 + 512;        // operands + constants of both batch tiles
+  constexpr int CHUNK = 8192 + 512;         // per chunk: operands + constants of both batch tiles
+  constexpr int SHARED = NC * CHUNK;
   constexpr int PERW = NS * 1024 + 256;     // a wave's weights + scale/bias
   constexpr int STAGE = SHARED + T * PERW;
-  constexpr int XPW = 8 / T;                // operand loads per wave (8 x 1 KiB per group)
+  constexpr int XPW = 8 * NC / T;           // operand loads per wave (8 x 1 KiB per group and chunk)
   constexpr int NDMA = NS + 1 + XPW + 1;    // weights, scale/bias, operands, one constant block
   static_assert(P >= 3, "one stage is refilled while the next is in flight");
   constexpr int NWAIT = (P - 2) * NDMA;
@@ -533,9 +539,10 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
   }
   const uint32_t* ssrc =
       reinterpret_cast<const uint32_t*>(a.p1) + ((size_t)rtile * G << 5) + 16 * min(lane >> 4, NS - 1) + j;
-  // this wave's share of the operands: loads XPW * wave .. of the 8 (tile bt = load / 4, operand load % 4)
+  // this wave's share of the operands: loads XPW * wave .. of the 8 NC (chunk =
+  // load / 8, tile bt = load / 4 % 2, operand load % 4)
   const int x0 = XPW * wave;
-  const int cbt = wave & 1;  // constant block (waves 2.. load a copy of 0, 1's)
+  const int cbt = wave % (2 * NC);  // constant block (chunk cbt / 2, tile cbt % 2; later waves load copies)
 
   auto issue = [&](int g, int slot) {
     char* sb = smem + slot * STAGE;
@@ -545,10 +552,11 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
     dma4(ssrc + ((size_t)g << 5), mine + NS * 1024);
 #pragma unroll
     for (int i = 0; i < XPW; ++i) {
-      const int x = x0 + i, xbt = x >> 2, xi = x & 3;
-      dma16(XA + ((size_t)g * 2 + xbt) * 256 + xi * 64 + lane, sb + xbt * 4096 + xi * 1024);
+      const int x = x0 + i, xc = x >> 3, xbt = (x >> 2) & 1, xi = x & 3;
+      dma16(XA + (((size_t)xc * G + g) * 2 + xbt) * 256 + xi * 64 + lane, sb + xc * CHUNK + xbt * 4096 + xi * 1024);
     }
-    dma4(CA + ((size_t)g * 2 + cbt) * 64 + lane, sb + 8192 + cbt * 256);
+    const int cc = cbt >> 1, ct = cbt & 1;
+    dma4(CA + (((size_t)cc * G + g) * 2 + ct) * 64 + lane, sb + cc * CHUNK + 8192 + ct * 256);
   };
 
   f4 Y[NS][NBT];
@@ -557,18 +565,19 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int slot) {
+  // one chunk's two batch tiles at a time (the weights are read again per chunk)
+  auto compute_chunk = [&](int slot, int c) {
     const uint32_t base = smem_lds + slot * STAGE;
     const uint32_t mine = base + SHARED + wave * PERW;
+    const uint32_t cb = base + c * CHUNK;
     uint4 W[NS];
     uint32_t S[NS];
-    uint4 X[NBT][4];
-    float4 CC[NBT][4];
-    StageReads<2, NS>::run(mine + 16 * lane, mine + NS * 1024 + 4 * j, base + 16 * lane, base + 8192 + 16 * q, W, S, X,
-                           CC);
-    float CPv[NBT][4], XSv[NBT][4];
+    uint4 X[2][4];
+    float4 CC[2][4];
+    StageReads<2, NS>::run(mine + 16 * lane, mine + NS * 1024 + 4 * j, cb + 16 * lane, cb + 8192 + 16 * q, W, S, X, CC);
+    float CPv[2][4], XSv[2][4];
 #pragma unroll
-    for (int bt = 0; bt < NBT; ++bt) {
+    for (int bt = 0; bt < 2; ++bt) {
       CPv[bt][0] = CC[bt][0].x + CC[bt][1].x;
       CPv[bt][1] = CC[bt][0].y + CC[bt][1].y;
       CPv[bt][2] = CC[bt][0].z + CC[bt][1].z;
@@ -585,7 +594,7 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
       const float sc = bf16_to_f32(S[st] & 0xffffu);
       const float bi = bf16_to_f32(S[st] >> 16);
 #pragma unroll
-      for (int bt = 0; bt < NBT; ++bt) {
+      for (int bt = 0; bt < 2; ++bt) {
         // the MFMA adds the codes' dot product to -1024 XSP (the 1024 + c offset)
         f4 Pm = {CPv[bt][0], CPv[bt][1], CPv[bt][2], CPv[bt][3]};
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][0]), b0, Pm, 0, 0, 0);
@@ -594,9 +603,13 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
         Pm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, X[bt][3]), b1, Pm, 0, 0, 0);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
-          Y[st][bt][rr] = fmaf(bi, XSv[bt][rr], fmaf(sc, Pm[rr], Y[st][bt][rr]));
+          Y[st][2 * c + bt][rr] = fmaf(bi, XSv[bt][rr], fmaf(sc, Pm[rr], Y[st][2 * c + bt][rr]));
       }
     }
+  };
+  auto compute = [&](int slot) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) compute_chunk(slot, c);
   };
 
   // step i: wait for group g0 + i (P - 2 later groups stay in flight), publish
@@ -691,13 +704,13 @@ inline int split_ranges(const GemvArgs& a) {
   return tiles >= 512 ? 4 : (tiles >= 256 || G < 256) ? 8 : 16;
 }
 
-template <int KS, int T, int P, int EPI>
+template <int KS, int T, int P, int EPI, int NC = 1>
 void launch_shared(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
   static_assert(EPI != EPI_SWIGLU, "SwiGLU keeps the per-wave kernel");
   const int tiles = (a.n_out + 31) / 32;
   float* part = static_cast<float*>(gemv_scratch(s, (size_t)KS * nb * a.n_out * sizeof(float), 1));
-  hipLaunchKernelGGL((a8_mma_shared_kernel<KS, T, P, EPI>), dim3((tiles + T - 1) / T, KS), dim3(64 * T), 0, s, a, XA,
-                     CA, nb, part);
+  hipLaunchKernelGGL((a8_mma_shared_kernel<KS, T, P, EPI, NC>), dim3((tiles + T - 1) / T, KS), dim3(64 * T), 0, s, a,
+                     XA, CA, nb, part);
   const int n4 = nb * (a.n_out / 4);
   hipLaunchKernelGGL((a8_reduce_kernel<KS, EPI>), dim3((n4 + 255) / 256), dim3(256), 0, s, a, nb, part);
 }
@@ -734,6 +747,18 @@ void launch_chunk(const GemvArgs& a, const uint4* XA, const float* CA, int nb, h
   }
 }
 
+// two 32-row chunks in one launch of the shared-operand kernel
+template <int EPI>
+void launch_pair(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
+  if constexpr (EPI != EPI_SWIGLU) {
+    switch (split_ranges(a)) {
+      case 4: return launch_shared<4, 8, 3, EPI, 2>(a, XA, CA, nb, s);
+      case 8: return launch_shared<8, 8, 3, EPI, 2>(a, XA, CA, nb, s);
+      default: return launch_shared<16, 4, 3, EPI, 2>(a, XA, CA, nb, s);
+    }
+  }
+}
+
 template <int EPI>
 void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   PGD_CHECK(act.K == a.n_in, kErrShape, "prepared activations have the wrong width");
@@ -741,12 +766,23 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   const uint4* XA = reinterpret_cast<const uint4*>(act.XA);
   int rows = act.rows;
   const bool sk = a8_sk_wanted(a, EPI);
-  for (int c = 0; rows > 0; ++c) {
-    const int nb = rows < 32 ? rows : 32;
+  // plain matrices stream their weights once per 64 rows when the second
+  // chunk of a pair holds more than 4 rows (full operand layout)
+  const bool pairs = EPI != EPI_SWIGLU && !sk && a.n_out % 4 == 0;
+  for (int c = 0; rows > 0;) {
     const uint4* xa = XA + (size_t)c * G * 2 * 256;
     const float* ca = act.CA + (size_t)c * G * 2 * 64;
-    if (sk && nb >= 5) run_a8_sk_chunk(a, xa, ca, nb, EPI, s);
-    else launch_chunk<EPI>(a, xa, ca, nb, s);
+    int nb;
+    if (pairs && rows > 36) {
+      nb = rows < 64 ? rows : 64;
+      launch_pair<EPI>(a, xa, ca, nb, s);
+      c += 2;
+    } else {
+      nb = rows < 32 ? rows : 32;
+      if (sk && nb >= 5) run_a8_sk_chunk(a, xa, ca, nb, EPI, s);
+      else launch_chunk<EPI>(a, xa, ca, nb, s);
+      c += 1;
+    }
     PGD_HIP(hipGetLastError());
     rows -= nb;
     if (a.y) a.y += (size_t)nb * a.ldy;

@@ -216,7 +216,7 @@ def test_prepared_activations_shared_across_matrices(dev):
 
 
 @pytest.mark.parametrize("n_out", [8200, 8192 + 64])
-@pytest.mark.parametrize("rows", [9, 19, 32, 45])
+@pytest.mark.parametrize("rows", [9, 19, 32, 45, 64])
 def test_a8_two_tile_waves_large_matrix(dev, n_out, rows):
     """Matrices of 256+ row tiles run two tiles per wave when a launch holds
     17-32 rows; an odd tile count leaves the last wave with one real tile.
@@ -236,11 +236,12 @@ def test_a8_two_tile_waves_large_matrix(dev, n_out, rows):
         np.testing.assert_array_equal(m.gemv(x[i]).view(np.uint32), y[i].view(np.uint32))
 
 
-@pytest.mark.parametrize("rows", [6, 16, 29])
+@pytest.mark.parametrize("rows", [6, 16, 29, 40, 64])
 def test_a8_wide_matrix_shared_stage(dev, rows):
     """A narrow matrix with K >= 16384 (256+ groups) runs 5..32-row launches
-    through the shared-operand kernel + range reduction; every row is bitwise
-    its one-row GEMV."""
+    through the shared-operand kernel + range reduction, and 37..64 rows as
+    one launch over two activation chunks; every row is bitwise its one-row
+    GEMV."""
     from pagoda_amd import Matrix
 
     n_out, K = 300, 16384
@@ -253,6 +254,32 @@ def test_a8_wide_matrix_shared_stage(dev, rows):
     assert rel_err(y, ref) < GEMV_TOL
     for i in (0, rows // 2, rows - 1):
         np.testing.assert_array_equal(m.gemv(x[i]).view(np.uint32), y[i].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows", [40, 64])
+def test_a8_pair_launch_residual(dev, rows):
+    """The residual epilogue of a two-chunk launch (in place, y = res):
+    equals residual + the plain GEMV bit for bit."""
+    from pagoda_amd import Matrix
+    from pagoda_amd.matrix import act_bytes, act_prep_dev
+
+    n_out, K = 8256, 512
+    m = Matrix.synth(dev, 0, n_out, K, 43, 11, 0.02)
+    rng = np.random.default_rng(100 + rows)
+    x = rng.normal(0, 1, (rows, K)).astype(np.float32)
+    res = rng.normal(0, 1, (rows, n_out)).astype(np.float32)
+    xd = dev.upload(x)
+    act = dev.alloc(act_bytes(rows, K))
+    act_prep_dev(dev, xd, K, rows, K, act)
+    yd = dev.alloc(rows * n_out * 4)
+    m.gemv_act_dev(act, rows, yd, n_out)
+    plain = dev.download(yd, (rows, n_out), np.float32)
+    rd = dev.upload(res)
+    m.gemv_act_dev(act, rows, rd, n_out, rd, n_out)
+    got = dev.download(rd, (rows, n_out), np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), (res + plain).view(np.uint32))
+    for p in (xd, act, yd, rd):
+        dev.free(p)
 
 
 def _class_checks(full, sub7, sub13, single, ref):
