@@ -74,15 +74,21 @@ struct Q4Raw {
   uint4 x[2][NBT][XF16 ? 1 : 2];  // per sub-block half and batch tile: 8 activations (f16: 16 B, f32: 32 B)
 };
 
+// KS == 1: a workgroup of kTilesKS1 waves, one tile each (no k split)
+constexpr int kTilesKS1 = 4;
+
 template <int NBT, int KS, int PF, bool XF16, int EPI>
-__global__ __launch_bounds__(64 * KS) void q4k_mma_kernel(GemvArgs a, int nb) {
+__global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kernel(GemvArgs a, int nb) {
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr int NS = DUAL ? 4 : 2;
   __shared__ f4 red[KS > 1 ? KS - 1 : 1][NS][NBT][64];
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, q = lane >> 4;
   const int G = a.n_in >> 6, nsb = a.nsb, G4 = 4 * nsb;
-  const int tile = blockIdx.x;
+  // wave = this wave's k range; KS == 1: every wave its own tile
+  const int wave = KS == 1 ? 0 : wv;
+  const int tile = KS == 1 ? blockIdx.x * kTilesKS1 + wv : blockIdx.x;
+  if (tile >= (a.n_out + 31) / 32) return;
 
   const uint8_t* wbase[NS];
   const uint8_t* hbase[NS];
@@ -239,7 +245,12 @@ inline int q4k_split(const GemvArgs& a) {
 
 template <int NBT, int KS, bool XF16, int EPI>
 void q4k_launch(const GemvArgs& a, int nb, hipStream_t s) {
-  hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI>), dim3((a.n_out + 31) / 32), dim3(64 * KS), 0, s, a, nb);
+  const int tiles = (a.n_out + 31) / 32;
+  if constexpr (KS == 1)
+    hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
+                       dim3(64 * kTilesKS1), 0, s, a, nb);
+  else
+    hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI>), dim3(tiles), dim3(64 * KS), 0, s, a, nb);
 }
 
 template <int NBT, bool XF16, int EPI>
@@ -302,14 +313,17 @@ struct Q6Raw {
 };
 
 template <int NBT, int KS, bool XF16, int EPI>
-__global__ __launch_bounds__(64 * KS) void q6k_mma_kernel(GemvArgs a, int nb) {
+__global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q6k_mma_kernel(GemvArgs a, int nb) {
   static_assert(EPI != EPI_SWIGLU, "one matrix per wave");
   constexpr int NS = 2;
   __shared__ f4 red[KS > 1 ? KS - 1 : 1][NS][NBT][64];
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, q = lane >> 4;
   const int H = a.n_in >> 7, nsb = a.nsb;
-  const int tile = blockIdx.x;
+  // wave = this wave's k range; KS == 1: every wave its own tile
+  const int wave = KS == 1 ? 0 : wv;
+  const int tile = KS == 1 ? blockIdx.x * kTilesKS1 + wv : blockIdx.x;
+  if (tile >= (a.n_out + 31) / 32) return;
 
   // per half u: block tile * 2 nsb + u of each plane
   const size_t blk0 = (size_t)tile * 2 * nsb;
@@ -462,7 +476,12 @@ inline int q6k_split(const GemvArgs& a) {
 
 template <int NBT, int KS, bool XF16, int EPI>
 void q6k_launch(const GemvArgs& a, int nb, hipStream_t s) {
-  hipLaunchKernelGGL((q6k_mma_kernel<NBT, KS, XF16, EPI>), dim3((a.n_out + 31) / 32), dim3(64 * KS), 0, s, a, nb);
+  const int tiles = (a.n_out + 31) / 32;
+  if constexpr (KS == 1)
+    hipLaunchKernelGGL((q6k_mma_kernel<NBT, KS, XF16, EPI>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
+                       dim3(64 * kTilesKS1), 0, s, a, nb);
+  else
+    hipLaunchKernelGGL((q6k_mma_kernel<NBT, KS, XF16, EPI>), dim3(tiles), dim3(64 * KS), 0, s, a, nb);
 }
 
 template <int NBT, bool XF16, int EPI>
