@@ -58,6 +58,7 @@ constexpr int kItemFields = 5;  // page_off, npages, row_off, nrows, chunk index
 // DIRECT: every row of the launch has one chunk; the item normalizes and
 // writes the final output (gate, out / prepared operands) itself.
 constexpr int kSubsets = 4;
+constexpr int kXcds = 8;  // MI355X: accelerator complex dies, one L2 each
 
 template <int HD>
 struct ItemLds {
@@ -73,7 +74,13 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
   constexpr int T = HD / 4;    // QK k-steps; lane (i, kq) holds d = T kq + t
   constexpr int NT = HD / 16;  // PV n-tiles; lane (j, kq) holds d = NT j + nt
   __shared__ __attribute__((aligned(16))) ItemLds<HD> sh;
-  const int item = blockIdx.x, kvh = blockIdx.y;
+  // workgroups are dispatched to the 8 XCDs round robin (linear id % 8), each
+  // with its own L2: give XCD x a contiguous range of the (kv head, item)
+  // work list, so the items of one chunk (adjacent in the plan) share an L2
+  const int total = gridDim.x, lin = blockIdx.x;
+  const int xcd = lin % kXcds, per = total / kXcds, rem = total % kXcds;
+  const int w = xcd * per + min(xcd, rem) + lin / kXcds;
+  const int item = w % plan.n_items, kvh = w / plan.n_items;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 15, kq = lane >> 4;
   const int* it = plan.items + (size_t)item * kItemFields;
@@ -328,13 +335,13 @@ void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L,
   const size_t ml_floats = (size_t)plan.n_slots * L.kv_heads * G * 2;
   // one chunk per row (n_slots == rows): the items finish the rows themselves
   if (plan.n_slots == rows) {
-    hipLaunchKernelGGL((attn_item_kernel<HD, true>), dim3(plan.n_items, L.kv_heads), dim3(256), 0, s, q, gate, out,
+    hipLaunchKernelGGL((attn_item_kernel<HD, true>), dim3(plan.n_items * L.kv_heads), dim3(256), 0, s, q, gate, out,
                        L, m, plan, G, nullptr, nullptr, act);
     return;
   }
   PGD_CHECK(plan.max_row_slots <= kMergeMax, kErrShape, "attention context too long for the merge");
   float* ws = static_cast<float*>(gemv::gemv_scratch(s, (o_floats + ml_floats) * sizeof(float), 4));
-  hipLaunchKernelGGL((attn_item_kernel<HD, false>), dim3(plan.n_items, L.kv_heads), dim3(256), 0, s, q, gate, out,
+  hipLaunchKernelGGL((attn_item_kernel<HD, false>), dim3(plan.n_items * L.kv_heads), dim3(256), 0, s, q, gate, out,
                      L, m, plan, G, ws, ws + o_floats, act);
   hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(rows, L.kv_heads, G), dim3(HD), 0, s,
                      gate, out, L, plan, G, ws, ws + o_floats, act);

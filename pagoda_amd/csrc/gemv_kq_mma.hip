@@ -76,19 +76,45 @@ struct Q4Raw {
 
 // KS == 1: a workgroup of kTilesKS1 waves, one tile each (no k split)
 constexpr int kTilesKS1 = 4;
+// activation rows staged in LDS (XL kernels): at most this many bytes, rows
+// padded by 16 B against bank conflicts
+constexpr int kXLdsMax = 64 * 1024;
+__host__ __device__ inline int x_lds_stride(int K, bool f16) { return K * (f16 ? 2 : 4) + 16; }
 
-template <int NBT, int KS, int PF, bool XF16, int EPI>
+// rows 0 .. 16 NBT - 1 of the launch's activations into LDS (rows past the
+// batch repeat the last one); every thread of the workgroup takes part
+template <int NBT, bool XF16>
+__device__ inline void stage_x(char* xs, const GemvArgs& a, int nb) {
+  constexpr int XE = XF16 ? 2 : 4;
+  const int K = a.n_in, RS = x_lds_stride(K, XF16);
+  const int nvec = K * XE / 16, total = 16 * NBT * nvec;
+  const uint8_t* xb = reinterpret_cast<const uint8_t*>(a.x);
+  for (int i = threadIdx.x; i < total; i += blockDim.x) {
+    const int b = i / nvec, c = i - b * nvec;
+    const uint4 v = *reinterpret_cast<const uint4*>(xb + ((size_t)min(b, nb - 1) * a.ldx) * XE + c * 16);
+    *reinterpret_cast<uint4*>(xs + b * RS + c * 16) = v;
+  }
+  __syncthreads();
+}
+
+// XL (KS == 1 only): the activation rows are staged in LDS once per
+// workgroup and read from there; the register ring then carries weights only.
+template <int NBT, int KS, int PF, bool XF16, int EPI, bool XL = false>
 __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kernel(GemvArgs a, int nb) {
+  static_assert(!XL || KS == 1, "staged activations with whole-K waves only");
+  extern __shared__ __attribute__((aligned(16))) char xs[];
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr int NS = DUAL ? 4 : 2;
   __shared__ f4 red[KS > 1 ? KS - 1 : 1][NS][NBT][64];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, q = lane >> 4;
   const int G = a.n_in >> 6, nsb = a.nsb, G4 = 4 * nsb;
+  if constexpr (XL) stage_x<NBT, XF16>(xs, a, nb);
   // wave = this wave's k range; KS == 1: every wave its own tile
   const int wave = KS == 1 ? 0 : wv;
   const int tile = KS == 1 ? blockIdx.x * kTilesKS1 + wv : blockIdx.x;
   if (tile >= (a.n_out + 31) / 32) return;
+  const int XRS = x_lds_stride(a.n_in, XF16);
 
   const uint8_t* wbase[NS];
   const uint8_t* hbase[NS];
@@ -115,18 +141,25 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kerne
       R.w[st] = *reinterpret_cast<const uint2*>(wbase[st] + (size_t)g * 1024);
       R.hdr[st] = *reinterpret_cast<const uint4*>(hbase[st] + (size_t)(g >> 2) * 512);
     }
+    if constexpr (!XL) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int bt = 0; bt < NBT; ++bt) {
-        const int k0 = 64 * g + 32 * h + 8 * q;
-        if constexpr (XF16) {
-          R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 2);
-        } else {
-          R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4);
-          R.x[h][bt][1] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4 + 16);
+        for (int bt = 0; bt < NBT; ++bt) {
+          const int k0 = 64 * g + 32 * h + 8 * q;
+          if constexpr (XF16) {
+            R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 2);
+          } else {
+            R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4);
+            R.x[h][bt][1] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4 + 16);
+          }
         }
-      }
+    }
+  };
+  // staged activations: the same 16 (f16) or 32 (f32) bytes, from LDS
+  auto x_lds = [&](int g, int h, int bt, int i) -> uint4 {
+    const int k0 = 64 * g + 32 * h + 8 * q;
+    return *reinterpret_cast<const uint4*>(xs + (16 * bt + j) * XRS + k0 * (XF16 ? 2 : 4) + 16 * i);
   };
 
   f4 Y[NS][NBT];
@@ -144,14 +177,16 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kerne
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) {
+        const uint4 x0 = XL ? x_lds(g, h, bt, 0) : R.x[h][bt][0];
         if constexpr (XF16) {
-          xh[h][bt] = __builtin_bit_cast(h8, R.x[h][bt][0]);
+          xh[h][bt] = __builtin_bit_cast(h8, x0);
           XS[h][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[h][bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         } else {
-          const float v[8] = {__builtin_bit_cast(float, R.x[h][bt][0].x), __builtin_bit_cast(float, R.x[h][bt][0].y),
-                              __builtin_bit_cast(float, R.x[h][bt][0].z), __builtin_bit_cast(float, R.x[h][bt][0].w),
-                              __builtin_bit_cast(float, R.x[h][bt][1].x), __builtin_bit_cast(float, R.x[h][bt][1].y),
-                              __builtin_bit_cast(float, R.x[h][bt][1].z), __builtin_bit_cast(float, R.x[h][bt][1].w)};
+          const uint4 x1 = XL ? x_lds(g, h, bt, 1) : R.x[h][bt][XF16 ? 0 : 1];
+          const float v[8] = {__builtin_bit_cast(float, x0.x), __builtin_bit_cast(float, x0.y),
+                              __builtin_bit_cast(float, x0.z), __builtin_bit_cast(float, x0.w),
+                              __builtin_bit_cast(float, x1.x), __builtin_bit_cast(float, x1.y),
+                              __builtin_bit_cast(float, x1.z), __builtin_bit_cast(float, x1.w)};
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const _Float16 hv = (_Float16)v[e];
@@ -235,6 +270,9 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kerne
   }
 }
 
+#ifndef Q4_LPF
+#define Q4_LPF 2
+#endif
 // split of the groups: depends on the matrix shape only
 inline int q4k_split(const GemvArgs& a) {
   const int tiles = (a.n_out + 31) / 32, G = a.n_in / 64;
@@ -246,11 +284,18 @@ inline int q4k_split(const GemvArgs& a) {
 template <int NBT, int KS, bool XF16, int EPI>
 void q4k_launch(const GemvArgs& a, int nb, hipStream_t s) {
   const int tiles = (a.n_out + 31) / 32;
-  if constexpr (KS == 1)
-    hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
-                       dim3(64 * kTilesKS1), 0, s, a, nb);
-  else
+  const size_t xlds = (size_t)16 * NBT * x_lds_stride(a.n_in, XF16);
+  if constexpr (KS == 1) {
+    // staged activations pay at <= 16 rows (measured: slower at 17..32)
+    if (NBT == 1 && xlds <= kXLdsMax)
+      hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, Q4_LPF, XF16, EPI, true>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
+                         dim3(64 * kTilesKS1), xlds, s, a, nb);
+    else
+      hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
+                         dim3(64 * kTilesKS1), 0, s, a, nb);
+  } else {
     hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI>), dim3(tiles), dim3(64 * KS), 0, s, a, nb);
+  }
 }
 
 template <int NBT, bool XF16, int EPI>
@@ -466,6 +511,143 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q6k_mma_kerne
   }
 }
 
+// Tall matrices with a short K (no k split, one wave per tile): the launch's
+// activation rows are staged in LDS once per workgroup (rows padded by 16 B
+// against bank conflicts), so the tiles of a workgroup share one copy and
+// only the weights stream through a PF-deep register ring. Same arithmetic
+// and order as q6k_mma_kernel with KS == 1.
+
+template <int NS>
+struct Q6W {
+  uint4 ql[NS];
+  uint2 qh[NS];
+  uint2 sc[NS];
+  uint32_t d[NS];
+};
+
+template <int NBT, int PF, bool XF16, int EPI>
+__global__ __launch_bounds__(64 * kTilesKS1) void q6k_lds_kernel(GemvArgs a, int nb) {
+  static_assert(EPI != EPI_SWIGLU, "one matrix per wave");
+  constexpr int NS = 2, XE = XF16 ? 2 : 4;
+  extern __shared__ __attribute__((aligned(16))) char xs[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, q = lane >> 4;
+  const int H = a.n_in >> 7, nsb = a.nsb, K = a.n_in;
+  const int RS = x_lds_stride(K, XF16);
+  stage_x<NBT, XF16>(xs, a, nb);
+  const int tile = blockIdx.x * kTilesKS1 + wv;
+  if (tile >= (a.n_out + 31) / 32) return;
+
+  const size_t blk0 = (size_t)tile * 2 * nsb;
+  const uint8_t* qlb[NS];
+  const uint8_t* qhb[NS];
+  const uint8_t* scb[NS];
+  const uint16_t* db[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int ln = (4 * st + q) * 16 + j;
+    qlb[st] = a.p0 + (blk0 << 11) + ln * 16;
+    qhb[st] = a.p1 + (blk0 << 10) + ln * 8;
+    scb[st] = a.p2 + (blk0 << 8) + (16 * st + j) * 8;
+    db[st] = reinterpret_cast<const uint16_t*>(a.p3) + (size_t)tile * nsb * 32 + 16 * st + j;
+  }
+  using W = Q6W<NS>;
+  auto load = [&](int u, W& R) {
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      R.ql[st] = *reinterpret_cast<const uint4*>(qlb[st] + ((size_t)u << 11));
+      R.qh[st] = *reinterpret_cast<const uint2*>(qhb[st] + ((size_t)u << 10));
+      R.sc[st] = *reinterpret_cast<const uint2*>(scb[st] + ((size_t)u << 8));
+      R.d[st] = db[st][(u >> 1) * 32];
+    }
+  };
+
+  f4 Y[NS][NBT];
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+  const h4 ones = {1, 1, 1, 1};
+  const char* xl0 = xs + j * RS + 4 * q * XE;
+
+  auto compute = [&](int u, const W& R) {
+    float dv[NS];
+#pragma unroll
+    for (int st = 0; st < NS; ++st) dv[st] = f16_to_f32(R.d[st] & 0xffffu);
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) {
+      h4 xh[NBT], xlo[NBT];
+      f4 XS[NBT];
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const char* xp = xl0 + 16 * bt * RS + (128 * u + 16 * sb) * XE;
+        if constexpr (XF16) {
+          xh[bt] = __builtin_bit_cast(h4, *reinterpret_cast<const uint2*>(xp));
+          XS[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        } else {
+          const float4 v4 = *reinterpret_cast<const float4*>(xp);
+          const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const _Float16 hv = (_Float16)v[e];
+            xh[bt][e] = hv;
+            xlo[bt][e] = (_Float16)(v[e] - (float)hv);
+          }
+          f4 t = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          XS[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo[bt], ones, t, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        const uint32_t scw = sb < 4 ? R.sc[st].x : R.sc[st].y;
+        const float sc = (float)(int8_t)((scw >> (8 * (sb & 3))) & 255u);
+        const float ca = dv[st] * sc;
+        const float cb = 1056.0f * ca;
+        const uint32_t qlw = (sb & 3) == 0 ? R.ql[st].x : (sb & 3) == 1 ? R.ql[st].y : (sb & 3) == 2 ? R.ql[st].z : R.ql[st].w;
+        const h4 bq = q6_codes(qlw, (sb & 1) ? R.qh[st].y : R.qh[st].x, sb >> 2, 2 * (sb >> 1));
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+          f4 P = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], bq, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          if constexpr (!XF16) P = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo[bt], bq, P, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(ca, P[r], fmaf(-cb, XS[bt][r], Y[st][bt][r]));
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // PF halves in flight; loads past the last half re-read it (cache hits)
+  W buf[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) load(min(i, H - 1), buf[i]);
+  for (int u = 0; u < H; u += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      if (u + i < H) compute(u + i, buf[i]);
+      load(min(u + i + PF, H - 1), buf[i]);
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int n = tile * 32 + 16 * st + j;
+    if (n >= a.n_out) continue;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int b = 16 * bt + 4 * q + r;
+        if (b >= nb) continue;
+        const size_t o = (size_t)b * a.ldy + n;
+        if constexpr (EPI == EPI_STORE) a.y[o] = Y[st][bt][r];
+        if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];
+      }
+  }
+}
+
+#ifndef Q6_LPF
+#define Q6_LPF 2
+#endif
 // split of the 128-element halves: depends on the matrix shape only
 inline int q6k_split(const GemvArgs& a) {
   const int tiles = (a.n_out + 31) / 32, H = a.n_in / 128;
@@ -477,7 +659,11 @@ inline int q6k_split(const GemvArgs& a) {
 template <int NBT, int KS, bool XF16, int EPI>
 void q6k_launch(const GemvArgs& a, int nb, hipStream_t s) {
   const int tiles = (a.n_out + 31) / 32;
-  if constexpr (KS == 1)
+  const size_t xlds = (size_t)16 * NBT * x_lds_stride(a.n_in, XF16);
+  if (KS == 1 && xlds <= kXLdsMax)
+    hipLaunchKernelGGL((q6k_lds_kernel<NBT, Q6_LPF, XF16, EPI>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
+                       dim3(64 * kTilesKS1), xlds, s, a, nb);
+  else if constexpr (KS == 1)
     hipLaunchKernelGGL((q6k_mma_kernel<NBT, KS, XF16, EPI>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
                        dim3(64 * kTilesKS1), 0, s, a, nb);
   else

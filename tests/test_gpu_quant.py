@@ -185,6 +185,34 @@ def test_config2_sweep_f16_activations(dev, fmt, shape, rows):
     dev.free(yd)
 
 
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("x_f16", [True, False])
+def test_kquant_tall_matrix_staged_activations(dev, fmt, x_f16):
+    """Tall Q4_K/Q6_K matrices (>= 1024 row tiles, K = 896: one wave per tile)
+    stage the launch's activation rows in LDS once per workgroup. Checked
+    against fp64 at 1, 17 and 64 rows, and each batched row bitwise against
+    its one-row GEMV."""
+    from pagoda_amd import Matrix
+
+    n_out, n_in = 33000, 896
+    m = Matrix.synth(dev, fmt, n_out, n_in, 91, fmt + 40, 0.02)
+    deq = m.dequant().astype(np.float64)
+    rng = np.random.default_rng(fmt * 2 + int(x_f16))
+    x = rng.normal(0, 1, (64, n_in)).astype(np.float16 if x_f16 else np.float32)
+    xd = dev.upload(x)
+    yd = dev.alloc(64 * n_out * 4)
+    outs = {}
+    for rows in (1, 17, 64):
+        m.gemv_dev(xd, n_in, rows, yd, n_out, x_f16=x_f16)
+        outs[rows] = dev.download(yd, (rows, n_out), np.float32)
+        ref = x[:rows].astype(np.float64) @ deq.T
+        assert rel_err(outs[rows], ref) < GEMV_TOL
+    np.testing.assert_array_equal(outs[17][0].view(np.uint32), outs[1][0].view(np.uint32))
+    np.testing.assert_array_equal(outs[64][:17].view(np.uint32), outs[17].view(np.uint32))
+    dev.free(xd)
+    dev.free(yd)
+
+
 def test_prepared_activations_shared_across_matrices(dev):
     """One activation prep feeds several A8 matrices (qwen3_gemv.rs:149-253
     gemv_shared); results are bitwise those of the unprepared calls."""
