@@ -330,8 +330,9 @@ void q4k_rows(GemvArgs a, int nrows, hipStream_t s) {
 // q = (ql[e % 64] nibble e / 64) | ((qh[e % 32] >> 2 (e / 32)) & 3) << 4 and
 // weight d * sc[e / 16] * (q - 32). The scale changes every 16 elements, so
 // one v_mfma_f32_16x16x16_f16 covers one 16-element sub-block s:
-//   P[b, n] = sum (1024 + q) x,  XS[b] = sum x  (MFMA against ones)
-//   Y += d sc P - 1056 d sc XS
+//   XS[b] = sum x  (MFMA against ones)
+//   P[b, n] = -1056 XS + sum (1024 + q) x   (the chain starts from -1056 XS)
+//   Y += d sc P
 // Lane (j, quarter q) holds elements 16 s + 4 q .. + 3 of every sub-block:
 // ql bytes 16 (s % 4) + 4 q (nibble s / 4) and qh bytes 16 (s % 2) + 4 q
 // (shift 2 (s / 2)): four ql dwords and two qh dwords per half and row,
@@ -447,19 +448,22 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q6k_mma_kerne
           XS[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xl[bt], ones, t, 0, 0, 0);
         }
       }
+      f4 NXS[NBT];
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) NXS[bt] = XS[bt] * -1056.0f;
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         const uint32_t scw = sb < 4 ? R.sc[st].x : R.sc[st].y;
         const float sc = (float)(int8_t)((scw >> (8 * (sb & 3))) & 255u);
         const float ca = dv[st] * sc;
-        const float cb = 1056.0f * ca;
         const h4 bq = q6_codes(R.ql[st][sb & 3], R.qh[st][sb & 1], sb >> 2, 2 * (sb >> 1));
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
-          f4 P = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], bq, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          // the chain starts from -1056 XS: P = sum (q - 32) x
+          f4 P = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], bq, NXS[bt], 0, 0, 0);
           if constexpr (!XF16) P = __builtin_amdgcn_mfma_f32_16x16x16f16(xl[bt], bq, P, 0, 0, 0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(ca, P[r], fmaf(-cb, XS[bt][r], Y[st][bt][r]));
+          for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(ca, P[r], Y[st][bt][r]);
         }
       }
       // one sub-block at a time: keeps the operands of the others out of registers
@@ -597,20 +601,23 @@ __global__ __launch_bounds__(64 * kTilesKS1) void q6k_lds_kernel(GemvArgs a, int
           XS[bt] = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo[bt], ones, t, 0, 0, 0);
         }
       }
+      f4 NXS[NBT];
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) NXS[bt] = XS[bt] * -1056.0f;
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         const uint32_t scw = sb < 4 ? R.sc[st].x : R.sc[st].y;
         const float sc = (float)(int8_t)((scw >> (8 * (sb & 3))) & 255u);
         const float ca = dv[st] * sc;
-        const float cb = 1056.0f * ca;
         const uint32_t qlw = (sb & 3) == 0 ? R.ql[st].x : (sb & 3) == 1 ? R.ql[st].y : (sb & 3) == 2 ? R.ql[st].z : R.ql[st].w;
         const h4 bq = q6_codes(qlw, (sb & 1) ? R.qh[st].y : R.qh[st].x, sb >> 2, 2 * (sb >> 1));
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
-          f4 P = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], bq, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          // the chain starts from -1056 XS: P = sum (q - 32) x
+          f4 P = __builtin_amdgcn_mfma_f32_16x16x16f16(xh[bt], bq, NXS[bt], 0, 0, 0);
           if constexpr (!XF16) P = __builtin_amdgcn_mfma_f32_16x16x16f16(xlo[bt], bq, P, 0, 0, 0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(ca, P[r], fmaf(-cb, XS[bt][r], Y[st][bt][r]));
+          for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(ca, P[r], Y[st][bt][r]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
