@@ -337,6 +337,65 @@ def kernel_sweeps():
     return out
 
 
+A8_SHAPES = [("gdn_in", 12352, 5120, 0), ("gdn_out", 5120, 4096, 1), ("attn_qkv", 14336, 5120, 0),
+             ("attn_o", 5120, 6144, 1), ("down", 5120, 17408, 1), ("gateup", 17408, 5120, 2),
+             ("lm_head", 151936, 5120, 0)]
+
+
+def a8_sweep(rows_list, only=None):
+    """Every config-4 A8 GEMV shape (epilogue as in the decode step: store,
+    residual or fused SwiGLU) at the given row counts, prepared activations,
+    HIP-event timed over launches cycling through weight copies that exceed
+    the last-level cache (so every launch streams from HBM)."""
+    from pagoda_amd import Device, Event, Matrix
+    from pagoda_amd.matrix import act_bytes, act_prep_dev
+
+    dev = Device(os.environ.get("PAGODA_DEVICE", "hip"))
+    rng = np.random.default_rng(1)
+    out = []
+    for name, N, K, epi in A8_SHAPES:
+        if only and name not in only:
+            continue
+        per = N * K * 8.5 / 8 * (2 if epi == 2 else 1)
+        ncopy = max(2, int(1.6e9 // per) + 1)
+        ms = [Matrix.synth(dev, 0, N, K, 7 + i, i * 16 + 1) for i in range(ncopy)]
+        us = [Matrix.synth(dev, 0, N, K, 7 + i, i * 16 + 2) for i in range(ncopy)] if epi == 2 else None
+        for rows in rows_list:
+            x = dev.upload(rng.normal(0, 1, (rows, K)).astype(np.float32))
+            act = dev.alloc(act_bytes(rows, K))
+            y = dev.alloc(rows * N * 4)
+            res = dev.alloc(rows * N * 4)
+            act_prep_dev(dev, x, K, rows, K, act)
+
+            def run(i):
+                if epi == 2:
+                    Matrix.gemv_swiglu_act_dev(ms[i], us[i], act, rows, y, N)
+                elif epi == 1:
+                    ms[i].gemv_act_dev(act, rows, y, N, res, N)
+                else:
+                    ms[i].gemv_act_dev(act, rows, y, N)
+
+            for i in range(ncopy):
+                run(i)
+            L = max(24, 2 * ncopy)
+            e0 = Event(dev).record()
+            for i in range(L):
+                run(i % ncopy)
+            e1 = Event(dev).record()
+            t_us = e0.elapsed_ms(e1) / L * 1e3
+            algo = per + rows * K * 4 + rows * N * 4
+            gbs = algo / (t_us * 1e-6) / 1e9
+            log(f"{name:9s} N={N:6d} K={K:5d} rows={rows:2d}: {t_us:8.1f} us {gbs:7.0f} GB/s {100 * gbs / HBM_PEAK_GBS:5.1f}%")
+            out.append({"matrix": name, "N": N, "K": K, "rows": rows, "us": round(t_us, 2), "algo_bytes": algo,
+                        "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            for p in (x, act, y, res):
+                dev.free(p)
+        for m in ms + (us or []):
+            m.free()
+    dev.close()
+    return out
+
+
 def config5_only():
     from pagoda_amd import Device
     from pagoda_amd.engine import QWEN35_27B, Model
@@ -448,6 +507,9 @@ def main():
                     help="run only the config-5 passes (for kernel traces of that workload)")
     ap.add_argument("--attn-scan", action="store_true",
                     help="time the paged attention alone over context lengths (for kernel traces)")
+    ap.add_argument("--a8-sweep", default=None, metavar="ROWS",
+                    help="time every config-4 A8 GEMV shape at these row counts (e.g. 1,16,32,64)")
+    ap.add_argument("--a8-only", default=None, metavar="NAMES", help="restrict --a8-sweep to these matrices")
     ap.add_argument("--kernel-sweeps", action="store_true",
                     help="config 2 (Q4_K/Q6_K GEMV sweep) and config 3 (GDN step) kernel timings")
     args = ap.parse_args()
@@ -463,6 +525,11 @@ def main():
         return
     if args.attn_scan:
         attn_scan()
+        return
+    if args.a8_sweep:
+        rows = [int(r) for r in args.a8_sweep.split(",")]
+        only = args.a8_only.split(",") if args.a8_only else None
+        print(json.dumps({"a8_sweep": a8_sweep(rows, only)}), flush=True)
         return
     if args.kernel_sweeps:
         print(json.dumps(kernel_sweeps()), flush=True)
