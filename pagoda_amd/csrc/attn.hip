@@ -45,7 +45,7 @@ namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kItemFields = 5;  // page_off, npages, row_off, nrows, chunk index
+constexpr int kItemFields = 6;  // page_off, npages, row_off, first query, queries, chunk index
 
 // ---------------------------------------------------------------------------
 // item kernel
@@ -84,8 +84,8 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 15, kq = lane >> 4;
   const int* it = plan.items + (size_t)item * kItemFields;
-  const int page_off = it[0], npages = it[1], row_off = it[2], nrows = it[3], chunk = it[4];
-  const int nq = nrows * G;
+  // queries q0 .. q0 + nq - 1 of the rows from slot row_off on (query = row * G + head)
+  const int page_off = it[0], npages = it[1], row_off = it[2], q0 = it[3], nq = it[4], chunk = it[5];
   const int chunk_pos0 = chunk * kChunkPages * L.block;
   const float inv_scale = 1.0f / sqrtf((float)HD);
   // this wave's pages: w, w + 4, ... (none when the chunk has fewer pages)
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
     // this lane's query vector n = j: Q[n][T kq + t] (zero past the item's queries)
     const int qi = t0 + j;
     const bool qlive = qi < nq;
-    const int krow = qlive ? qi / G : 0, g = qlive ? qi % G : 0;
+    const int krow = qlive ? (q0 + qi) / G : 0, g = qlive ? (q0 + qi) % G : 0;
     const int row = plan.item_rows[row_off + krow];
     const int len = m.pos_of_row[row] + 1;  // positions [0, len) are visible
     float Q[T];
@@ -231,7 +231,8 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
 #pragma unroll
         for (int e = 0; e < 16; ++e) v[e] += sh.o[w][n][d0 + e] * wt;
       }
-      const int orow = plan.item_rows[row_off + (live ? qo / G : 0)], head = kvh * G + (live ? qo % G : 0);
+      const int qa = q0 + (live ? qo : 0);
+      const int orow = plan.item_rows[row_off + qa / G], head = kvh * G + qa % G;
       if constexpr (DIRECT) {
         const size_t oo = ((size_t)orow * L.heads + head) * HD + d0;
 #pragma unroll
@@ -251,7 +252,7 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
           a8act::emit_slice(act, orow, col >> 6, (col >> 4) & 3, v, live);
         }
       } else if (live) {
-        const int slot = row_off + qo / G, go = qo % G;
+        const int slot = row_off + qa / G, go = qa % G;
         float* po = part_o + (((size_t)slot * L.kv_heads + kvh) * G + go) * HD + d0;
 #pragma unroll
         for (int e = 0; e < 16; e += 4) *reinterpret_cast<float4*>(po + e) = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
@@ -355,9 +356,6 @@ void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L,
 void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, const int* block_tables,
                      int max_blocks, int block, int group, std::vector<int>& out) {
   PGD_CHECK(group > 0 && group <= 64 && block == 16, kErrShape, "attention plan: group <= 64 heads, pages of 16");
-  // rows per item: one 16-query tile (a tile's result does not depend on the
-  // item's size, so this only trades shared K/V reads for parallelism)
-  const int max_rows = std::max(1, 16 / group);
   struct Key {
     int chunk;
     std::vector<int> pages;
@@ -395,21 +393,24 @@ void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, con
       row_chunk_group[r].push_back(gid);
     }
   }
-  // items: each group's rows in runs of max_rows
+  // items: each group's queries (row-major over its rows, G heads per row) in
+  // runs of 16, one matrix-core tile; a query's result does not depend on the
+  // other queries of its tile, so tiles may cut between a row's heads
   std::vector<int> items, pages, item_rows;
   std::vector<std::vector<int>> group_slot0(keys.size());  // slot of each member
   for (size_t gi = 0; gi < keys.size(); ++gi) {
     const int page_off = (int)pages.size();
     pages.insert(pages.end(), keys[gi].pages.begin(), keys[gi].pages.end());
     const auto& mem = members[gi];
-    for (size_t k0 = 0; k0 < mem.size(); k0 += max_rows) {
-      const int nr = (int)std::min<size_t>(max_rows, mem.size() - k0);
-      items.insert(items.end(), {page_off, (int)keys[gi].pages.size(), (int)item_rows.size(), nr, keys[gi].chunk});
-      for (int k = 0; k < nr; ++k) {
-        group_slot0[gi].push_back((int)item_rows.size());
-        item_rows.push_back(mem[k0 + k]);
-      }
+    const int base = (int)item_rows.size();
+    for (size_t k = 0; k < mem.size(); ++k) {
+      group_slot0[gi].push_back(base + (int)k);
+      item_rows.push_back(mem[k]);
     }
+    const int nqs = (int)mem.size() * group;
+    for (int qs = 0; qs < nqs; qs += 16)
+      items.insert(items.end(), {page_off, (int)keys[gi].pages.size(), base + qs / group, qs % group,
+                                 std::min(16, nqs - qs), keys[gi].chunk});
   }
   // row -> slots in chunk order
   std::vector<int> row_slot_off(rows + 1), row_slots;

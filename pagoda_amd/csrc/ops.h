@@ -106,7 +106,7 @@ void qkv_prep(const QkvPrep& p, const AttnLayout& L, const RowMeta& m, int rows,
 constexpr int kChunkPages = 16;
 struct AttnPlan {
   int n_items, n_slots, max_row_slots;
-  const int* items;         // [n_items][5]: page_off, npages, row_off, nrows, chunk
+  const int* items;         // [n_items][6]: page_off, npages, row_off, first query, queries, chunk
   const int* pages;         // page ids of the items' chunks
   const int* item_rows;     // rows of the items; index = partial slot
   const int* row_slot_off;  // [rows + 1]
