@@ -47,7 +47,28 @@ struct GemvArgs {
   // no); row0 = first row of this launch within that activation
   a8act::Dst oact;
   int row0;
+  // deferred RMSNorm of the input (null: none): rss rows of this launch,
+  // rss_nh partials per row, row width rss_n, eps; outputs are scaled by
+  // rss_inv() of their row. inv: optional per-launch-row copy of those
+  // factors written by the stream-K kernel for its fix-up kernel.
+  const float* rss;
+  int rss_nh, rss_n;
+  float rss_eps;
+  float* inv;
 };
+
+// 1/rms of one deferred-norm row from its partial sums of squares: lane l adds
+// partials l, l + 64, ... in turn, then a xor butterfly (each step adds the
+// same two values on both lanes, so every lane ends with the same sum). The
+// whole wave calls it; the same function in every consumer.
+__device__ inline float rss_inv(const float* rss_row, int nh, int n, float eps) {
+  const int lane = threadIdx.x & 63;
+  float s = 0.0f;
+  for (int i = lane; i < nh; i += 64) s += rss_row[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  return 1.0f / sqrtf(s / (float)n + eps);
+}
 
 enum { EPI_STORE = 0, EPI_RES = 1, EPI_SWIGLU = 2 };
 

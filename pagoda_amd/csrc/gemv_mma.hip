@@ -91,6 +91,51 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
   a8act::emit_slice(d, row, g, q, v, live);
 }
 
+// RMSNorm with a deferred scale (rms_zero, pagoda-hf/src/qwen3_5.rs:1736-1745,
+// reordered): operands of x * w, and per (row, group) the sum of x^2 over the
+// group's 64 values (each lane's 16 in order, then quarters (0 + 1) + (2 + 3)).
+// Layout and lanes as a8_xprep_kernel; rss: [rows][G].
+__global__ __launch_bounds__(256) void a8_gnorm_prep_kernel(const float* __restrict__ x, int ldx,
+                                                            const float* __restrict__ w, a8act::Dst d,
+                                                            float* __restrict__ rss) {
+  const size_t item = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int bt = (int)(item & 1);
+  const size_t cg = item >> 1;
+  const int g = (int)(cg % d.G), c = (int)(cg / d.G);
+  if (32 * c >= d.rows) return;
+  if (a8act::chunk_compact(d.rows, c) && bt) return;
+  const int jr = lane >> 2, q = lane & 3;
+  const int row = 32 * c + 16 * bt + jr;
+  float v[16], ss = 0.0f;
+  if (row < d.rows) {
+    const float4* xp = reinterpret_cast<const float4*>(x + (size_t)row * ldx + (g << 6) + 16 * q);
+    const float4* wp = reinterpret_cast<const float4*>(w + (g << 6) + 16 * q);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 f = xp[i], h = wp[i];
+      v[4 * i] = f.x;
+      v[4 * i + 1] = f.y;
+      v[4 * i + 2] = f.z;
+      v[4 * i + 3] = f.w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss += v[4 * i + e] * v[4 * i + e];
+      v[4 * i] *= h.x;
+      v[4 * i + 1] *= h.y;
+      v[4 * i + 2] *= h.z;
+      v[4 * i + 3] *= h.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+  }
+  ss += __shfl_xor(ss, 1, 64);
+  ss += __shfl_xor(ss, 2, 64);
+  const bool live = a8act::chunk_compact(d.rows, c) ? (jr < 4) : true;
+  if (live && q == 0 && row < d.rows) rss[(size_t)row * d.G + g] = ss;
+  a8act::emit_slice(d, row, g, q, v, live);
+}
+
 // Fused RMSNorm (rms_zero, pagoda-hf/src/qwen3_5.rs:1736-1745) + activation
 // prep: one workgroup of NT threads per output row; thread t owns 16-wide
 // slices t, t+NT, ... (slice u = 4g + q), kept in registers between the two passes together
@@ -399,6 +444,15 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
       }
   }
 
+  // deferred RMSNorm of the input: the waves share out the rows' 1/rms
+  __shared__ float s_inv[32];
+  if (a.rss) {
+    for (int b = wave; b < nb; b += KP) {
+      const float v = rss_inv(a.rss + (size_t)b * a.rss_nh, a.rss_nh, a.rss_n, a.rss_eps);
+      if (lane == 0) s_inv[b] = v;
+    }
+  }
+
   // ---- split-K reduction (fixed order: range 0 + 1 + ... + KS-1) ----
   // range wave * R + r holds Ys[r] for r < rc, Y for r == rc, zero after
   wait_vmcnt<0>();
@@ -435,6 +489,18 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
     for (int st = 0; st < NS; ++st)
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[v][st][bt][lane];
+
+  if (a.rss) {
+#pragma unroll
+    for (int st = 0; st < NS; ++st)
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int b = 16 * bt + 4 * q + r;
+          Y[st][bt][r] *= b < nb ? s_inv[b] : 1.0f;
+        }
+  }
 
   // ---- epilogue: lane holds weight row n for batch rows 16bt + 4q + r ----
   if constexpr (DUAL) {
@@ -660,9 +726,11 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
 template <int KS, int EPI>
 __global__ __launch_bounds__(256) void a8_reduce_kernel(GemvArgs a, int nb, const float* __restrict__ part) {
   const int n4 = a.n_out >> 2;
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= nb * n4) return;
-  const int b = i / n4, n = (i - b * n4) * 4;
+  const int b = blockIdx.y, i4 = blockIdx.x * 256 + threadIdx.x;
+  // deferred RMSNorm of the input (whole waves, before any lane leaves)
+  const float inv = a.rss ? rss_inv(a.rss + (size_t)b * a.rss_nh, a.rss_nh, a.rss_n, a.rss_eps) : 1.0f;
+  if (i4 >= n4) return;
+  const int n = i4 * 4;
   const size_t plane = (size_t)nb * a.n_out, e = (size_t)b * a.n_out + n;
   float4 v[KS];
 #pragma unroll
@@ -674,6 +742,12 @@ __global__ __launch_bounds__(256) void a8_reduce_kernel(GemvArgs a, int nb, cons
     y.y += v[r].y;
     y.z += v[r].z;
     y.w += v[r].w;
+  }
+  if (a.rss) {
+    y.x *= inv;
+    y.y *= inv;
+    y.z *= inv;
+    y.w *= inv;
   }
   const size_t o = (size_t)b * a.ldy + n;
   if constexpr (EPI == EPI_RES) {
@@ -711,8 +785,8 @@ void launch_shared(const GemvArgs& a, const uint4* XA, const float* CA, int nb, 
   float* part = static_cast<float*>(gemv_scratch(s, (size_t)KS * nb * a.n_out * sizeof(float), 1));
   hipLaunchKernelGGL((a8_mma_shared_kernel<KS, T, P, EPI, NC>), dim3((tiles + T - 1) / T, KS), dim3(64 * T), 0, s, a,
                      XA, CA, nb, part);
-  const int n4 = nb * (a.n_out / 4);
-  hipLaunchKernelGGL((a8_reduce_kernel<KS, EPI>), dim3((n4 + 255) / 256), dim3(256), 0, s, a, nb, part);
+  const int n4 = a.n_out / 4;
+  hipLaunchKernelGGL((a8_reduce_kernel<KS, EPI>), dim3((n4 + 255) / 256, nb), dim3(256), 0, s, a, nb, part);
 }
 
 // one launch per chunk of up to 32 rows; the mode stages only the rows present
@@ -765,6 +839,12 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   const int G = a.n_in / 64;
   const uint4* XA = reinterpret_cast<const uint4*>(act.XA);
   int rows = act.rows;
+  if (act.rss) {
+    a.rss = act.rss;
+    a.rss_nh = act.K / 64;
+    a.rss_n = act.K;
+    a.rss_eps = act.eps;
+  }
   const bool sk = a8_sk_wanted(a, EPI);
   // plain matrices stream their weights once per 64 rows when the second
   // chunk of a pair holds more than 4 rows (full operand layout)
@@ -787,6 +867,7 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
     rows -= nb;
     if (a.y) a.y += (size_t)nb * a.ldy;
     if (a.res) a.res += (size_t)nb * a.ldres;
+    if (a.rss) a.rss += (size_t)nb * a.rss_nh;
     a.row0 += nb;
   }
 }
@@ -801,9 +882,12 @@ void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s) {
 
 }  // namespace gemv
 
-size_t a8_act_bytes(int rows, int K) {
-  return a8act::xa_bytes(rows, K / 64) + a8act::ca_bytes(rows, K / 64);
+// operands | constants | deferred-norm row sums ([rows][K / 64], 256 B aligned)
+static size_t rss_offset(int rows, int K) {
+  return (a8act::xa_bytes(rows, K / 64) + a8act::ca_bytes(rows, K / 64) + 255) & ~(size_t)255;
 }
+
+size_t a8_act_bytes(int rows, int K) { return rss_offset(rows, K) + (size_t)rows * (K / 64) * sizeof(float); }
 
 A8Act a8_act_view(void* buf, int rows, int K) {
   A8Act a;
@@ -824,6 +908,20 @@ A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream
   if (rows <= 0) return a;
   const size_t items = ((size_t)rows + 31) / 32 * (K / 64) * 2;
   hipLaunchKernelGGL(gemv::a8_xprep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, x, ldx, a8_act_dst(a));
+  PGD_HIP(hipGetLastError());
+  return a;
+}
+
+A8Act a8_gnorm_prep(const float* x, int ldx, int rows, int n, const float* w, float eps, void* buf, hipStream_t s) {
+  PGD_CHECK(n % 64 == 0 && ldx % 4 == 0, kErrShape, "A8 activation width must be a multiple of 64");
+  A8Act a = a8_act_view(buf, rows, n);
+  float* rss = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(buf) + rss_offset(rows, n));
+  a.rss = rss;
+  a.eps = eps;
+  if (rows <= 0) return a;
+  const size_t items = ((size_t)rows + 31) / 32 * (n / 64) * 2;
+  hipLaunchKernelGGL(gemv::a8_gnorm_prep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, x, ldx, w,
+                     a8_act_dst(a), rss);
   PGD_HIP(hipGetLastError());
   return a;
 }

@@ -161,6 +161,21 @@ __device__ __attribute__((always_inline)) inline void wave_epilogue(
   }
 }
 
+// Deferred RMSNorm of the input: accumulators of batch row b times inv_rows[b].
+template <int NS, int NBT>
+__device__ __attribute__((always_inline)) inline void scale_rows(f4 (&Y)[NS][NBT], const float* inv_rows, int nb) {
+  const int q = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int b = 16 * bt + 4 * q + rr;
+      const float f = b < nb ? inv_rows[b] : 1.0f;
+#pragma unroll
+      for (int st = 0; st < NS; ++st) Y[st][bt][rr] *= f;
+    }
+}
+
 // D: units of weights in flight per wave.
 template <int MODE, int EPI, int D>
 __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const uint4* __restrict__ XA,
@@ -179,6 +194,19 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
   const long long u0 = run_start(U, k.nwg, blockIdx.x), u1 = run_start(U, k.nwg, blockIdx.x + 1);
   if (u0 >= u1) return;
   float* hb = reinterpret_cast<float*>(smem + 2 * Gm::SLOT) + wave * 32 * 33;
+  // deferred RMSNorm of the input: the rows' 1/rms, shared out over the waves;
+  // workgroup 0 also leaves them for the fix-up kernel
+  __shared__ float s_inv[32];
+  if (a.rss) {
+    for (int b = wave; b < nb; b += kWaves) {
+      const float v = rss_inv(a.rss + (size_t)b * a.rss_nh, a.rss_nh, a.rss_n, a.rss_eps);
+      if (lane == 0) {
+        s_inv[b] = v;
+        if (blockIdx.x == 0) a.inv[b] = v;
+      }
+    }
+    __syncthreads();
+  }
 
   // ---- per-unit register payload: weights, scale/bias, one operand slice ----
   struct WR {
@@ -287,7 +315,10 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
     if (++cg == G) {
       cg = 0;
       if (cb == first_blk && cut_head) store_part(0);
-      else wave_epilogue<MODE, EPI>(a, nb, cb, wave, Y, hb);
+      else {
+        if (a.rss) scale_rows(Y, s_inv, nb);
+        wave_epilogue<MODE, EPI>(a, nb, cb, wave, Y, hb);
+      }
       zero_y();
       ++cb;
     }
@@ -360,6 +391,7 @@ __global__ __launch_bounds__(64) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArg
         for (int bt = 0; bt < NBT; ++bt) V[st][bt] = r + t == r0 ? P[t][st][bt] : V[st][bt] + P[t][st][bt];
     }
   }
+  if (a.rss) scale_rows(V, a.inv, nb);
   wave_epilogue<MODE, EPI>(a, nb, blk, wave, V, reinterpret_cast<float*>(smem));
 }
 
@@ -409,8 +441,10 @@ bool a8_sk_wanted(const GemvArgs& a, int epi) {
   return epi == EPI_SWIGLU || (a.n_out + 31) / 32 >= 2048;
 }
 
-void run_a8_sk_chunk(const GemvArgs& a, const uint4* XA, const float* CA, int nb, int epi, hipStream_t s) {
+void run_a8_sk_chunk(const GemvArgs& a_in, const uint4* XA, const float* CA, int nb, int epi, hipStream_t s) {
   PGD_CHECK(nb >= 5 && nb <= 32, kErrArg, "stream-K A8 GEMV takes 5..32 rows per launch");
+  GemvArgs a = a_in;
+  if (a.rss) a.inv = static_cast<float*>(gemv_scratch(s, 32 * sizeof(float), 5));
   if (epi == EPI_SWIGLU) launch_chunk_sk<EPI_SWIGLU>(a, XA, CA, nb, s);
   else if (epi == EPI_RES) launch_chunk_sk<EPI_RES>(a, XA, CA, nb, s);
   else launch_chunk_sk<EPI_STORE>(a, XA, CA, nb, s);

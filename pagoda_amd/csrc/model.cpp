@@ -459,7 +459,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     int ld_q = 0, ld_kv = 0;
     if (hybrid) {
       // one fused norm + operand prep, one launch for all projections
-      A8Act act = a8_norm_prep(w.x, H, nullptr, rows, H, L.in_norm, eps, nullptr, 0, w.act, st);
+      A8Act act = a8_gnorm_prep(w.x, H, rows, H, L.in_norm, eps, w.act, st);
       qmat_gemv_a8(L.proj, act, w.A, (int)w.lda, nullptr, 0, st);
       if (L.full) {
         q_raw = w.A;
@@ -537,7 +537,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     }
     // ---- SwiGLU MLP ----
     if (hybrid) {
-      A8Act act = a8_norm_prep(w.x, H, nullptr, rows, H, L.post_norm, eps, nullptr, 0, w.act, st);
+      A8Act act = a8_gnorm_prep(w.x, H, rows, H, L.post_norm, eps, w.act, st);
       // the SwiGLU epilogue writes the down projection's operands itself
       const A8Act mid = a8_act_view(w.act2, rows, c.intermediate);
       qmat_gemv_a8_swiglu(L.gate, L.up, act, nullptr, 0, st, &mid);

@@ -125,6 +125,12 @@ struct A8Act {
   const void* XA = nullptr;
   const float* CA = nullptr;
   int rows = 0, K = 0;
+  // deferred RMSNorm (a8_gnorm_prep): the operands hold x * w without the
+  // 1/rms factor, rss holds per row the K/64 partial sums of x^2 (one per
+  // 64-wide group), and the consuming GEMV scales row b's outputs by
+  // 1/sqrt(sum / K + eps). Null: the operands are the finished input.
+  const float* rss = nullptr;
+  float eps = 0.0f;
 };
 size_t a8_act_bytes(int rows, int K);
 A8Act a8_act_view(void* buf, int rows, int K);
@@ -132,6 +138,10 @@ A8Act a8_act_view(void* buf, int rows, int K);
 a8act::Dst a8_act_dst(const A8Act& a);
 // from f32 rows x [rows, ldx]
 A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream_t s);
+// RMSNorm with the scale deferred to the consumer: operands of x * w and the
+// row's partial sums of squares (A8Act.rss); one wave per (32-row chunk,
+// group, 16-row tile), no per-row reduction. Feeds A8 GEMVs only.
+A8Act a8_gnorm_prep(const float* x, int ldx, int rows, int n, const float* w, float eps, void* buf, hipStream_t s);
 // fused RMSNorm (x * rsqrt(mean x^2 + eps) * w) + prep; y (nullable) also
 // receives the normalized rows; rows_idx (nullable) selects source rows
 A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps, float* y,
