@@ -37,13 +37,12 @@ __host__ __device__ inline size_t ca_bytes(int rows, int G) { return ((size_t)ro
 
 __device__ inline bool chunk_compact(int rows, int c) { return rows - 32 * c <= 4; }
 
-// the four operands of one 16-wide k slice and its partial sums
-__device__ inline void prep16(const float* v, uint4 (&o)[4], float& xs, float& xsp) {
-  uint32_t hw[8], lw[8];
-  xs = 0.0f;
-  xsp = 0.0f;
+// half a 16-wide k slice (8 values): its two operand words (xh, xl of the 8
+// k) and the running sums, continued from xs / xsp (in slice order)
+__device__ inline void prep8(const float* v, uint4& oh, uint4& ol, float& xs, float& xsp) {
+  uint32_t hw[4], lw[4];
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
+  for (int p = 0; p < 4; ++p) {
     const _Float16 h0 = (_Float16)v[2 * p], h1 = (_Float16)v[2 * p + 1];
     const _Float16 l0 = (_Float16)(v[2 * p] - (float)h0), l1 = (_Float16)(v[2 * p + 1] - (float)h1);
     hw[p] = __builtin_bit_cast(uint32_t, (h2){h0, h1});
@@ -51,10 +50,16 @@ __device__ inline void prep16(const float* v, uint4 (&o)[4], float& xs, float& x
     xs += v[2 * p] + v[2 * p + 1];
     xsp += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
   }
-  o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-  o[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-  o[2] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  o[3] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+  oh = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  ol = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+}
+
+// the four operands of one 16-wide k slice and its partial sums
+__device__ inline void prep16(const float* v, uint4 (&o)[4], float& xs, float& xsp) {
+  xs = 0.0f;
+  xsp = 0.0f;
+  prep8(v, o[0], o[2], xs, xsp);
+  prep8(v + 8, o[1], o[3], xs, xsp);
 }
 
 // operands of slice (row, g, q)
@@ -69,6 +74,18 @@ __device__ inline void put_operands(const Dst& d, int row, int g, int q, const u
     uint4* p = d.XA + item * 256 + q * 16 + (row & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) p[i * 64] = o[i];
+  }
+}
+
+// operand i (0..3) alone of slice (row, g, q): for producers whose lanes hold
+// half a slice (i = 0, 2: k 0..7; i = 1, 3: k 8..15)
+__device__ inline void put_operand(const Dst& d, int row, int g, int q, int i, const uint4& o) {
+  const int c = row >> 5;
+  if (chunk_compact(d.rows, c)) {
+    d.XA[(size_t)c * d.G * 512 + ((size_t)g * 4 + (row & 31)) * 16 + q + i * 4] = o;
+  } else {
+    const size_t item = ((size_t)c * d.G + g) * 2 + ((row >> 4) & 1);
+    d.XA[item * 256 + q * 16 + (row & 15) + i * 64] = o;
   }
 }
 

@@ -55,6 +55,12 @@ struct GemvArgs {
   int rss_nh, rss_n;
   float rss_eps;
   float* inv;
+  // residual launches only: also emit the next RMSNorm's deferred input from
+  // the new rows h = res + W x (operands of h * nw into nact, per-32-column
+  // sums of h^2 into nrss [rows][n_out / 32]); nact.XA null: no
+  a8act::Dst nact;
+  const float* nw;
+  float* nrss;
 };
 
 // 1/rms of one deferred-norm row from its partial sums of squares: lane l adds

@@ -92,9 +92,9 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
 }
 
 // RMSNorm with a deferred scale (rms_zero, pagoda-hf/src/qwen3_5.rs:1736-1745,
-// reordered): operands of x * w, and per (row, group) the sum of x^2 over the
-// group's 64 values (each lane's 16 in order, then quarters (0 + 1) + (2 + 3)).
-// Layout and lanes as a8_xprep_kernel; rss: [rows][G].
+// reordered): operands of x * w, and per (row, 32-wide half group) the sum of
+// x^2 (each lane's 16 in order, then quarters 0 + 1 or 2 + 3). Layout and
+// lanes as a8_xprep_kernel; rss: [rows][K / 32].
 __global__ __launch_bounds__(256) void a8_gnorm_prep_kernel(const float* __restrict__ x, int ldx,
                                                             const float* __restrict__ w, a8act::Dst d,
                                                             float* __restrict__ rss) {
@@ -129,10 +129,9 @@ __global__ __launch_bounds__(256) void a8_gnorm_prep_kernel(const float* __restr
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = 0.0f;
   }
-  ss += __shfl_xor(ss, 1, 64);
-  ss += __shfl_xor(ss, 2, 64);
+  ss += __shfl_xor(ss, 1, 64);  // half group: quarters (0 + 1), (2 + 3)
   const bool live = a8act::chunk_compact(d.rows, c) ? (jr < 4) : true;
-  if (live && q == 0 && row < d.rows) rss[(size_t)row * d.G + g] = ss;
+  if (live && (q & 1) == 0 && row < d.rows) rss[(size_t)row * 2 * d.G + 2 * g + (q >> 1)] = ss;
   a8act::emit_slice(d, row, g, q, v, live);
 }
 
@@ -535,6 +534,10 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
       if (!a.y) return;
     }
   }
+  // residual + next RMSNorm's input: the new rows also go to LDS (with one
+  // tile per workgroup: 32 outputs = half a group of the next activation)
+  const bool emit = EPI == EPI_RES && MT == 1 && a.nact.XA;
+  float* hn = reinterpret_cast<float*>(smem);  // [32][33]
 #pragma unroll
   for (int st = 0; st < NSM; ++st) {
     const int n = (blockIdx.x * MT + (st >> 1)) * 32 + 16 * (st & 1) + j;
@@ -547,9 +550,41 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
         if (b >= nb) continue;
         const size_t o = (size_t)b * a.ldy + n;
         if constexpr (EPI == EPI_STORE) a.y[o] = Y[st][bt][r];
-        if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];
+        if constexpr (EPI == EPI_RES) {
+          const float h = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];
+          a.y[o] = h;
+          if (emit) hn[b * 33 + 16 * st + j] = h;
+        }
         if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(Y[st][bt][r]) * Y[NSM + st][bt][r];
       }
+  }
+  if constexpr (EPI == EPI_RES && MT == 1) {
+    if (emit) {
+      // as a8_gnorm_prep_kernel: lane L takes row L % 32, quarter pair L / 32
+      // of the tile; sum of h^2 in k order, then operands of h * nw
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int tile = blockIdx.x, b = lane & 31, hh = lane >> 5;
+      const bool live = b < nb;
+      const float4* wp = reinterpret_cast<const float4*>(a.nw + tile * 32 + 16 * hh);
+      float v[16], ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 w4 = wp[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * i + e] = live ? hn[b * 33 + 16 * hh + 4 * i + e] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += v[4 * i + e] * v[4 * i + e];
+        v[4 * i] *= w4.x;
+        v[4 * i + 1] *= w4.y;
+        v[4 * i + 2] *= w4.z;
+        v[4 * i + 3] *= w4.w;
+      }
+      ss += __shfl_xor(ss, 32, 64);
+      if (live && hh == 0) a.nrss[(size_t)(a.row0 + b) * (a.n_out >> 5) + tile] = ss;
+      a8act::emit_slice<32>(a.nact, a.row0 + b, tile >> 1, (tile & 1) * 2 + hh, v, live);
+    }
   }
 }
 
@@ -763,6 +798,81 @@ __global__ __launch_bounds__(256) void a8_reduce_kernel(GemvArgs a, int nb, cons
   a.y[o + 3] = y.w;
 }
 
+// The residual reduction of a8_reduce_kernel that also emits the next
+// RMSNorm's deferred input (as a8_gnorm_prep_kernel, bit for bit): a thread
+// holds 8 consecutive outputs of row b, lanes 2s and 2s + 1 the two halves of
+// 16-wide slice s. Slice sums run in k order: the first half's lane starts
+// them, the second continues from its partner's totals.
+template <int KS>
+__global__ __launch_bounds__(256) void a8_reduce_emit_kernel(GemvArgs a, int nb, const float* __restrict__ part) {
+  const int n8 = a.n_out >> 3;
+  const int b = blockIdx.y, i8 = blockIdx.x * 256 + threadIdx.x;
+  const bool live = i8 < n8;  // every lane stays for the shuffles
+  const int n = (live ? i8 : 0) * 8;
+  const size_t plane = (size_t)nb * a.n_out, e = (size_t)b * a.n_out + n;
+  float4 v0[KS], v1[KS];
+#pragma unroll
+  for (int r = 0; r < KS; ++r) {
+    v0[r] = *reinterpret_cast<const float4*>(part + r * plane + e);
+    v1[r] = *reinterpret_cast<const float4*>(part + r * plane + e + 4);
+  }
+  const float* rs = a.res + (size_t)b * a.ldres + n;
+  const float4 r0 = *reinterpret_cast<const float4*>(rs), r1 = *reinterpret_cast<const float4*>(rs + 4);
+  float4 y0 = v0[0], y1 = v1[0];
+#pragma unroll
+  for (int r = 1; r < KS; ++r) {
+    y0.x += v0[r].x;
+    y0.y += v0[r].y;
+    y0.z += v0[r].z;
+    y0.w += v0[r].w;
+    y1.x += v1[r].x;
+    y1.y += v1[r].y;
+    y1.z += v1[r].z;
+    y1.w += v1[r].w;
+  }
+  float h[8] = {r0.x + y0.x, r0.y + y0.y, r0.z + y0.z, r0.w + y0.w, r1.x + y1.x, r1.y + y1.y, r1.z + y1.z, r1.w + y1.w};
+  if (live) {
+    float* yo = a.y + (size_t)b * a.ldy + n;
+    *reinterpret_cast<float4*>(yo) = make_float4(h[0], h[1], h[2], h[3]);
+    *reinterpret_cast<float4*>(yo + 4) = make_float4(h[4], h[5], h[6], h[7]);
+  }
+  // ---- next RMSNorm's input ----
+  const int half = i8 & 1, slice = i8 >> 1, g = slice >> 2, q = slice & 3;
+  const float4 w0 = *reinterpret_cast<const float4*>(a.nw + n), w1 = *reinterpret_cast<const float4*>(a.nw + n + 4);
+  const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  // first half's running sums, handed to the second half
+  float ss = 0.0f, xs = 0.0f, xsp = 0.0f;
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = h[k] * w[k];
+  if (half == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ss += h[k] * h[k];
+  }
+  uint4 oh, ol;
+  if (half == 0) a8act::prep8(v, oh, ol, xs, xsp);
+  const float ss0 = __shfl_xor(ss, 1, 64), xs0 = __shfl_xor(xs, 1, 64), xsp0 = __shfl_xor(xsp, 1, 64);
+  if (half == 1) {
+    ss = ss0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ss += h[k] * h[k];
+    xs = xs0;
+    xsp = xsp0;
+    a8act::prep8(v, oh, ol, xs, xsp);
+  }
+  // half group: slices q and q ^ 1 (their second-half lanes are 2 apart)
+  const float ssh = ss + __shfl_xor(ss, 2, 64);
+  const float xsh = xs + __shfl_xor(xs, 2, 64), xsph = xsp + __shfl_xor(xsp, 2, 64);
+  if (!live) return;
+  const int row = a.row0 + b;
+  a8act::put_operand(a.nact, row, g, q, half, oh);
+  a8act::put_operand(a.nact, row, g, q, 2 + half, ol);
+  if (half == 1 && (q & 1) == 0) {
+    a.nrss[(size_t)row * (a.n_out >> 5) + 2 * g + (q >> 1)] = ssh;
+    a8act::put_half(a.nact, row, g, q >> 1, xsh, xsph);
+  }
+}
+
 template <int MODE, int KS, int KP, int P, int MT, int EPI>
 void launch_kernel(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipStream_t s) {
   const int tiles = (a.n_out + 31) / 32;
@@ -785,6 +895,11 @@ void launch_shared(const GemvArgs& a, const uint4* XA, const float* CA, int nb, 
   float* part = static_cast<float*>(gemv_scratch(s, (size_t)KS * nb * a.n_out * sizeof(float), 1));
   hipLaunchKernelGGL((a8_mma_shared_kernel<KS, T, P, EPI, NC>), dim3((tiles + T - 1) / T, KS), dim3(64 * T), 0, s, a,
                      XA, CA, nb, part);
+  if (EPI == EPI_RES && a.nact.XA) {
+    const int n8 = a.n_out / 8;
+    hipLaunchKernelGGL((a8_reduce_emit_kernel<KS>), dim3((n8 + 255) / 256, nb), dim3(256), 0, s, a, nb, part);
+    return;
+  }
   const int n4 = a.n_out / 4;
   hipLaunchKernelGGL((a8_reduce_kernel<KS, EPI>), dim3((n4 + 255) / 256, nb), dim3(256), 0, s, a, nb, part);
 }
@@ -841,11 +956,12 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   int rows = act.rows;
   if (act.rss) {
     a.rss = act.rss;
-    a.rss_nh = act.K / 64;
+    a.rss_nh = act.K / 32;
     a.rss_n = act.K;
     a.rss_eps = act.eps;
   }
   const bool sk = a8_sk_wanted(a, EPI);
+  PGD_CHECK(!(a.nact.XA && sk), kErrShape, "norm-emitting residual GEMV on a stream-K matrix");
   // plain matrices stream their weights once per 64 rows when the second
   // chunk of a pair holds more than 4 rows (full operand layout)
   const bool pairs = EPI != EPI_SWIGLU && !sk && a.n_out % 4 == 0;
@@ -882,12 +998,16 @@ void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s) {
 
 }  // namespace gemv
 
-// operands | constants | deferred-norm row sums ([rows][K / 64], 256 B aligned)
+// operands | constants | deferred-norm row sums ([rows][K / 32], 256 B aligned)
 static size_t rss_offset(int rows, int K) {
   return (a8act::xa_bytes(rows, K / 64) + a8act::ca_bytes(rows, K / 64) + 255) & ~(size_t)255;
 }
 
-size_t a8_act_bytes(int rows, int K) { return rss_offset(rows, K) + (size_t)rows * (K / 64) * sizeof(float); }
+float* a8_act_rss(void* buf, int rows, int K) {
+  return reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(buf) + rss_offset(rows, K));
+}
+
+size_t a8_act_bytes(int rows, int K) { return rss_offset(rows, K) + (size_t)rows * (K / 32) * sizeof(float); }
 
 A8Act a8_act_view(void* buf, int rows, int K) {
   A8Act a;
@@ -915,7 +1035,7 @@ A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream
 A8Act a8_gnorm_prep(const float* x, int ldx, int rows, int n, const float* w, float eps, void* buf, hipStream_t s) {
   PGD_CHECK(n % 64 == 0 && ldx % 4 == 0, kErrShape, "A8 activation width must be a multiple of 64");
   A8Act a = a8_act_view(buf, rows, n);
-  float* rss = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(buf) + rss_offset(rows, n));
+  float* rss = a8_act_rss(buf, rows, n);
   a.rss = rss;
   a.eps = eps;
   if (rows <= 0) return a;

@@ -265,6 +265,8 @@ struct Ws {
   float *x, *xn, *A, *B, *C0, *C1, *D, *E, *F, *G, *logits;
   void* act;   // prepared A8 activation operands
   void* act2;  // second set: the SwiGLU product feeding the down projection
+  void* act3;  // third set: the post-mixer norm's input, written by the mixer's
+               // output projection while it reads act
   size_t lda, ldb, ldd, lde;
 };
 
@@ -276,15 +278,16 @@ Ws carve_ws(Model& m, int rows, int lrows) {
   size_t ldc = std::max<size_t>(align_up(std::max(c.v_heads, 1), 8), m.kv_width);
   size_t ldd = std::max<size_t>(m.conv_dim, (size_t)c.heads * c.head_dim);
   size_t lde = std::max<size_t>(m.value_dim, (size_t)c.heads * c.head_dim);
-  size_t act_floats = 0, act2_floats = 0;
+  size_t act_floats = 0, act2_floats = 0, act3_floats = 0;
   if (c.arch == PGD_ARCH_QWEN35) {
     int kmax = std::max(std::max(c.hidden, c.intermediate), std::max(m.value_dim, c.heads * c.head_dim));
     act_floats = (a8_act_bytes(rows, kmax) + 3) / 4;
     act2_floats = (a8_act_bytes(rows, c.intermediate) + 3) / 4;
+    act3_floats = (a8_act_bytes(rows, c.hidden) + 3) / 4;
   }
   size_t sizes[] = {rows * H, rows * H, rows * lda, rows * ldb, rows * ldc, rows * ldc, rows * ldd, rows * lde,
                     rows * (size_t)c.heads * c.head_dim, rows * (size_t)c.intermediate, (size_t)lrows * c.vocab,
-                    act_floats, act2_floats};
+                    act_floats, act2_floats, act3_floats};
   size_t total = 0;
   for (size_t v : sizes) total += align_up(v, 64);
   if (m.ws.bytes < total * 4) {
@@ -292,13 +295,13 @@ Ws carve_ws(Model& m, int rows, int lrows) {
     m.ws = DevBuf(total * 4);
   }
   float* p = m.ws.as<float>();
-  float* ptrs[13];
-  for (int i = 0; i < 13; ++i) {
+  float* ptrs[14];
+  for (int i = 0; i < 14; ++i) {
     ptrs[i] = p;
     p += align_up(sizes[i], 64);
   }
   Ws w{ptrs[0], ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], ptrs[6], ptrs[7], ptrs[8], ptrs[9], ptrs[10],
-       (void*)ptrs[11], (void*)ptrs[12], lda, ldb, ldd, lde};
+       (void*)ptrs[11], (void*)ptrs[12], (void*)ptrs[13], lda, ldb, ldd, lde};
   return w;
 }
 
@@ -453,13 +456,19 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   qmat_embed(m.embed, d_tok, rows, w.x, H, st);
   const size_t per_lin = m.conv_floats + m.state_floats;
   const bool hybrid = c.arch == PGD_ARCH_QWEN35;
-  for (auto& L : m.layers) {
+  // the next input norm's deferred input, when the last residual GEMV wrote it
+  A8Act next_in;
+  bool have_next_in = false;
+  for (size_t li = 0; li < m.layers.size(); ++li) {
+    auto& L = m.layers[li];
+    A8Act post_in;  // the post-mixer norm's deferred input
     // ---- projections of the normed input ----
     const float *q_raw = nullptr, *k_raw = nullptr, *v_raw = nullptr;
     int ld_q = 0, ld_kv = 0;
     if (hybrid) {
-      // one fused norm + operand prep, one launch for all projections
-      A8Act act = a8_gnorm_prep(w.x, H, rows, H, L.in_norm, eps, w.act, st);
+      // the input norm's deferred operands: written by the previous layer's down
+      // projection, or prepared here for the first layer; one GEMV for all projections
+      A8Act act = have_next_in ? next_in : a8_gnorm_prep(w.x, H, rows, H, L.in_norm, eps, w.act, st);
       qmat_gemv_a8(L.proj, act, w.A, (int)w.lda, nullptr, 0, st);
       if (L.full) {
         q_raw = w.A;
@@ -506,7 +515,8 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       gp.state_base = d_sb;
       gp.state_off = (size_t)L.lin_index * per_lin + m.conv_floats;
       gdn_step(gp, sm, nseq, st);
-      qmat_gemv_a8(L.out, act, w.x, H, w.x, H, st);
+      // the residual GEMV also writes the post-mixer norm's input (act3)
+      post_in = qmat_gemv_a8_res_norm(L.out, act, w.x, H, L.post_norm, eps, w.act3, st);
     } else {
       AttnLayout al{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.kv_block, L.k_pool, L.v_pool};
       QkvPrep qp{};
@@ -529,7 +539,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
         const A8Act act = a8_act_view(w.act, rows, c.heads * c.head_dim);
         const a8act::Dst dst = a8_act_dst(act);
         attn_decode(w.D, w.F, nullptr, al, rm, ap, rows, st, &dst);
-        qmat_gemv_a8(L.o, act, w.x, H, w.x, H, st);
+        post_in = qmat_gemv_a8_res_norm(L.o, act, w.x, H, L.post_norm, eps, w.act3, st);
       } else {
         attn_decode(w.D, nullptr, w.E, al, rm, ap, rows, st);
         qmat_gemv(L.o, w.E, 0, c.heads * c.head_dim, rows, w.x, H, w.x, H, st);
@@ -537,11 +547,17 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     }
     // ---- SwiGLU MLP ----
     if (hybrid) {
-      A8Act act = a8_gnorm_prep(w.x, H, rows, H, L.post_norm, eps, w.act, st);
+      const A8Act act = post_in;
       // the SwiGLU epilogue writes the down projection's operands itself
       const A8Act mid = a8_act_view(w.act2, rows, c.intermediate);
       qmat_gemv_a8_swiglu(L.gate, L.up, act, nullptr, 0, st, &mid);
-      qmat_gemv_a8(L.down, mid, w.x, H, w.x, H, st);
+      // the residual GEMV also writes the next layer's input norm (act)
+      if (li + 1 < m.layers.size()) {
+        next_in = qmat_gemv_a8_res_norm(L.down, mid, w.x, H, m.layers[li + 1].in_norm, eps, w.act, st);
+        have_next_in = true;
+      } else {
+        qmat_gemv_a8(L.down, mid, w.x, H, w.x, H, st);
+      }
     } else {
       rmsnorm_rows(w.x, H, nullptr, rows, H, L.post_norm, eps, norm_mode, w.xn, H, st);
       qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);

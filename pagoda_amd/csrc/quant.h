@@ -126,8 +126,8 @@ struct A8Act {
   const float* CA = nullptr;
   int rows = 0, K = 0;
   // deferred RMSNorm (a8_gnorm_prep): the operands hold x * w without the
-  // 1/rms factor, rss holds per row the K/64 partial sums of x^2 (one per
-  // 64-wide group), and the consuming GEMV scales row b's outputs by
+  // 1/rms factor, rss holds per row the K/32 partial sums of x^2 (one per
+  // 32-wide half group), and the consuming GEMV scales row b's outputs by
   // 1/sqrt(sum / K + eps). Null: the operands are the finished input.
   const float* rss = nullptr;
   float eps = 0.0f;
@@ -138,6 +138,15 @@ A8Act a8_act_view(void* buf, int rows, int K);
 a8act::Dst a8_act_dst(const A8Act& a);
 // from f32 rows x [rows, ldx]
 A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream_t s);
+// the deferred-norm row sums region of an activation buffer
+float* a8_act_rss(void* buf, int rows, int K);
+// Residual A8 GEMV y += W act (in place) that also writes the next RMSNorm's
+// deferred input from the new rows into nbuf (a8_act_bytes(rows, n_out)):
+// operands of y * nw and their row sums, exactly as a8_gnorm_prep would make
+// them from y. n_out must be a multiple of 32; matrices that take the
+// stream-K kernel are not supported.
+A8Act qmat_gemv_a8_res_norm(const QMat& m, const A8Act& act, float* y, int ldy, const float* nw, float eps,
+                            void* nbuf, hipStream_t s);
 // RMSNorm with the scale deferred to the consumer: operands of x * w and the
 // row's partial sums of squares (A8Act.rss); one wave per (32-row chunk,
 // group, 16-row tile), no per-row reduction. Feeds A8 GEMVs only.

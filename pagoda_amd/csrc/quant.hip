@@ -559,6 +559,26 @@ void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const floa
   run_a8_mma(a, act, res ? EPI_RES : EPI_STORE, s);
 }
 
+A8Act qmat_gemv_a8_res_norm(const QMat& m, const A8Act& act, float* y, int ldy, const float* nw, float eps,
+                            void* nbuf, hipStream_t s) {
+  PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "prepared activations feed A8 matrices");
+  PGD_CHECK(m.n_out % 32 == 0 && ldy % 4 == 0, kErrShape, "norm-emitting residual GEMV: width");
+  A8Act out = a8_act_view(nbuf, act.rows, m.n_out);
+  out.rss = a8_act_rss(nbuf, act.rows, m.n_out);
+  out.eps = eps;
+  if (act.rows <= 0) return out;
+  GemvArgs a = make_args(m);
+  a.y = y;
+  a.ldy = ldy;
+  a.res = y;
+  a.ldres = ldy;
+  a.nact = a8_act_dst(out);
+  a.nw = nw;
+  a.nrss = const_cast<float*>(out.rss);
+  run_a8_mma(a, act, EPI_RES, s);
+  return out;
+}
+
 void qmat_gemv_a8_swiglu(const QMat& gate, const QMat& up, const A8Act& act, float* mid, int ldm, hipStream_t s,
                          const A8Act* mid_act) {
   PGD_CHECK(gate.fmt == FMT_A8 && up.fmt == FMT_A8 && gate.n_out == up.n_out && gate.n_in == up.n_in, kErrShape,
