@@ -157,6 +157,26 @@ typedef struct pgd_session pgd_session;
 /* Build a model with seeded synthetic weights generated on the device (the
  * configs use random-init weights; no reference counterpart). */
 int pgd_model_synth(pgd_dev* dev, const pgd_model_config* cfg, uint64_t seed, pgd_model** out);
+/* Qwen35::load (pagoda-hf/src/qwen3_5.rs:338-452, store 1587-1698): the
+ * language model of an MLX directory (config.json; model.safetensors.index.json
+ * and its shards, or a single model.safetensors). Matrices are 8-bit affine
+ * group 64 (u32 codes, bf16 scales / biases); norms, conv, A_log and dt_bias
+ * F32 / BF16 / F16. Layer kinds come from config.json's layer_types.
+ * max_pos <= 0: max_position_embeddings; kv_blocks > 0: KV pages per
+ * full-attention layer. Errors (missing tensors, shapes, quantization other
+ * than 8-bit affine group 64) return kErrFormat and allocate nothing. */
+int pgd_model_load_mlx(pgd_dev* dev, const char* dir, int max_pos, int kv_blocks, pgd_model** out);
+/* Qwen2 GGUF load (pagoda-hf/src/qwen2_gguf.rs:65-140): GGUF v2/v3,
+ * general.architecture "qwen2"; Q4_K / Q6_K matrices, F32 / F16 norms and
+ * q/k/v biases; lm_head is output.weight or the tied token_embd.weight.
+ * Tensors in other ggml block types are an error naming the tensor.
+ * max_pos <= 0: qwen2.context_length. */
+int pgd_model_load_gguf(pgd_dev* dev, const char* path, int max_pos, int kv_blocks, pgd_model** out);
+/* The configuration a loader derives from a checkpoint (a directory: MLX;
+ * a file: GGUF), without a device; no reference counterpart. */
+int pgd_checkpoint_config(const char* path, int max_pos, int kv_blocks, pgd_model_config* cfg);
+/* The configuration of a model (synthetic or loaded). */
+int pgd_model_config_get(const pgd_model* m, pgd_model_config* cfg);
 int pgd_model_free(pgd_model* m);
 /* weight bytes on the device, algorithmic weight bytes per decode step, KV pages free */
 int pgd_model_info(const pgd_model* m, size_t* weight_bytes, double* algo_bytes_per_token, int* kv_free);

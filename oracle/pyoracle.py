@@ -341,6 +341,9 @@ class Qwen2:
             raise ValueError(f"oracle forward failed {rc}")
         return out
 
+    def tensor_ptr(self, layer: int, kind: int, part: int = 0) -> int:
+        return lib().ora_qwen2_tensor(self.h, layer, kind, part)
+
     def __del__(self):
         try:
             lib().ora_qwen2_free(self.h)

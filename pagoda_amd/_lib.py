@@ -47,6 +47,10 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_matrix_gemv_act_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_int]),
     "pgd_matrix_gemv_swiglu_act_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int]),
     "pgd_model_synth": (c_int, [c_void_p, c_void_p, c_uint64, P(c_void_p)]),
+    "pgd_model_load_mlx": (c_int, [c_void_p, c_char_p, c_int, c_int, P(c_void_p)]),
+    "pgd_model_load_gguf": (c_int, [c_void_p, c_char_p, c_int, c_int, P(c_void_p)]),
+    "pgd_checkpoint_config": (c_int, [c_char_p, c_int, c_int, c_void_p]),
+    "pgd_model_config_get": (c_int, [c_void_p, c_void_p]),
     "pgd_model_free": (c_int, [c_void_p]),
     "pgd_model_info": (c_int, [c_void_p, P(c_size_t), P(c_double), P(c_int)]),
     "pgd_session_new": (c_int, [c_void_p, P(c_void_p)]),

@@ -16,26 +16,9 @@
 
 #include "common.h"
 
-struct pgd_model {
-  pgd::Model m;
-};
-
-struct pgd_session {
-  pgd::Session s;
-};
-
 namespace pgd {
 
 namespace {
-
-// Tensor keys of the synthetic generator: (layer << 8) | kind, layer 0xFFFF
-// for model-global tensors.
-enum {
-  K_EMBED = 1, K_HEAD = 2, K_FINAL_NORM = 3,
-  K_IN_NORM = 10, K_POST_NORM = 11, K_GATE = 12, K_UP = 13, K_DOWN = 14,
-  K_QKV = 20, K_Z = 21, K_A = 22, K_B = 23, K_OUT = 24, K_CONV = 25, K_ALOG = 26, K_DTB = 27, K_GNORM = 28,
-  K_Q = 30, K_K = 31, K_V = 32, K_O = 33, K_QNORM = 34, K_KNORM = 35, K_QB = 36, K_KB = 37, K_VB = 38
-};
 
 uint64_t tkey(int layer, int kind) { return ((uint64_t)(layer < 0 ? 0xFFFF : layer) << 8) | (uint64_t)kind; }
 
@@ -49,13 +32,9 @@ float* dev_floats(Model& m, size_t n) {
   return (float*)p;
 }
 
-float* dev_const(Model& m, size_t n, float v, hipStream_t s) {
-  float* p = dev_floats(m, n);
-  fill_f32(p, n, v, s);
-  return p;
-}
+}  // namespace
 
-void validate(const pgd_model_config& c) {
+void validate_config(const pgd_model_config& c, bool synthetic) {
   PGD_CHECK(c.arch == PGD_ARCH_QWEN35 || c.arch == PGD_ARCH_QWEN2, kErrArg, "unknown arch");
   PGD_CHECK(c.n_layers > 0 && c.hidden > 0 && c.intermediate > 0 && c.vocab > 0, kErrShape, "model dims");
   PGD_CHECK(c.heads > 0 && c.kv_heads > 0 && c.heads % c.kv_heads == 0, kErrShape, "heads / kv_heads");
@@ -67,14 +46,12 @@ void validate(const pgd_model_config& c) {
   PGD_CHECK(c.hidden % kmul == 0 && c.intermediate % kmul == 0 && (c.heads * c.head_dim) % kmul == 0, kErrShape,
             "GEMV input widths must be multiples of the quant group");
   if (c.arch == PGD_ARCH_QWEN35) {
-    PGD_CHECK(c.full_every >= 1, kErrShape, "full_every");
+    PGD_CHECK(!synthetic || c.full_every >= 1, kErrShape, "full_every");
     PGD_CHECK(c.k_dim == 128 && c.v_dim == 128, kErrShape, "gated delta needs k_dim == v_dim == 128");
     PGD_CHECK(c.k_heads > 0 && c.v_heads % c.k_heads == 0, kErrShape, "v_heads % k_heads");
     PGD_CHECK(c.conv_kernel >= 2 && c.conv_kernel <= 8, kErrShape, "conv kernel");
   }
 }
-
-}  // namespace
 
 // ---------------------------------------------------------------------------
 Model::~Model() {
@@ -155,13 +132,18 @@ Session::~Session() {
 }
 
 // ---------------------------------------------------------------------------
-// synthetic model
+// model build (from any weight source) and the synthetic source
 // ---------------------------------------------------------------------------
-static void build_synth(Model& m, uint64_t seed) {
+void build_model(Model& m, WeightSource& src) {
   const pgd_model_config& c = m.cfg;
   hipStream_t s = m.dev->stream;
   const int H = c.hidden;
   m.kv_width = c.kv_heads * c.head_dim;
+  auto vec = [&](size_t n, int li, int kind) {
+    float* p = dev_floats(m, n);
+    src.vec(p, n, li, kind, s);
+    return p;
+  };
   if (c.arch == PGD_ARCH_QWEN35) {
     m.key_dim = c.k_heads * c.k_dim;
     m.value_dim = c.v_heads * c.v_dim;
@@ -169,75 +151,58 @@ static void build_synth(Model& m, uint64_t seed) {
     m.q_out = c.heads * c.head_dim * 2;
     m.proj_lin = m.conv_dim + m.value_dim + 2 * c.v_heads;
     m.proj_full = m.q_out + 2 * m.kv_width;
-    qmat_alloc(m.embed, FMT_A8, c.vocab, H, s);
-    qmat_synth(m.embed, seed, tkey(-1, K_EMBED), 0.02f, s);
-    qmat_alloc(m.head, FMT_A8, c.vocab, H, s);
-    qmat_synth(m.head, seed, tkey(-1, K_HEAD), 0.02f, s);
+    src.matrix(m.embed, FMT_A8, c.vocab, H, -1, K_EMBED, s);
   } else {
     m.q_out = c.heads * c.head_dim;
-    qmat_alloc(m.embed, FMT_Q6K, c.vocab, H, s);
-    qmat_synth(m.embed, seed, tkey(-1, K_EMBED), 0.02f, s);
+    src.matrix(m.embed, FMT_Q6K, c.vocab, H, -1, K_EMBED, s);
+  }
+  if (src.tied_head()) {
     m.head = m.embed;  // tied lm_head (qwen2_gguf.rs:96-99)
     m.tied = true;
+  } else {
+    src.matrix(m.head, m.embed.fmt, c.vocab, H, -1, K_HEAD, s);
   }
-  m.final_norm = dev_const(m, H, 1.0f, s);
+  m.final_norm = vec(H, -1, K_FINAL_NORM);
   m.layers.resize(c.n_layers);
   size_t kv_per_layer = (size_t)c.kv_blocks * c.kv_heads * c.kv_block * c.head_dim;
-  auto mat = [&](QMat& q, int fmt, int n_out, int n_in, int li, int kind) {
-    qmat_alloc(q, fmt, n_out, n_in, s);
-    qmat_synth(q, seed, tkey(li, kind), 0.02f, s);
-  };
   for (int i = 0; i < c.n_layers; ++i) {
     Layer& L = m.layers[i];
-    L.in_norm = dev_const(m, H, 1.0f, s);
-    L.post_norm = dev_const(m, H, 1.0f, s);
+    L.in_norm = vec(H, i, K_IN_NORM);
+    L.post_norm = vec(H, i, K_POST_NORM);
     if (c.arch == PGD_ARCH_QWEN35) {
-      L.full = (i % c.full_every) == c.full_every - 1;
-      mat(L.gate, FMT_A8, c.intermediate, H, i, K_GATE);
-      mat(L.up, FMT_A8, c.intermediate, H, i, K_UP);
-      mat(L.down, FMT_A8, H, c.intermediate, i, K_DOWN);
+      L.full = src.full_layer(i);
+      src.matrix(L.gate, FMT_A8, c.intermediate, H, i, K_GATE, s);
+      src.matrix(L.up, FMT_A8, c.intermediate, H, i, K_UP, s);
+      src.matrix(L.down, FMT_A8, H, c.intermediate, i, K_DOWN, s);
       if (!L.full) {
         L.lin_index = m.n_lin++;
-        // [qkv | z | b | a] stacked; each range keeps its own tensor key
-        qmat_alloc(L.proj, FMT_A8, m.proj_lin, H, s);
-        qmat_synth_rows(L.proj, 0, m.conv_dim, seed, tkey(i, K_QKV), 0.02f, s);
-        qmat_synth_rows(L.proj, m.conv_dim, m.value_dim, seed, tkey(i, K_Z), 0.02f, s);
-        qmat_synth_rows(L.proj, m.conv_dim + m.value_dim, c.v_heads, seed, tkey(i, K_B), 0.02f, s);
-        qmat_synth_rows(L.proj, m.conv_dim + m.value_dim + c.v_heads, c.v_heads, seed, tkey(i, K_A), 0.02f, s);
-        mat(L.out, FMT_A8, H, m.value_dim, i, K_OUT);
-        L.conv = dev_floats(m, (size_t)m.conv_dim * c.conv_kernel);
-        synth_normal_f32(L.conv, (size_t)m.conv_dim * c.conv_kernel, seed, tkey(i, K_CONV), 0.2f, s);
-        L.a_log = dev_floats(m, c.v_heads);
-        synth_uniform_f32(L.a_log, c.v_heads, seed, tkey(i, K_ALOG), 2.7725887f, s);
-        L.dt_bias = dev_floats(m, c.v_heads);
-        synth_normal_f32(L.dt_bias, c.v_heads, seed, tkey(i, K_DTB), 0.1f, s);
-        L.gnorm = dev_const(m, c.v_dim, 1.0f, s);
+        // [qkv | z | b | a] stacked, one launch
+        src.stacked(L.proj, H, {{K_QKV, m.conv_dim}, {K_Z, m.value_dim}, {K_B, c.v_heads}, {K_A, c.v_heads}}, i, s);
+        src.matrix(L.out, FMT_A8, H, m.value_dim, i, K_OUT, s);
+        L.conv = vec((size_t)m.conv_dim * c.conv_kernel, i, K_CONV);
+        L.a_log = vec(c.v_heads, i, K_ALOG);
+        L.dt_bias = vec(c.v_heads, i, K_DTB);
+        L.gnorm = vec(c.v_dim, i, K_GNORM);
       } else {
         L.full_index = m.n_full++;
-        qmat_alloc(L.proj, FMT_A8, m.proj_full, H, s);
-        qmat_synth_rows(L.proj, 0, m.q_out, seed, tkey(i, K_Q), 0.02f, s);
-        qmat_synth_rows(L.proj, m.q_out, m.kv_width, seed, tkey(i, K_K), 0.02f, s);
-        qmat_synth_rows(L.proj, m.q_out + m.kv_width, m.kv_width, seed, tkey(i, K_V), 0.02f, s);
-        mat(L.o, FMT_A8, H, c.heads * c.head_dim, i, K_O);
-        L.q_norm = dev_const(m, c.head_dim, 1.0f, s);
-        L.k_norm = dev_const(m, c.head_dim, 1.0f, s);
+        src.stacked(L.proj, H, {{K_Q, m.q_out}, {K_K, m.kv_width}, {K_V, m.kv_width}}, i, s);
+        src.matrix(L.o, FMT_A8, H, c.heads * c.head_dim, i, K_O, s);
+        L.q_norm = vec(c.head_dim, i, K_QNORM);
+        L.k_norm = vec(c.head_dim, i, K_KNORM);
       }
     } else {
       L.full = true;
       L.full_index = m.n_full++;
-      mat(L.q, FMT_Q4K, m.q_out, H, i, K_Q);
-      mat(L.k, FMT_Q4K, m.kv_width, H, i, K_K);
-      mat(L.v, FMT_Q6K, m.kv_width, H, i, K_V);
-      mat(L.o, FMT_Q4K, H, c.heads * c.head_dim, i, K_O);
-      mat(L.gate, FMT_Q4K, c.intermediate, H, i, K_GATE);
-      mat(L.up, FMT_Q4K, c.intermediate, H, i, K_UP);
-      mat(L.down, i % 2 == 0 ? FMT_Q6K : FMT_Q4K, H, c.intermediate, i, K_DOWN);
-      L.qb = dev_floats(m, m.q_out);
-      synth_normal_f32(L.qb, m.q_out, seed, tkey(i, K_QB), 0.02f, s);
-      L.kb = dev_floats(m, m.kv_width);
-      synth_normal_f32(L.kb, m.kv_width, seed, tkey(i, K_KB), 0.02f, s);
-      L.vb = dev_floats(m, m.kv_width);
-      synth_normal_f32(L.vb, m.kv_width, seed, tkey(i, K_VB), 0.02f, s);
+      src.matrix(L.q, FMT_Q4K, m.q_out, H, i, K_Q, s);
+      src.matrix(L.k, FMT_Q4K, m.kv_width, H, i, K_K, s);
+      src.matrix(L.v, FMT_Q6K, m.kv_width, H, i, K_V, s);
+      src.matrix(L.o, FMT_Q4K, H, c.heads * c.head_dim, i, K_O, s);
+      src.matrix(L.gate, FMT_Q4K, c.intermediate, H, i, K_GATE, s);
+      src.matrix(L.up, FMT_Q4K, c.intermediate, H, i, K_UP, s);
+      src.matrix(L.down, i % 2 == 0 ? FMT_Q6K : FMT_Q4K, H, c.intermediate, i, K_DOWN, s);
+      L.qb = vec(m.q_out, i, K_QB);
+      L.kb = vec(m.kv_width, i, K_KB);
+      L.vb = vec(m.kv_width, i, K_VB);
     }
     if (L.full) {
       L.k_pool = dev_floats(m, kv_per_layer);
@@ -255,6 +220,49 @@ static void build_synth(Model& m, uint64_t seed) {
   for (int b = 0; b < c.kv_blocks; ++b) m.free_blocks[b] = c.kv_blocks - 1 - b;
   PGD_HIP(hipStreamSynchronize(s));
 }
+
+namespace {
+
+// Seeded synthetic weights, generated on the device: matrices N(0, 0.02)
+// quantized in their format, norms 1, conv N(0, 0.2), A_log ln(16) U(0,1),
+// dt_bias N(0, 0.1), q/k/v biases N(0, 0.02).
+class SynthSource : public WeightSource {
+ public:
+  SynthSource(const pgd_model_config& c, uint64_t seed) : c_(c), seed_(seed) {}
+  bool full_layer(int i) const override { return (i % c_.full_every) == c_.full_every - 1; }
+  bool tied_head() const override { return c_.arch == PGD_ARCH_QWEN2; }
+  void matrix(QMat& q, int fmt, int n_out, int n_in, int li, int kind, hipStream_t s) override {
+    qmat_alloc(q, fmt, n_out, n_in, s);
+    qmat_synth(q, seed_, tkey(li, kind), 0.02f, s);
+  }
+  void stacked(QMat& q, int n_in, const std::vector<std::pair<int, int>>& parts, int li, hipStream_t s) override {
+    int n = 0;
+    for (auto& p : parts) n += p.second;
+    qmat_alloc(q, FMT_A8, n, n_in, s);
+    int r = 0;
+    for (auto& p : parts) {  // each range keeps its own tensor key
+      qmat_synth_rows(q, r, p.second, seed_, tkey(li, p.first), 0.02f, s);
+      r += p.second;
+    }
+  }
+  void vec(float* p, size_t n, int li, int kind, hipStream_t s) override {
+    switch (kind) {
+      case K_CONV: synth_normal_f32(p, n, seed_, tkey(li, kind), 0.2f, s); break;
+      case K_ALOG: synth_uniform_f32(p, n, seed_, tkey(li, kind), 2.7725887f, s); break;
+      case K_DTB: synth_normal_f32(p, n, seed_, tkey(li, kind), 0.1f, s); break;
+      case K_QB:
+      case K_KB:
+      case K_VB: synth_normal_f32(p, n, seed_, tkey(li, kind), 0.02f, s); break;
+      default: fill_f32(p, n, 1.0f, s);  // norm weights
+    }
+  }
+
+ private:
+  pgd_model_config c_;
+  uint64_t seed_;
+};
+
+}  // namespace
 
 // ---------------------------------------------------------------------------
 // ragged step
@@ -618,12 +626,13 @@ int pgd_model_synth(pgd_dev* dev, const pgd_model_config* cfg, uint64_t seed, pg
   pgd_model* held = nullptr;
   int rc = guard([&] {
     PGD_CHECK(dev && cfg && out, kErrArg, "null argument");
-    validate(*cfg);
+    validate_config(*cfg, true);
     DeviceScope scope(dev);
     held = new pgd_model();
     held->m.dev = dev;
     held->m.cfg = *cfg;
-    build_synth(held->m, seed);
+    SynthSource src(*cfg, seed);
+    build_model(held->m, src);
     *out = held;
   });
   if (rc && held) delete held;

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <utility>
 #include <vector>
 
 #include "../../include/pagoda_hip.h"
@@ -96,6 +97,36 @@ struct Session {
   ~Session();
 };
 
+// Tensor kinds: model-level (layer -1) and per-layer tensors. The synthetic
+// generator keys its streams by (layer << 8) | kind.
+enum TensorKind {
+  K_EMBED = 1, K_HEAD = 2, K_FINAL_NORM = 3,
+  K_IN_NORM = 10, K_POST_NORM = 11, K_GATE = 12, K_UP = 13, K_DOWN = 14,
+  K_QKV = 20, K_Z = 21, K_A = 22, K_B = 23, K_OUT = 24, K_CONV = 25, K_ALOG = 26, K_DTB = 27, K_GNORM = 28,
+  K_Q = 30, K_K = 31, K_V = 32, K_O = 33, K_QNORM = 34, K_KNORM = 35, K_QB = 36, K_KB = 37, K_VB = 38
+};
+
+// Where a model's tensors come from: seeded synthesis or a checkpoint.
+struct WeightSource {
+  virtual ~WeightSource() = default;
+  virtual bool full_layer(int layer) const = 0;
+  // lm_head shares the embedding matrix
+  virtual bool tied_head() const = 0;
+  // allocate q and fill it; fmt is the synthetic model's format, which a
+  // checkpoint replaces by the stored one
+  virtual void matrix(QMat& q, int fmt, int n_out, int n_in, int layer, int kind, hipStream_t s) = 0;
+  // one A8 matrix of row ranges taken from several tensors: parts = {kind, rows}
+  virtual void stacked(QMat& q, int n_in, const std::vector<std::pair<int, int>>& parts, int layer,
+                       hipStream_t s) = 0;
+  // fill n device floats
+  virtual void vec(float* dst, size_t n, int layer, int kind, hipStream_t s) = 0;
+};
+
+// Allocate and fill every tensor of m (m.dev and m.cfg set, cfg validated).
+void build_model(Model& m, WeightSource& src);
+// Checks of a configuration; synthetic models also need the layer pattern.
+void validate_config(const pgd_model_config& c, bool synthetic);
+
 // Output request of a step.
 struct StepOut {
   // rows whose logits are computed: 0 = last row of each sequence, 1 = every row
@@ -111,3 +142,12 @@ struct StepOut {
 void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, int nseq, StepOut& out);
 
 }  // namespace pgd
+
+// the opaque handles of the C ABI
+struct pgd_model {
+  pgd::Model m;
+};
+
+struct pgd_session {
+  pgd::Session s;
+};

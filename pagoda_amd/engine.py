@@ -58,6 +58,24 @@ QWEN2_05B = ModelConfig(arch=ARCH_QWEN2, n_layers=24, hidden=896, intermediate=4
                         k_dim=0, v_dim=0, conv_kernel=0, full_every=1, max_pos=32768, kv_blocks=2048)
 
 
+def _from_ctype(c: _Cfg) -> ModelConfig:
+    return ModelConfig(**{f.name: getattr(c, f.name) for f in fields(ModelConfig)})
+
+
+def _config_of(h: C.c_void_p) -> ModelConfig:
+    c = _Cfg()
+    call("pgd_model_config_get", h, C.byref(c))
+    return _from_ctype(c)
+
+
+def checkpoint_config(path: str, max_pos: int = 0, kv_blocks: int = 2048) -> ModelConfig:
+    """The configuration pgd_model_load_mlx (a directory) or
+    pgd_model_load_gguf (a file) derives from a checkpoint; needs no device."""
+    c = _Cfg()
+    call("pgd_checkpoint_config", str(path).encode(), int(max_pos), int(kv_blocks), C.byref(c))
+    return _from_ctype(c)
+
+
 def _u32(a) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(a, dtype=np.uint32).reshape(-1))
 
@@ -78,6 +96,22 @@ class Model:
         c = cfg.ctype()
         call("pgd_model_synth", dev.handle, C.byref(c), C.c_uint64(seed), C.byref(h))
         return cls(dev, h, replace(cfg))
+
+    @classmethod
+    def load_mlx(cls, dev: Device, path: str, max_pos: int = 0, kv_blocks: int = 2048) -> "Model":
+        """Qwen35::load (pagoda-hf/src/qwen3_5.rs:338-452): an MLX 8-bit model
+        directory. max_pos 0: the config's max_position_embeddings."""
+        h = C.c_void_p()
+        call("pgd_model_load_mlx", dev.handle, str(path).encode(), int(max_pos), int(kv_blocks), C.byref(h))
+        return cls(dev, h, _config_of(h))
+
+    @classmethod
+    def load_gguf(cls, dev: Device, path: str, max_pos: int = 0, kv_blocks: int = 2048) -> "Model":
+        """Qwen2 GGUF load (pagoda-hf/src/qwen2_gguf.rs:65-140). max_pos 0:
+        qwen2.context_length."""
+        h = C.c_void_p()
+        call("pgd_model_load_gguf", dev.handle, str(path).encode(), int(max_pos), int(kv_blocks), C.byref(h))
+        return cls(dev, h, _config_of(h))
 
     def info(self) -> dict:
         wb, ab, kf = C.c_size_t(), C.c_double(), C.c_int()
