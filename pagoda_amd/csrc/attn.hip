@@ -103,6 +103,12 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
     const int krow = qlive ? (q0 + qi) / G : 0, g = qlive ? (q0 + qi) % G : 0;
     const int row = plan.item_rows[row_off + krow];
     const int len = m.pos_of_row[row] + 1;  // positions [0, len) are visible
+    // V rows at or past every live query's length are unwritten slots of the
+    // last page (any bit pattern). P is 0 there, but 0 * NaN is not 0, so
+    // those rows are zeroed before P V.
+    int lmax = qlive ? len : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lmax = max(lmax, __shfl_xor(lmax, o, 64));
     float Q[T];
     {
       const float* qp = q + ((size_t)row * L.heads + kvh * G + g) * HD + T * kq;
@@ -191,6 +197,13 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
         const float al = __shfl(alpha, 4 * kq + r, 64);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) O[nt][r] *= al;
+      }
+      if (pos0 - 4 * kq + L.block > lmax) {  // wave-uniform: a page with unwritten slots
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          if (pos0 + s >= lmax)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) Vr[s][nt] = 0.0f;
       }
       // ---- O += P V: A = P[n = j][p = 4 kq + s] (= sc[s]), B = V[4 kq + s][NT j + nt] ----
 #pragma unroll

@@ -112,8 +112,12 @@ def test_gdn_ragged_mix(dev):
         r += n
 
 
+@pytest.mark.parametrize("poison", [False, True])
 @pytest.mark.parametrize("heads,kvh,hd", [(24, 4, 256), (14, 2, 64), (8, 8, 128)])
-def test_paged_attention_ragged(dev, heads, kvh, hd):
+def test_paged_attention_ragged(dev, heads, kvh, hd, poison):
+    """Ragged rows over scattered pages. poison: every slot past a sequence's
+    last visible position, and every unused page, holds NaN (a pool reusing
+    freed memory holds any bit pattern there); results must not change."""
     from pagoda_amd._lib import call
     import ctypes as C
 
@@ -137,6 +141,16 @@ def test_paged_attention_ragged(dev, heads, kvh, hd):
     # one query row per sequence at its last position, plus one mid-sequence row
     seq_of_row = list(range(len(lens))) + [5]
     pos_of_row = [n - 1 for n in lens] + [150]
+    if poison:
+        used = set()
+        for sq, t in enumerate(tables):
+            used.update(t)
+            for p in range(lens[sq], len(t) * block):
+                kpool[t[p // block], :, p % block] = np.nan
+                vpool[t[p // block], :, p % block] = np.nan
+        for pg in set(range(total_pages)) - used:
+            kpool[pg] = np.nan
+            vpool[pg] = np.nan
     rows = len(seq_of_row)
     q = rng.normal(0, 1, (rows, heads, hd)).astype(np.float32)
     gate = rng.normal(0, 1, (rows, heads, hd)).astype(np.float32)
