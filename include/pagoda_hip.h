@@ -74,6 +74,12 @@ int pgd_matrix_upload_a8(pgd_dev* dev, const uint32_t* packed, const uint16_t* s
  * replaces the QTensor -> QMatMul load of pagoda-hf/src/qwen2_gguf.rs:283-289. */
 int pgd_matrix_upload_q4k(pgd_dev* dev, const void* blocks, int n_out, int n_in, pgd_matrix** out);
 int pgd_matrix_upload_q6k(pgd_dev* dev, const void* blocks, int n_out, int n_in, pgd_matrix** out);
+/* GGML block_q8_0 / block_q5_0 rows of n_in/32 blocks (34 B / 22 B; n_in a
+ * multiple of 32): the types a Q4_K_M GGUF holds for rows that are not whole
+ * 256-weight super-blocks, loaded by candle at pagoda-hf/src/qwen2_gguf.rs:
+ * 283-289 like the k-quants. Format ids 3 and 4 in pgd_matrix_info. */
+int pgd_matrix_upload_q8_0(pgd_dev* dev, const void* blocks, int n_out, int n_in, pgd_matrix** out);
+int pgd_matrix_upload_q5_0(pgd_dev* dev, const void* blocks, int n_out, int n_in, pgd_matrix** out);
 /* Seeded synthetic matrix: N(0, std) weights quantized on the device (no
  * reference counterpart: the reference only loads checkpoints). */
 int pgd_matrix_synth(pgd_dev* dev, int fmt, int n_out, int n_in, uint64_t seed, uint64_t key, float std,
@@ -167,7 +173,7 @@ int pgd_model_synth(pgd_dev* dev, const pgd_model_config* cfg, uint64_t seed, pg
  * than 8-bit affine group 64) return kErrFormat and allocate nothing. */
 int pgd_model_load_mlx(pgd_dev* dev, const char* dir, int max_pos, int kv_blocks, pgd_model** out);
 /* Qwen2 GGUF load (pagoda-hf/src/qwen2_gguf.rs:65-140): GGUF v2/v3,
- * general.architecture "qwen2"; Q4_K / Q6_K matrices, F32 / F16 norms and
+ * general.architecture "qwen2"; Q4_K / Q6_K / Q8_0 / Q5_0 matrices, F32 / F16 norms and
  * q/k/v biases; lm_head is output.weight or the tied token_embd.weight.
  * Tensors in other ggml block types are an error naming the tensor.
  * max_pos <= 0: qwen2.context_length. */

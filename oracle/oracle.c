@@ -394,6 +394,41 @@ void ora_q6k_quantize(const float* w, int n_out, int n_in, uint8_t* blocks) {
   }
 }
 
+/* GGML Q8_0 and Q5_0 blocks of 32 weights (the public GGML block formats,
+ * which the reference reads through candle-core 0.8.4, pagoda-hf/Cargo.lock:
+ * 165; not under /root/reference). Q8_0: f16 d, int8 q[32], y = q * d.
+ * Q5_0: f16 d, 4 bytes qh (one little-endian u32 of high bits), 16 bytes qs;
+ * for j < 16, y[j] = (((qs[j] & 15) | (bit j of qh) << 4) - 16) * d and
+ * y[j + 16] = (((qs[j] >> 4) | (bit j + 16 of qh) << 4) - 16) * d.
+ * Pinned by hand-built blocks with known values (tests/test_oracle_formats.py). */
+void ora_q8_0_dequant(const uint8_t* blocks, int row0, int rows, int n_in, float* out) {
+  const int nb = n_in / 32;
+  for (int r = 0; r < rows; ++r)
+    for (int b = 0; b < nb; ++b) {
+      const uint8_t* blk = blocks + ((size_t)(row0 + r) * nb + b) * ORA_Q8_0_BYTES;
+      const float d = ora_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+      for (int j = 0; j < 32; ++j) out[(size_t)r * n_in + 32 * b + j] = (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+void ora_q5_0_dequant(const uint8_t* blocks, int row0, int rows, int n_in, float* out) {
+  const int nb = n_in / 32;
+  for (int r = 0; r < rows; ++r)
+    for (int b = 0; b < nb; ++b) {
+      const uint8_t* blk = blocks + ((size_t)(row0 + r) * nb + b) * ORA_Q5_0_BYTES;
+      const float d = ora_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+      const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                          ((uint32_t)blk[5] << 24);
+      float* o = out + (size_t)r * n_in + 32 * b;
+      for (int j = 0; j < 16; ++j) {
+        const int lo = (int)((blk[6 + j] & 15u) | (((qh >> j) & 1u) << 4)) - 16;
+        const int hi = (int)((blk[6 + j] >> 4) | (((qh >> (j + 16)) & 1u) << 4)) - 16;
+        o[j] = (float)lo * d;
+        o[j + 16] = (float)hi * d;
+      }
+    }
+}
+
 /* GGML dequantize_row_q6_K (public): y = d * sc * (q - 32), q from the low
  * nibble plane ql and the 2-bit plane qh, 128 elements per half block. */
 void ora_q6k_dequant(const uint8_t* blocks, int row0, int rows, int n_in, float* out) {
@@ -643,7 +678,7 @@ uint32_t ora_argmax_first(const float* x, int n) {
 /* ------------------------------------------------------------------ */
 /* quantized matrices                                                   */
 /* ------------------------------------------------------------------ */
-enum { FMT_A8 = 0, FMT_Q4K = 1, FMT_Q6K = 2 };
+enum { FMT_A8 = 0, FMT_Q4K = 1, FMT_Q6K = 2, FMT_Q8_0 = 3, FMT_Q5_0 = 4 };
 
 typedef struct {
   int fmt, n_out, n_in;
@@ -701,7 +736,9 @@ static void qmat_free(qmat* m) {
 static void qmat_dequant(const qmat* m, int row0, int rows, float* out) {
   if (m->fmt == FMT_A8) ora_a8_dequant(m->packed, m->scales, m->biases, row0, rows, m->n_in, out);
   else if (m->fmt == FMT_Q4K) ora_q4k_dequant(m->blocks, row0, rows, m->n_in, out);
-  else ora_q6k_dequant(m->blocks, row0, rows, m->n_in, out);
+  else if (m->fmt == FMT_Q6K) ora_q6k_dequant(m->blocks, row0, rows, m->n_in, out);
+  else if (m->fmt == FMT_Q8_0) ora_q8_0_dequant(m->blocks, row0, rows, m->n_in, out);
+  else ora_q5_0_dequant(m->blocks, row0, rows, m->n_in, out);
 }
 
 static const void* qmat_part(const qmat* m, int part) {
@@ -721,9 +758,7 @@ static void qmat_linear(const qmat* m, const float* x, int seq, float* y) {
 #pragma omp for schedule(static)
     for (int c0 = 0; c0 < n_out; c0 += chunk) {
       int n = n_out - c0 < chunk ? n_out - c0 : chunk;
-      if (m->fmt == FMT_A8) ora_a8_dequant(m->packed, m->scales, m->biases, c0, n, n_in, rows);
-      else if (m->fmt == FMT_Q4K) ora_q4k_dequant(m->blocks, c0, n, n_in, rows);
-      else ora_q6k_dequant(m->blocks, c0, n, n_in, rows);
+      qmat_dequant(m, c0, n, rows);
       for (int t = 0; t < seq; ++t)
         for (int r = 0; r < n; ++r) {
           const float* w = rows + (size_t)r * n_in;
@@ -1254,6 +1289,36 @@ const void* ora_qwen2_tensor(const ora_qwen2* m, int layer, int kind, int part) 
     case K_VB: return L->vb;
   }
   return NULL;
+}
+
+int ora_qwen2_set_matrix(ora_qwen2* m, int layer, int kind, int fmt, const uint8_t* blocks) {
+  qmat* q = NULL;
+  if (layer < 0) {
+    if (kind == K_EMBED) q = &m->embed;
+  } else if (layer < m->cfg.n_layers) {
+    q2_layer* L = &m->layers[layer];
+    switch (kind) {
+      case K_Q: q = &L->q; break;
+      case K_K: q = &L->k; break;
+      case K_V: q = &L->v; break;
+      case K_O: q = &L->o; break;
+      case K_GATE: q = &L->gate; break;
+      case K_UP: q = &L->up; break;
+      case K_DOWN: q = &L->down; break;
+    }
+  }
+  if (!q || fmt < FMT_Q4K || fmt > FMT_Q5_0) return -1;
+  if ((fmt == FMT_Q4K || fmt == FMT_Q6K) ? q->n_in % ORA_QK != 0 : q->n_in % 32 != 0) return -1;
+  size_t bytes = fmt == FMT_Q4K   ? (size_t)q->n_out * (q->n_in / ORA_QK) * ORA_Q4K_BYTES
+                 : fmt == FMT_Q6K ? (size_t)q->n_out * (q->n_in / ORA_QK) * ORA_Q6K_BYTES
+                 : fmt == FMT_Q8_0 ? (size_t)q->n_out * (q->n_in / 32) * ORA_Q8_0_BYTES
+                                   : (size_t)q->n_out * (q->n_in / 32) * ORA_Q5_0_BYTES;
+  uint8_t* nb = (uint8_t*)malloc(bytes);
+  memcpy(nb, blocks, bytes);
+  free(q->blocks);
+  q->blocks = nb;
+  q->fmt = fmt;
+  return 0;
 }
 
 ora_qwen2_cache* ora_qwen2_cache_new(const ora_qwen2* m) {

@@ -44,6 +44,13 @@ void ora_q6k_quantize(const float* w, int n_out, int n_in, uint8_t* blocks);
 void ora_q4k_dequant(const uint8_t* blocks, int row0, int rows, int n_in, float* out);
 void ora_q6k_dequant(const uint8_t* blocks, int row0, int rows, int n_in, float* out);
 
+/* ---- GGML 32-weight blocks (the fallback types of Q4_K_M files for rows
+ * that are not whole 256-weight super-blocks) ---- */
+#define ORA_Q8_0_BYTES 34
+#define ORA_Q5_0_BYTES 22
+void ora_q8_0_dequant(const uint8_t* blocks, int row0, int rows, int n_in, float* out);
+void ora_q5_0_dequant(const uint8_t* blocks, int row0, int rows, int n_in, float* out);
+
 /* ---- small ops ---- */
 void ora_rms_zero(float* x, const float* w, int n);
 void ora_rms_gated(float* x, const float* w, const float* gate, int n);
@@ -109,6 +116,9 @@ void ora_qwen2_cache_free(ora_qwen2_cache* c);
 int ora_qwen2_forward(ora_qwen2* m, const uint32_t* toks, int n, ora_qwen2_cache* c,
                       float* logits);
 const void* ora_qwen2_tensor(const ora_qwen2* m, int layer, int kind, int part);
+/* replace one matrix of the model by GGML blocks of format fmt (1 Q4_K,
+ * 2 Q6_K, 3 Q8_0, 4 Q5_0), rows x n_in as before; returns 0 or -1 */
+int ora_qwen2_set_matrix(ora_qwen2* m, int layer, int kind, int fmt, const uint8_t* blocks);
 
 /* greedy tie rule of the engine sampler: first max over finite values
  * (pagoda/src/sampler.rs:59-69). */

@@ -71,6 +71,9 @@ def lib():
         _lib.ora_qwen2_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
         _lib.ora_qwen35_tensor.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int]
         _lib.ora_qwen2_tensor.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int]
+        _lib.ora_qwen2_set_matrix.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]
+        for n in ("ora_q8_0_dequant", "ora_q5_0_dequant"):
+            getattr(_lib, n).argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]
         _lib.ora_qwen35_cache_to_bytes.restype = C.c_size_t
         _lib.ora_qwen35_cache_to_bytes.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
         _lib.ora_qwen35_cache_len.restype = C.c_int
@@ -145,6 +148,18 @@ def q4k_dequant(blocks: np.ndarray, n_out: int, n_in: int) -> np.ndarray:
 def q6k_dequant(blocks: np.ndarray, n_out: int, n_in: int) -> np.ndarray:
     out = np.empty((n_out, n_in), np.float32)
     lib().ora_q6k_dequant(_p(np.ascontiguousarray(blocks, np.uint8)), 0, n_out, n_in, _p(out))
+    return out
+
+
+def q8_0_dequant(blocks: np.ndarray, n_out: int, n_in: int) -> np.ndarray:
+    out = np.empty((n_out, n_in), np.float32)
+    lib().ora_q8_0_dequant(_p(np.ascontiguousarray(blocks, np.uint8)), 0, n_out, n_in, _p(out))
+    return out
+
+
+def q5_0_dequant(blocks: np.ndarray, n_out: int, n_in: int) -> np.ndarray:
+    out = np.empty((n_out, n_in), np.float32)
+    lib().ora_q5_0_dequant(_p(np.ascontiguousarray(blocks, np.uint8)), 0, n_out, n_in, _p(out))
     return out
 
 
@@ -343,6 +358,12 @@ class Qwen2:
 
     def tensor_ptr(self, layer: int, kind: int, part: int = 0) -> int:
         return lib().ora_qwen2_tensor(self.h, layer, kind, part)
+
+    def set_matrix(self, layer: int, kind: int, fmt: int, blocks: np.ndarray) -> None:
+        """Replace one matrix by GGML blocks (fmt 1 Q4_K, 2 Q6_K, 3 Q8_0, 4 Q5_0)."""
+        b = np.ascontiguousarray(blocks, np.uint8)
+        if lib().ora_qwen2_set_matrix(self.h, layer, kind, fmt, _p(b)):
+            raise ValueError("ora_qwen2_set_matrix rejected the matrix")
 
     def __del__(self):
         try:

@@ -33,6 +33,8 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_matrix_upload_a8": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, P(c_void_p)]),
     "pgd_matrix_upload_q4k": (c_int, [c_void_p, c_void_p, c_int, c_int, P(c_void_p)]),
     "pgd_matrix_upload_q6k": (c_int, [c_void_p, c_void_p, c_int, c_int, P(c_void_p)]),
+    "pgd_matrix_upload_q8_0": (c_int, [c_void_p, c_void_p, c_int, c_int, P(c_void_p)]),
+    "pgd_matrix_upload_q5_0": (c_int, [c_void_p, c_void_p, c_int, c_int, P(c_void_p)]),
     "pgd_matrix_synth": (c_int, [c_void_p, c_int, c_int, c_int, c_uint64, c_uint64, c_float, P(c_void_p)]),
     "pgd_matrix_free": (c_int, [c_void_p]),
     "pgd_matrix_info": (c_int, [c_void_p, P(c_int), P(c_int), P(c_int), P(c_size_t), P(c_double)]),

@@ -196,6 +196,14 @@ int pgd_matrix_upload_q6k(pgd_dev* dev, const void* blocks, int n_out, int n_in,
   return upload_kq(dev, FMT_Q6K, blocks, n_out, n_in, out);
 }
 
+int pgd_matrix_upload_q8_0(pgd_dev* dev, const void* blocks, int n_out, int n_in, pgd_matrix** out) {
+  return upload_kq(dev, FMT_Q8_0, blocks, n_out, n_in, out);
+}
+
+int pgd_matrix_upload_q5_0(pgd_dev* dev, const void* blocks, int n_out, int n_in, pgd_matrix** out) {
+  return upload_kq(dev, FMT_Q5_0, blocks, n_out, n_in, out);
+}
+
 int pgd_matrix_synth(pgd_dev* dev, int fmt, int n_out, int n_in, uint64_t seed, uint64_t key, float std,
                      pgd_matrix** out) {
   pgd_matrix* held = nullptr;

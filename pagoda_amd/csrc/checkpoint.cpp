@@ -201,7 +201,7 @@ enum GgufType {
 };
 
 // ggml tensor types the backend stores
-enum { GGML_F32 = 0, GGML_F16 = 1, GGML_Q4_K = 12, GGML_Q6_K = 14 };
+enum { GGML_F32 = 0, GGML_F16 = 1, GGML_Q5_0 = 6, GGML_Q8_0 = 8, GGML_Q4_K = 12, GGML_Q6_K = 14 };
 
 struct Cursor {
   const uint8_t* p;
@@ -330,6 +330,12 @@ GgufFile::GgufFile(const std::string& path) : file_(std::make_unique<MappedFile>
         t.dtype = in.type == GGML_Q4_K ? DType::Q4K : DType::Q6K;
         bytes = outer * (inner / 256) * (in.type == GGML_Q4_K ? 144 : 210);
         break;
+      case GGML_Q8_0:
+      case GGML_Q5_0:
+        if (inner % 32) bad(path + ": " + in.name + " rows are not whole 32-weight blocks");
+        t.dtype = in.type == GGML_Q8_0 ? DType::Q8_0 : DType::Q5_0;
+        bytes = outer * (inner / 32) * (in.type == GGML_Q8_0 ? 34 : 22);
+        break;
       default:
         // other block types are tolerated until a tensor of that type is asked for
         other_types_[in.name] = in.type;
@@ -352,7 +358,7 @@ const TensorView& GgufFile::at(const std::string& name) const {
   if (t) return *t;
   auto it = other_types_.find(name);
   if (it != other_types_.end())
-    bad(name + " has ggml type " + std::to_string(it->second) + "; the backend stores F32, F16, Q4_K and Q6_K tensors");
+    bad(name + " has ggml type " + std::to_string(it->second) + "; the backend stores F32, F16, Q4_K, Q6_K, Q8_0 and Q5_0 tensors");
   bad("missing " + name);
 }
 

@@ -35,7 +35,7 @@ class MappedFile {
 };
 
 // element types of checkpoint tensors
-enum class DType { U32, BF16, F16, F32, Q4K, Q6K };
+enum class DType { U32, BF16, F16, F32, Q4K, Q6K, Q8_0, Q5_0 };
 
 struct TensorView {
   DType dtype;

@@ -2,7 +2,7 @@
 // instantiation files (gemv_a8.hip, gemv_q4k.hip, gemv_q6k.hip).
 //
 // Dequant-in-register GEMV / skinny GEMM on the vector ALUs for GGML Q4_K /
-// Q6_K matrices (MLX affine-8 runs on the matrix cores, gemv_mma.hip).
+// Q6_K / Q8_0 / Q5_0 matrices (MLX affine-8 runs on the matrix cores, gemv_mma.hip).
 //
 // GEMV mapping (wave64): a wave owns ROWS consecutive output rows. A row is
 // cut into 16-byte chunks of its main plane (Q4K qs / Q6K ql);
@@ -235,6 +235,82 @@ struct Q6K {
   }
 };
 
+// Q8_0: chunk p = block p of the row (32 weights): weights 32p..32p+15 are
+// the low half, 32p+16..32p+31 the high half; y = q * d.
+struct Q80 {
+  struct W {
+    uint4 lo, hi;
+    float d;
+  };
+  static __device__ inline int chunks(const GemvArgs& a) { return a.nsb; }
+  static __device__ inline bool pos(const GemvArgs& a, int p, int& lo, int& hi) {
+    lo = p << 5;
+    hi = lo + 16;
+    return true;
+  }
+  static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t*, const uint8_t*,
+                                  const GemvArgs& a, int row, int p) {
+    W w;
+    const uint8_t* q = c0 + (size_t)row * a.n_in + (p << 5);
+    w.lo = *reinterpret_cast<const uint4*>(q);
+    w.hi = *reinterpret_cast<const uint4*>(q + 16);
+    w.d = f16_to_f32(reinterpret_cast<const uint16_t*>(c1)[(size_t)row * a.nsb + p]);
+    return w;
+  }
+  static __device__ inline float acc(float r, const W& w, const float* xl, const float* xh, float, float, int,
+                                     bool) {
+    float dl = 0.0f, dh = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      dl = fmaf((float)(int8_t)byte_of(w.lo, i), xl[i], dl);
+      dh = fmaf((float)(int8_t)byte_of(w.hi, i), xh[i], dh);
+    }
+    r = fmaf(w.d, dl, r);
+    return fmaf(w.d, dh, r);
+  }
+};
+
+// Q5_0: chunk p = block p of the row; qs byte j holds weight j (low nibble)
+// and weight j + 16 (high nibble), qh bit j / j + 16 their fifth bit;
+// y = (q - 16) * d.
+struct Q50 {
+  struct W {
+    uint4 q;
+    uint32_t qh;
+    float d;
+  };
+  static __device__ inline int chunks(const GemvArgs& a) { return a.nsb; }
+  static __device__ inline bool pos(const GemvArgs& a, int p, int& lo, int& hi) {
+    lo = p << 5;
+    hi = lo + 16;
+    return true;
+  }
+  static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t* c2, const uint8_t*,
+                                  const GemvArgs& a, int row, int p) {
+    W w;
+    const size_t b = (size_t)row * a.nsb + p;
+    w.q = *reinterpret_cast<const uint4*>(c0 + b * 16);
+    w.qh = reinterpret_cast<const uint32_t*>(c1)[b];
+    w.d = f16_to_f32(reinterpret_cast<const uint16_t*>(c2)[b]);
+    return w;
+  }
+  static __device__ inline float acc(float r, const W& w, const float* xl, const float* xh, float sl, float sh, int,
+                                     bool) {
+    float dl = 0.0f, dh = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t b = byte_of(w.q, i);
+      const uint32_t ql = (b & 15u) | (((w.qh >> i) & 1u) << 4);
+      const uint32_t qh = (b >> 4) | (((w.qh >> (i + 16)) & 1u) << 4);
+      dl = fmaf((float)ql, xl[i], dl);
+      dh = fmaf((float)qh, xh[i], dh);
+    }
+    // sum (q - 16) x = sum q x - 16 sum x
+    r = fmaf(w.d, fmaf(-16.0f, sl, dl), r);
+    return fmaf(w.d, fmaf(-16.0f, sh, dh), r);
+  }
+};
+
 template <class F>
 struct Acc {
   template <class W>
@@ -345,6 +421,8 @@ void launch_rows(GemvArgs a, int nrows, hipStream_t s) {
 // entry points of the instantiation files
 void run_q4k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 void run_q6k(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
+void run_q80(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
+void run_q50(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 // Q4K on the matrix cores (n_in % 64 == 0)
 bool q4k_mma_ok(const GemvArgs& a);
 void run_q4k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);

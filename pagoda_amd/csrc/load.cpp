@@ -126,7 +126,7 @@ class MlxSource : public WeightSource {
 };
 
 // ---------------------------------------------------------------------------
-// Qwen2 GGUF (qwen2_gguf.rs:88-124): Q4_K / Q6_K matrices, F32 / F16 vectors;
+// Qwen2 GGUF (qwen2_gguf.rs:88-124): Q4_K / Q6_K / Q8_0 / Q5_0 matrices, F32 / F16 vectors;
 // lm_head is output.weight, else the embedding (qwen2_gguf.rs:96-99)
 // ---------------------------------------------------------------------------
 class GgufSource : public WeightSource {
@@ -139,10 +139,17 @@ class GgufSource : public WeightSource {
     (void)fmt;
     const std::string nm = name(li, kind);
     const TensorView& t = f_.at(nm);
-    if (t.dtype != DType::Q4K && t.dtype != DType::Q6K) bad(nm + " must be Q4_K or Q6_K");
+    int f;
+    switch (t.dtype) {
+      case DType::Q4K: f = FMT_Q4K; break;
+      case DType::Q6K: f = FMT_Q6K; break;
+      case DType::Q8_0: f = FMT_Q8_0; break;
+      case DType::Q5_0: f = FMT_Q5_0; break;
+      default: bad(nm + " must be Q4_K, Q6_K, Q8_0 or Q5_0");
+    }
     if (t.shape.size() != 2 || t.shape[0] != (uint64_t)n_out || t.shape[1] != (uint64_t)n_in)
       bad(nm + ": expected " + std::to_string(n_out) + " x " + std::to_string(n_in));
-    qmat_alloc(q, t.dtype == DType::Q4K ? FMT_Q4K : FMT_Q6K, n_out, n_in, s);
+    qmat_alloc(q, f, n_out, n_in, s);
     qmat_upload_kq(q, t.data, s);
   }
 

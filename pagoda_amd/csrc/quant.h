@@ -25,17 +25,21 @@
 
 namespace pgd {
 
-enum Fmt : int { FMT_A8 = 0, FMT_Q4K = 1, FMT_Q6K = 2 };
+enum Fmt : int { FMT_A8 = 0, FMT_Q4K = 1, FMT_Q6K = 2, FMT_Q8_0 = 3, FMT_Q5_0 = 4 };
+
+// GGML 32-weight block formats (row-major planes, block b of row r at r * nsb + b)
+constexpr int kQ8_0Bytes = 34, kQ5_0Bytes = 22;
 
 struct QMat {
   int fmt = FMT_A8;
+  // nsb: 256-weight super-blocks per row (Q4K / Q6K), 32-weight blocks per row (Q8_0 / Q5_0)
   int n_out = 0, n_in = 0, nsb = 0;
   uint8_t* base = nullptr;  // owning device allocation
   size_t bytes = 0;
   // plane pointers (into base)
-  uint8_t* p0 = nullptr;  // A8 codes | Q4K qs | Q6K ql
-  uint8_t* p1 = nullptr;  // A8 sb    | Q4K hdr | Q6K qh
-  uint8_t* p2 = nullptr;  //                      Q6K sc
+  uint8_t* p0 = nullptr;  // A8 codes | Q4K qs | Q6K ql | Q8_0 int8 q [n_out][n_in] | Q5_0 qs [n_out][n_in / 2]
+  uint8_t* p1 = nullptr;  // A8 sb    | Q4K hdr | Q6K qh | Q8_0 f16 d [n_out][nsb] | Q5_0 u32 qh [n_out][nsb]
+  uint8_t* p2 = nullptr;  //                      Q6K sc |                        | Q5_0 f16 d [n_out][nsb]
   uint8_t* p3 = nullptr;  //                      Q6K d
 };
 

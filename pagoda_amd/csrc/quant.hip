@@ -32,6 +32,8 @@ void run_fmt(const QMat& m, const GemvArgs& a, int nrows, int x_f16, int epi, hi
       if (q6k_mma_ok(a, epi)) run_q6k_mma(a, nrows, x_f16, epi, s);
       else run_q6k(a, nrows, x_f16, epi, s);
       break;
+    case FMT_Q8_0: run_q80(a, nrows, x_f16, epi, s); break;
+    case FMT_Q5_0: run_q50(a, nrows, x_f16, epi, s); break;
     default: throw Error{kErrFormat, "unknown matrix format"};
   }
 }
@@ -128,9 +130,46 @@ __global__ void dequant_q6k_kernel(const uint8_t* qlp, const uint8_t* qhp, const
   }
 }
 
+// Q8_0 / Q5_0: one thread per 16-weight half block; y = q * d (GGML order)
+__global__ void dequant_q80_kernel(const int8_t* q, const uint16_t* dp, int n_in, int nsb, int row0, int rows,
+                                   const uint32_t* ids, float* out, int ldo) {
+  size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int runs = nsb * 2;
+  if (t >= (size_t)rows * runs) return;
+  const int r = (int)(t / runs), c = (int)(t % runs);
+  const int row = ids ? (int)ids[r] : row0 + r;
+  const float d = f16_to_f32(dp[(size_t)row * nsb + (c >> 1)]);
+  const int8_t* src = q + (size_t)row * n_in + 16 * c;
+  float* o = out + (size_t)r * ldo + 16 * c;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = (float)src[i] * d;
+}
+
+__global__ void dequant_q50_kernel(const uint8_t* qs, const uint32_t* qhp, const uint16_t* dp, int n_in, int nsb,
+                                   int row0, int rows, const uint32_t* ids, float* out, int ldo) {
+  size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int runs = nsb * 2;
+  if (t >= (size_t)rows * runs) return;
+  const int r = (int)(t / runs), c = (int)(t % runs), b = c >> 1, h = c & 1;
+  const int row = ids ? (int)ids[r] : row0 + r;
+  const size_t bi = (size_t)row * nsb + b;
+  const float d = f16_to_f32(dp[bi]);
+  const uint32_t qh = qhp[bi];
+  const uint8_t* src = qs + bi * 16;
+  float* o = out + (size_t)r * ldo + 32 * b + 16 * h;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t nib = h ? (uint32_t)(src[j] >> 4) : (uint32_t)(src[j] & 15u);
+    const int qv = (int)(nib | (((qh >> (j + 16 * h)) & 1u) << 4)) - 16;
+    o[j] = (float)qv * d;
+  }
+}
+
 void launch_dequant(const QMat& m, int row0, int rows, const uint32_t* ids, float* out, int ldo, hipStream_t s) {
   if (rows <= 0) return;
-  size_t runs = m.fmt == FMT_A8 ? (size_t)(m.n_in >> 4) : (size_t)m.nsb * 8;
+  size_t runs = m.fmt == FMT_A8                                ? (size_t)(m.n_in >> 4)
+                : (m.fmt == FMT_Q8_0 || m.fmt == FMT_Q5_0) ? (size_t)m.nsb * 2
+                                                             : (size_t)m.nsb * 8;
   size_t n = runs * rows;
   int blocks = (int)((n + 255) / 256);
   switch (m.fmt) {
@@ -145,6 +184,15 @@ void launch_dequant(const QMat& m, int row0, int rows, const uint32_t* ids, floa
     case FMT_Q6K:
       hipLaunchKernelGGL(dequant_q6k_kernel, dim3(blocks), dim3(256), 0, s, m.p0, m.p1,
                          reinterpret_cast<const int8_t*>(m.p2), reinterpret_cast<const uint16_t*>(m.p3), m.n_in,
+                         m.nsb, row0, rows, ids, out, ldo);
+      break;
+    case FMT_Q8_0:
+      hipLaunchKernelGGL(dequant_q80_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<const int8_t*>(m.p0),
+                         reinterpret_cast<const uint16_t*>(m.p1), m.n_in, m.nsb, row0, rows, ids, out, ldo);
+      break;
+    case FMT_Q5_0:
+      hipLaunchKernelGGL(dequant_q50_kernel, dim3(blocks), dim3(256), 0, s, m.p0,
+                         reinterpret_cast<const uint32_t*>(m.p1), reinterpret_cast<const uint16_t*>(m.p2), m.n_in,
                          m.nsb, row0, rows, ids, out, ldo);
       break;
     default: throw Error{kErrFormat, "unknown matrix format"};
@@ -389,6 +437,8 @@ double qmat_algo_bytes(const QMat& m) {
     case FMT_A8: return n * 8.5 / 8.0;
     case FMT_Q4K: return n * 4.5 / 8.0;
     case FMT_Q6K: return n * 6.5625 / 8.0;
+    case FMT_Q8_0: return n * 8.5 / 8.0;
+    case FMT_Q5_0: return n * 5.5 / 8.0;
   }
   return 0.0;
 }
@@ -398,7 +448,7 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s) {
   m.fmt = fmt;
   m.n_out = n_out;
   m.n_in = n_in;
-  m.nsb = (n_in + 255) / 256;
+  m.nsb = (fmt == FMT_Q8_0 || fmt == FMT_Q5_0) ? n_in / 32 : (n_in + 255) / 256;
   size_t rows = (size_t)n_out;
   size_t off[4] = {0, 0, 0, 0};
   size_t total = 0;
@@ -424,6 +474,15 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s) {
     place(1, tiles * m.nsb * 2048);
     place(2, tiles * m.nsb * 512);
     place(3, tiles * m.nsb * 64);
+  } else if (fmt == FMT_Q8_0) {
+    PGD_CHECK(n_in % 32 == 0, kErrShape, "Q8_0 n_in must be a multiple of 32");
+    place(0, rows * n_in);
+    place(1, rows * m.nsb * 2);
+  } else if (fmt == FMT_Q5_0) {
+    PGD_CHECK(n_in % 32 == 0, kErrShape, "Q5_0 n_in must be a multiple of 32");
+    place(0, rows * n_in / 2);
+    place(1, rows * m.nsb * 4);
+    place(2, rows * m.nsb * 2);
   } else {
     throw Error{kErrFormat, "unknown matrix format"};
   }
@@ -434,7 +493,7 @@ void qmat_alloc(QMat& m, int fmt, int n_out, int n_in, hipStream_t s) {
   m.bytes = total;
   m.p0 = m.base + off[0];
   m.p1 = m.base + off[1];
-  m.p2 = fmt == FMT_Q6K ? m.base + off[2] : nullptr;
+  m.p2 = (fmt == FMT_Q6K || fmt == FMT_Q5_0) ? m.base + off[2] : nullptr;
   m.p3 = fmt == FMT_Q6K ? m.base + off[3] : nullptr;
   // zero the padding rows of the last tile, ordered before the writes that
   // follow on the same stream
@@ -501,8 +560,32 @@ void qmat_upload_kq(QMat& m, const uint8_t* blocks, hipStream_t s) {
     PGD_HIP(hipMemcpyAsync(m.p2, sc.data(), sc.size(), hipMemcpyHostToDevice, s));
     PGD_HIP(hipMemcpyAsync(m.p3, d.data(), d.size() * 2, hipMemcpyHostToDevice, s));
     PGD_HIP(hipStreamSynchronize(s));
+  } else if (m.fmt == FMT_Q8_0 || m.fmt == FMT_Q5_0) {
+    // GGML blocks (row-major) -> row-major planes: quants, (Q5_0: high bits), scales
+    const bool q8 = m.fmt == FMT_Q8_0;
+    const size_t nbk = (size_t)m.n_out * m.nsb, qb = q8 ? 32 : 16;
+    std::vector<uint8_t> q(nbk * qb), qh(q8 ? 0 : nbk * 4);
+    std::vector<uint16_t> d(nbk);
+    for (size_t i = 0; i < nbk; ++i) {
+      const uint8_t* b = blocks + i * (q8 ? kQ8_0Bytes : kQ5_0Bytes);
+      d[i] = (uint16_t)(b[0] | (b[1] << 8));
+      if (q8) {
+        std::copy(b + 2, b + 34, q.data() + i * 32);
+      } else {
+        std::copy(b + 2, b + 6, qh.data() + i * 4);
+        std::copy(b + 6, b + 22, q.data() + i * 16);
+      }
+    }
+    PGD_HIP(hipMemcpyAsync(m.p0, q.data(), q.size(), hipMemcpyHostToDevice, s));
+    if (q8) {
+      PGD_HIP(hipMemcpyAsync(m.p1, d.data(), d.size() * 2, hipMemcpyHostToDevice, s));
+    } else {
+      PGD_HIP(hipMemcpyAsync(m.p1, qh.data(), qh.size(), hipMemcpyHostToDevice, s));
+      PGD_HIP(hipMemcpyAsync(m.p2, d.data(), d.size() * 2, hipMemcpyHostToDevice, s));
+    }
+    PGD_HIP(hipStreamSynchronize(s));
   } else {
-    throw Error{kErrFormat, "k-quant upload on a non k-quant matrix"};
+    throw Error{kErrFormat, "block upload on an A8 matrix"};
   }
 }
 
@@ -607,11 +690,13 @@ void qmat_synth(QMat& m, uint64_t seed, uint64_t key, float std, hipStream_t s) 
     size_t n = (size_t)m.n_out * m.nsb;
     hipLaunchKernelGGL(synth_q4k_kernel, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, s, m.p0,
                        reinterpret_cast<uint4*>(m.p1), m.n_out, m.n_in, m.nsb, stream, std);
-  } else {
+  } else if (m.fmt == FMT_Q6K) {
     size_t n = (size_t)m.n_out * m.nsb;
     hipLaunchKernelGGL(synth_q6k_kernel, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, s, m.p0, m.p1,
                        reinterpret_cast<int8_t*>(m.p2), reinterpret_cast<uint16_t*>(m.p3), m.n_out, m.n_in, m.nsb,
                        stream, std);
+  } else {
+    throw Error{kErrFormat, "no synthetic generator for this format"};
   }
   PGD_HIP(hipGetLastError());
 }

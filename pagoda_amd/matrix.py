@@ -8,8 +8,8 @@ import numpy as np
 from ._lib import call
 from .device import Device
 
-FMT_A8, FMT_Q4K, FMT_Q6K = 0, 1, 2
-FMT_NAMES = {FMT_A8: "a8", FMT_Q4K: "q4k", FMT_Q6K: "q6k"}
+FMT_A8, FMT_Q4K, FMT_Q6K, FMT_Q8_0, FMT_Q5_0 = 0, 1, 2, 3, 4
+FMT_NAMES = {FMT_A8: "a8", FMT_Q4K: "q4k", FMT_Q6K: "q6k", FMT_Q8_0: "q8_0", FMT_Q5_0: "q5_0"}
 
 
 def _ptr(a: np.ndarray) -> C.c_void_p:
@@ -49,11 +49,15 @@ class Matrix:
 
     @classmethod
     def upload_kq(cls, dev: Device, fmt: int, blocks: np.ndarray, n_out: int, n_in: int):
+        """GGML blocks, row-major: Q4_K / Q6_K super-blocks or Q8_0 / Q5_0 blocks."""
         blocks = np.ascontiguousarray(blocks, np.uint8)
-        per = 144 if fmt == FMT_Q4K else 210
-        assert blocks.size == n_out * ((n_in + 255) // 256) * per
+        if fmt in (FMT_Q8_0, FMT_Q5_0):
+            assert blocks.size == n_out * (n_in // 32) * (34 if fmt == FMT_Q8_0 else 22)
+        else:
+            assert blocks.size == n_out * ((n_in + 255) // 256) * (144 if fmt == FMT_Q4K else 210)
         h = C.c_void_p()
-        name = "pgd_matrix_upload_q4k" if fmt == FMT_Q4K else "pgd_matrix_upload_q6k"
+        name = {FMT_Q4K: "pgd_matrix_upload_q4k", FMT_Q6K: "pgd_matrix_upload_q6k", FMT_Q8_0: "pgd_matrix_upload_q8_0",
+                FMT_Q5_0: "pgd_matrix_upload_q5_0"}[fmt]
         call(name, dev.handle, _ptr(blocks), n_out, n_in, C.byref(h))
         return cls(dev, h)
 

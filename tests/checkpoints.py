@@ -154,7 +154,7 @@ def perturb_norms_qwen35(cfg, oracle, rng) -> None:
 # GGUF
 # ---------------------------------------------------------------------------
 G_U32, G_I32, G_F32, G_STR, G_ARR = 4, 5, 6, 8, 9
-GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 8, 12, 14
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K = 0, 1, 2, 6, 8, 12, 14
 
 
 def _gstr(s: str) -> bytes:
@@ -211,16 +211,24 @@ def qwen2_meta(cfg, arch="qwen2") -> list:
             ("tokenizer.ggml.token_type", G_ARR, (G_I32, [1, 1, 3]))]
 
 
-def gguf_tensors_from_oracle(cfg, oracle, untied: bool = False) -> list:
-    """Qwen2 tensors in the oracle's formats (Q6_K embedding, attn_v and even
-    ffn_down; Q4_K elsewhere; F32 norms and biases)."""
+BLOCK_BYTES = {GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210), GGML_Q8_0: (32, 34), GGML_Q5_0: (32, 22)}
+ORACLE_FMT = {GGML_Q4_K: 1, GGML_Q6_K: 2, GGML_Q8_0: 3, GGML_Q5_0: 4}
+
+
+def gguf_tensors_from_oracle(cfg, oracle, untied: bool = False, types=None) -> list:
+    """Qwen2 tensors as the oracle holds them: by default its synthetic
+    formats (Q6_K embedding, attn_v and even ffn_down; Q4_K elsewhere);
+    types[(layer, kind)] names another ggml type for a matrix the oracle
+    holds in that type (ora.Qwen2.set_matrix). Norms and biases F32."""
     H, kvw = cfg.hidden, cfg.kv_heads * cfg.head_dim
+    types = types or {}
     out = []
 
     def mat(name, layer, kind, n_out, n_in, q6):
-        nb = n_out * (n_in // 256) * (210 if q6 else 144)
-        raw = host_array(oracle.tensor_ptr(layer, kind), C.c_uint8, nb).tobytes()
-        out.append((name, GGML_Q6_K if q6 else GGML_Q4_K, (n_in, n_out), raw))
+        gt = types.get((layer, kind), GGML_Q6_K if q6 else GGML_Q4_K)
+        per, nbytes = BLOCK_BYTES[gt]
+        raw = host_array(oracle.tensor_ptr(layer, kind), C.c_uint8, n_out * (n_in // per) * nbytes).tobytes()
+        out.append((name, gt, (n_in, n_out), raw))
 
     def vec(name, layer, kind, n):
         out.append((name, GGML_F32, (n,), host_array(oracle.tensor_ptr(layer, kind), C.c_float, n).tobytes()))
@@ -244,6 +252,18 @@ def gguf_tensors_from_oracle(cfg, oracle, untied: bool = False) -> list:
         mat(p + ".ffn_up.weight", i, K_UP, cfg.intermediate, H, False)
         mat(p + ".ffn_down.weight", i, K_DOWN, H, cfg.intermediate, i % 2 == 0)
     return out
+
+
+def random_blocks(rng, ggml_type: int, n_out: int, n_in: int, d_std: float = 5e-4) -> np.ndarray:
+    """Random Q8_0 / Q5_0 blocks: f16 scales N(0, d_std), uniform quants."""
+    nb = n_out * n_in // 32
+    d = rng.normal(0, d_std, nb).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    if ggml_type == GGML_Q8_0:
+        q = rng.integers(0, 256, (nb, 32), dtype=np.uint8)
+        return np.concatenate([d, q], axis=1).reshape(-1)
+    qh = rng.integers(0, 256, (nb, 4), dtype=np.uint8)
+    qs = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+    return np.concatenate([d, qh, qs], axis=1).reshape(-1)
 
 
 def perturb_norms_qwen2(cfg, oracle, rng) -> None:

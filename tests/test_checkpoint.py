@@ -7,7 +7,7 @@ import struct
 import numpy as np
 import pytest
 
-from checkpoints import (G_F32, G_STR, G_U32, GGML_F32, GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, mlx_text_config,
+from checkpoints import (G_F32, G_STR, G_U32, GGML_F32, GGML_Q4_0, GGML_Q4_K, GGML_Q6_K, mlx_text_config,
                          qwen2_meta, write_gguf, write_mlx_config, write_safetensors_shards)
 
 
@@ -114,7 +114,7 @@ def gguf_file(tmp_path, meta=None, emb_type=GGML_Q6_K, emb_ne=None, corrupt=None
     _, q2 = cfgs()
     emb_ne = emb_ne or (q2.hidden, q2.vocab)
     nb = emb_ne[1] * (emb_ne[0] // 256)
-    emb_bytes = {GGML_Q6_K: 210 * nb, GGML_Q4_K: 144 * nb, GGML_Q8_0: 34 * emb_ne[1] * (emb_ne[0] // 32)}[emb_type]
+    emb_bytes = {GGML_Q6_K: 210 * nb, GGML_Q4_K: 144 * nb, GGML_Q4_0: 18 * emb_ne[1] * (emb_ne[0] // 32)}[emb_type]
     tensors = [("token_embd.weight", emb_type, emb_ne, bytes(emb_bytes)),
                ("output_norm.weight", GGML_F32, (q2.hidden,), np.ones(q2.hidden, np.float32).tobytes()),
                ("blk.0.ffn_gate.weight", GGML_Q4_K, (q2.hidden, q2.intermediate),
@@ -144,7 +144,7 @@ def test_gguf_config_defaults(tmp_path):
     ("magic", "not a GGUF file"),
     ("version", "GGUF version 1"),
     ("truncated", "truncated"),
-    ("q8_0", "token_embd.weight has ggml type 8"),
+    ("q4_0", "token_embd.weight has ggml type 2"),
     ("ragged", "super-blocks"),
     ("range", "out of range"),
     ("heads", "head_count_kv"),
@@ -161,8 +161,8 @@ def test_gguf_errors(tmp_path, case, fragment):
         kw["corrupt"] = lambda b: b[:4] + struct.pack("<I", 1) + b[8:]
     elif case == "truncated":
         kw["corrupt"] = lambda b: b[:200]
-    elif case == "q8_0":
-        kw["emb_type"] = GGML_Q8_0
+    elif case == "q4_0":
+        kw["emb_type"] = GGML_Q4_0
     elif case == "ragged":
         kw["emb_type"], kw["emb_ne"] = GGML_Q4_K, (96, q2.vocab)
     elif case == "range":

@@ -198,3 +198,39 @@ def test_synth_normal_moments_and_determinism():
     assert not np.array_equal(a[:1000], c)
     # Irwin-Hall values are k / 65536 exactly
     assert np.all(a[:1000] * 65536 == np.round(a[:1000] * 65536))
+
+
+# ------------------------------------------------ GGML 32-weight blocks
+def q8_0_block(d: float, q) -> bytes:
+    return np.float16(d).tobytes() + np.asarray(q, np.int8).tobytes()
+
+
+def q5_0_block(d: float, qh: int, qs) -> bytes:
+    return np.float16(d).tobytes() + int(qh).to_bytes(4, "little") + np.asarray(qs, np.uint8).tobytes()
+
+
+def test_q8_0_known_answers():
+    # q = 4j - 64 at d = 1/4 gives j - 16; the extremes at d = 2 give 254 / -256
+    b0 = q8_0_block(0.25, [4 * j - 64 for j in range(32)])
+    b1 = q8_0_block(2.0, [127, -128] * 16)
+    got = ora.q8_0_dequant(np.frombuffer(b0 + b1, np.uint8), 1, 64)
+    np.testing.assert_array_equal(got[0, :32], np.arange(32, dtype=np.float32) - 16)
+    np.testing.assert_array_equal(got[0, 32:], np.array([254.0, -256.0] * 16, np.float32))
+
+
+def test_q5_0_known_answers():
+    j = np.arange(16)
+    # qs byte j holds weight j (low nibble) and weight j + 16 (high nibble);
+    # qh bit j / j + 16 is their fifth bit: weights 0..31 become q = 0..31,
+    # value q - 16
+    b0 = q5_0_block(1.0, 0xFFFF0000, j | (j << 4))
+    # fifth bits only on the low half: weights j -> 31 - j, j + 16 -> 0,
+    # at d = -1/2
+    b1 = q5_0_block(-0.5, 0x0000FFFF, 15 - j)
+    got = ora.q5_0_dequant(np.frombuffer(b0 + b1, np.uint8), 1, 64)
+    np.testing.assert_array_equal(got[0, :32], np.arange(32, dtype=np.float32) - 16)
+    want = np.concatenate([(15 - j).astype(np.float32) * -0.5, np.full(16, 8.0, np.float32)])
+    np.testing.assert_array_equal(got[0, 32:], want)
+    # rows are consecutive runs of blocks
+    two = ora.q5_0_dequant(np.frombuffer(b1 + b0, np.uint8), 2, 32)
+    np.testing.assert_array_equal(two[1], got[0, :32])
