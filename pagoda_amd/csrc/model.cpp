@@ -499,26 +499,15 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       // stacked rows: [qkv (conv_dim) | z (value_dim) | b (v_heads) | a (v_heads)]
       const float* P = w.A;
       const int ldp = (int)w.lda;
+      conv_step(P, ldp, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb, (size_t)L.lin_index * per_lin, sm,
+                nseq, st);
       GdnParams gp{};
       gp.k_heads = c.k_heads;
       gp.v_heads = c.v_heads;
       gp.k_dim = c.k_dim;
       gp.v_dim = c.v_dim;
-      if (c.v_heads == 2 * c.k_heads && c.conv_kernel <= 4 && c.k_heads * nseq <= 256) {
-        // the recurrence kernel runs the causal conv on the raw columns itself;
-        // its two-head workgroups fit one CU each, so only while the grid fits
-        // the GPU in one round (more sequences: separate conv, one head each)
-        gp.conv_out = P;
-        gp.ld_conv = ldp;
-        gp.conv_w = L.conv;
-        gp.conv_kernel = c.conv_kernel;
-        gp.conv_state_off = (size_t)L.lin_index * per_lin;
-      } else {
-        conv_step(P, ldp, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb, (size_t)L.lin_index * per_lin,
-                  sm, nseq, st);
-        gp.conv_out = w.D;
-        gp.ld_conv = (int)w.ldd;
-      }
+      gp.conv_out = w.D;
+      gp.ld_conv = (int)w.ldd;
       gp.z = P + m.conv_dim;
       gp.ld_z = ldp;
       gp.b = P + m.conv_dim + m.value_dim;

@@ -48,13 +48,6 @@ struct GdnParams {
   a8act::Dst act;        // the same output as prepared A8 activations (XA null: no)
   float* const* state_base;  // per sequence; state at state_base[s] + state_off, [v_heads, k_dim, v_dim]
   size_t state_off;
-  // optional fused causal conv (conv_step's arithmetic): conv_out then holds the
-  // raw q | k | v columns; weights [channels, conv_kernel], conv state at
-  // state_base[s] + conv_state_off, [channels, conv_kernel - 1]. Null: conv_out
-  // is the conv output already. Needs v_heads == 2 * k_heads and conv_kernel <= 4.
-  const float* conv_w;
-  int conv_kernel;
-  size_t conv_state_off;
 };
 
 // Gated-DeltaNet recurrence over each sequence's rows in order

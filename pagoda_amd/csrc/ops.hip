@@ -76,69 +76,28 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // Gated-DeltaNet
 // ---------------------------------------------------------------------------
-// NH value heads per workgroup, 256 threads each (NH = 1: one workgroup per
-// (value head, sequence); NH = v_heads / k_heads: the value heads that share a
-// key head). Thread (rg, cg) of a head holds state rows 16rg..16rg+15, columns
-// 4cg..4cg+3 in 64 registers for the whole sequence chunk. Column sums over
-// rows (S^T k, S^T q) are folded through LDS across the 8 row groups.
-//
-// CONV: the inputs are the in-projection's raw q | k | v columns and the
-// causal conv + SiLU (the conv_step_kernel arithmetic) runs here: thread t of
-// a head convolves q/k channel t of the key head and, for t < 128, value
-// channel t of its head. Every value head of the key head is in this
-// workgroup, so the shared q/k conv state is read once per head at the start
-// and written back once, by the first head's threads, after a barrier.
+// One workgroup per (value head, sequence); 256 threads. Thread (rg, cg)
+// holds state rows 16rg..16rg+15, columns 4cg..4cg+3 in 64 registers for the
+// whole sequence chunk. Column sums over rows (S^T k, S^T q) are folded
+// through LDS across the 8 row groups.
 __device__ inline float softplus_f(float x) {
   if (x > 20.0f) return x;
   if (x < -20.0f) return expf(x);
   return logf(1.0f + expf(x));
 }
 
-constexpr int kConvMax = 4;  // fused conv widths (taps)
-
-template <int NH, bool CONV>
-__global__ __launch_bounds__(256 * NH) void gdn_kernel(GdnParams p, const int* row_start, const int* row_count) {
+__global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_start, const int* row_count) {
   constexpr int D = 128;
-  __shared__ float qs_[NH][D], ks_[NH][D], delta_[NH][D];
-  __shared__ float red_[NH][8][D];
-  __shared__ float part_[NH][4];
-  __shared__ float obuf_[NH][D];
-  const int hh = threadIdx.x >> 8, tid = threadIdx.x & 255, s = blockIdx.y;
-  const int h = blockIdx.x * NH + hh;
-  float* qs = qs_[hh];
-  float* ks = ks_[hh];
-  float* delta = delta_[hh];
-  float(*red)[D] = red_[hh];
-  float* part = part_[hh];
-  float* obuf = obuf_[hh];
+  __shared__ float qs[D], ks[D], delta[D];
+  __shared__ float red[8][D];
+  __shared__ float part[4];
+  __shared__ float obuf[D];
+  const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
   const int cg = tid & 31, rg = tid >> 5;
   const int repeat = p.v_heads / p.k_heads;
   const int kh = h / repeat;
   const int key_dim = p.k_heads * D;
   float* st = p.state_base[s] + p.state_off + (size_t)h * D * D;
-  // conv channels of this thread: q/k channel of the key head, value channel
-  const int cqk = tid < D ? kh * D + tid : key_dim + kh * D + (tid - D);
-  const int cv_ch = 2 * key_dim + h * D + tid;
-  const int hist = CONV ? p.conv_kernel - 1 : 0;
-  float wq[kConvMax - 1], wv[kConvMax - 1], tq[kConvMax], tv[kConvMax];
-  float* cst = CONV ? p.state_base[s] + p.conv_state_off : nullptr;
-  if constexpr (CONV) {
-    for (int k = 0; k < hist; ++k) wq[k] = cst[(size_t)cqk * hist + k];
-    for (int k = 0; k <= hist; ++k) tq[k] = p.conv_w[(size_t)cqk * p.conv_kernel + k];
-    if (tid < D) {
-      for (int k = 0; k < hist; ++k) wv[k] = cst[(size_t)cv_ch * hist + k];
-      for (int k = 0; k <= hist; ++k) tv[k] = p.conv_w[(size_t)cv_ch * p.conv_kernel + k];
-    }
-  }
-  // one conv output (conv_step_kernel's order); shifts the window
-  auto conv1 = [&](float* win, const float* wt, float xv) {
-    float acc = 0.0f;
-    for (int k = 0; k < hist; ++k) acc += win[k] * wt[k];
-    acc += xv * wt[hist];
-    for (int k = 0; k + 1 < hist; ++k) win[k] = win[k + 1];
-    if (hist > 0) win[hist - 1] = xv;
-    return acc / (1.0f + expf(-acc));
-  };
   float S[16][4];
 #pragma unroll
   for (int ii = 0; ii < 16; ++ii) {
@@ -158,13 +117,9 @@ __global__ __launch_bounds__(256 * NH) void gdn_kernel(GdnParams p, const int* r
     const int row = r0 + t;
     const float* cv = p.conv_out + (size_t)row * p.ld_conv;
     const float zg = tid < D ? p.z[(size_t)row * p.ld_z + h * D + tid] : 0.0f;
-    float vv = tid < D ? cv[cv_ch] : 0.0f;
+    const float vv = tid < D ? cv[2 * key_dim + h * D + tid] : 0.0f;
     // q (threads 0..127) and k (128..255), L2-normalized per head
-    float v = cv[cqk];
-    if constexpr (CONV) {
-      v = conv1(wq, tq, v);
-      if (tid < D) vv = conv1(wv, tv, vv);
-    }
+    float v = tid < D ? cv[kh * D + tid] : cv[key_dim + kh * D + (tid - D)];
     float ss = wave_sum(v * v);
     if ((tid & 63) == 0) part[tid >> 6] = ss;
     __syncthreads();
@@ -245,14 +200,6 @@ __global__ __launch_bounds__(256 * NH) void gdn_kernel(GdnParams p, const int* r
 #pragma unroll
   for (int ii = 0; ii < 16; ++ii)
     *reinterpret_cast<float4*>(st + (size_t)(16 * rg + ii) * D + 4 * cg) = make_float4(S[ii][0], S[ii][1], S[ii][2], S[ii][3]);
-  if constexpr (CONV) {
-    // every head read the q/k window at the start (barriers since); the
-    // first head writes it back
-    if (hh == 0)
-      for (int k = 0; k < hist; ++k) cst[(size_t)cqk * hist + k] = wq[k];
-    if (tid < D)
-      for (int k = 0; k < hist; ++k) cst[(size_t)cv_ch * hist + k] = wv[k];
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -436,16 +383,7 @@ void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, hipStream_t s) {
   PGD_CHECK(p.k_dim == 128 && p.v_dim == 128, kErrShape, "gated delta kernel needs k_dim == v_dim == 128");
   PGD_CHECK(p.k_heads > 0 && p.v_heads % p.k_heads == 0, kErrShape, "v_heads must be a multiple of k_heads");
   if (nseq <= 0) return;
-  if (p.conv_w) {
-    // conv fused: one workgroup holds every value head of a key head
-    PGD_CHECK(p.conv_kernel >= 1 && p.conv_kernel <= kConvMax, kErrShape, "fused conv kernel must be in 1..4");
-    PGD_CHECK(p.v_heads == 2 * p.k_heads, kErrShape, "fused conv + gated delta needs two value heads per key head");
-    hipLaunchKernelGGL((gdn_kernel<2, true>), dim3(p.k_heads, nseq), dim3(512), 0, s, p, meta.row_start,
-                       meta.row_count);
-  } else {
-    hipLaunchKernelGGL((gdn_kernel<1, false>), dim3(p.v_heads, nseq), dim3(256), 0, s, p, meta.row_start,
-                       meta.row_count);
-  }
+  hipLaunchKernelGGL(gdn_kernel, dim3(p.v_heads, nseq), dim3(256), 0, s, p, meta.row_start, meta.row_count);
   PGD_HIP(hipGetLastError());
 }
 

@@ -129,39 +129,6 @@ def test_ragged_batch_bitwise_equals_serial(which, request):
     assert [s.context_len() for s in batched] == [s.context_len() for s in serial]
 
 
-def test_fused_and_separate_conv_paths_bitwise_equal(dev):
-    """The causal conv runs inside the recurrence kernel while k_heads x
-    sequences <= 256 workgroups, and as its own kernel for larger steps; both
-    keep conv_step's arithmetic. 20 sequences of 16 key heads take the
-    separate conv batched and the fused one serially; 8-token prompts keep
-    every GEMV launch in the 5..32-row class, so logits are bitwise equal."""
-    from pagoda_amd.engine import Model
-
-    cfg = small35(n_layers=4, k_heads=16, v_heads=32)
-    model = Model.synth(dev, cfg, 21)
-    sessions = []
-    try:
-        rng = np.random.default_rng(8)
-        prompts = [rng.integers(0, cfg.vocab, 8) for _ in range(20)]
-        serial = [model.new_session() for _ in prompts]
-        batched = [model.new_session() for _ in prompts]
-        sessions = serial + batched
-        ser = [s.forward(p) for s, p in zip(serial, prompts)]
-        _, bl = model.step_ragged(batched, prompts, want_logits=True)
-        for i in range(len(prompts)):
-            np.testing.assert_array_equal(bl[i].view(np.uint32), ser[i].view(np.uint32))
-        # one more decode row each: batched (separate) vs serial (fused), state carried
-        feeds = [[int(np.argmax(x))] * 5 for x in ser]
-        ser = [s.forward(f) for s, f in zip(serial, feeds)]
-        _, bl = model.step_ragged(batched, feeds, want_logits=True)
-        for i in range(len(prompts)):
-            np.testing.assert_array_equal(bl[i].view(np.uint32), ser[i].view(np.uint32))
-    finally:
-        for x in sessions:
-            x.free()
-        model.free()
-
-
 def test_verify_equals_serial_greedy(m35):
     """forward_verify(4) == 4 serial greedy steps (pagoda-hf/examples/qwen3_8.rs:219-247)."""
     model, _ = m35
