@@ -34,6 +34,17 @@ std::string read_text(const std::string& path) {
   return ss.str();
 }
 
+// element count of a shape, rejecting products past 2^48 (no file holds more;
+// this keeps every byte count below computed exactly in 64 bits)
+uint64_t checked_numel(const std::vector<uint64_t>& shape, const std::string& what) {
+  uint64_t n = 1;
+  for (uint64_t d : shape) {
+    if (d > (1ull << 48) || (d && n > (1ull << 48) / d)) bad(what + ": shape too large");
+    n *= d;
+  }
+  return n;
+}
+
 size_t dtype_size(DType t) {
   switch (t) {
     case DType::U32:
@@ -147,7 +158,8 @@ void SafetensorsStore::add_file(const std::string& path, const std::map<std::str
       bad(path + ": data offsets out of range for " + kv.first);
     t.data = base + (size_t)b0;
     t.bytes = (size_t)(b1 - b0);
-    if (t.bytes != t.numel() * dtype_size(t.dtype)) bad(path + ": size does not match shape for " + kv.first);
+    if (t.bytes != checked_numel(t.shape, kv.first) * dtype_size(t.dtype))
+      bad(path + ": size does not match shape for " + kv.first);
     tensors_[kv.first] = t;
   }
 }
@@ -319,7 +331,7 @@ GgufFile::GgufFile(const std::string& path) : file_(std::make_unique<MappedFile>
     // GGUF lists ne[0] (innermost) first; the view keeps outermost first
     for (size_t d = in.ne.size(); d-- > 0;) t.shape.push_back(in.ne[d]);
     const uint64_t inner = in.ne[0];
-    const uint64_t outer = t.numel() / std::max<uint64_t>(inner, 1);
+    const uint64_t outer = checked_numel(t.shape, in.name) / std::max<uint64_t>(inner, 1);
     uint64_t bytes = 0;
     switch (in.type) {
       case GGML_F32: t.dtype = DType::F32; bytes = t.numel() * 4; break;

@@ -170,3 +170,26 @@ def test_gguf_errors(tmp_path, case, fragment):
     elif case == "heads":
         kw["meta"] = [m for m in meta if m[0] != "qwen2.attention.head_count_kv"]
     expect_error(gguf_file(tmp_path, **kw), fragment)
+
+
+def test_gguf_huge_dims_are_rejected(tmp_path):
+    """Dimensions whose product overflows 64-bit byte counts must not pass
+    the bounds check."""
+    _, q2 = cfgs()
+    p = tmp_path / "huge.gguf"
+    write_gguf(p, qwen2_meta(q2), [("token_embd.weight", GGML_Q4_K, (256, 1 << 62), bytes(144))])
+    expect_error(p, "too large")
+
+
+def test_safetensors_huge_shape_is_rejected(tmp_path):
+    d = mlx_dir(tmp_path)
+    shard = sorted(d.glob("*.safetensors"))[0]
+    raw = shard.read_bytes()
+    n = int.from_bytes(raw[:8], "little")
+    hdr = json.loads(raw[8:8 + n])
+    name = next(k for k in hdr if k != "__metadata__")
+    hdr[name]["shape"] = [1 << 40, 1 << 40]
+    h = json.dumps(hdr).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    shard.write_bytes(len(h).to_bytes(8, "little") + h + raw[8 + n:])
+    expect_error(d, "too large")
