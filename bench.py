@@ -100,13 +100,69 @@ def gpu_bench(args):
     s.free()
     c5 = None if args.no_config5 else config5(model, cfg)
     model.free()
+    c1 = config1(dev)
 
     roof = roofline(dev, cfg, batch)
     return {
         "tok_s": tok_s, "ms_per_step": ms_per_step, "batch1_tok_s": b1_tok_s, "step_ms_pct": pct, "config5": c5,
+        "config1": c1,
         "weight_gb": info["weight_bytes"] / 1e9, "algo_gb_per_step": info["algo_bytes_per_token"] / 1e9,
         "roofline": roof,
     }
+
+
+def config1(dev):
+    """Qwen2.5-0.5B architecture (GGUF Q4_K/Q6_K
+    layout, seeded weights), an 81-token random prompt, 32 greedy tokens, then
+    the warm rerun: a session holding the first 80 prompt tokens (the radix
+    graft) is forked and fed the last prompt token plus the 31 tokens it
+    generates, 32 fed tokens in all. The greedy rate is also timed over 128
+    decode steps."""
+    from pagoda_amd.engine import QWEN2_05B, Model
+
+    cfg = QWEN2_05B
+    model = Model.synth(dev, cfg, seed=1)
+    prompt = np.random.default_rng(81).integers(0, cfg.vocab, 81)
+    s = model.new_session()
+    dev.sync()
+    t0 = time.perf_counter()
+    ids, _ = model.step_ragged([s], [prompt])
+    tok = int(ids[0])
+    dev.sync()
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+    cold = [tok]
+    t0 = time.perf_counter()
+    for _ in range(31):
+        tok, _ = s.forward_greedy(tok)
+        cold.append(tok)
+    gen_s = time.perf_counter() - t0
+    for _ in range(8):
+        tok, _ = s.forward_greedy(tok)
+    t0 = time.perf_counter()
+    n = 128
+    for _ in range(n):
+        tok, _ = s.forward_greedy(tok)
+    dec_s = time.perf_counter() - t0
+    s.free()
+    trunk = model.new_session()
+    trunk.forward(prompt[:80])
+    w = trunk.fork()
+    fed = 1
+    ids, _ = model.step_ragged([w], [prompt[80:]])
+    tok = int(ids[0])
+    warm = [tok]
+    for _ in range(31):
+        tok, _ = w.forward_greedy(tok)
+        warm.append(tok)
+        fed += 1
+    for x in (w, trunk):
+        x.free()
+    model.free()
+    out = {"prompt": 81, "gen": 32, "prefill_ms": round(prefill_ms, 3), "gen_tok_s": round(31 / gen_s, 1),
+           "decode_tok_s": round(n / dec_s, 1), "warm_fed_tokens": fed, "warm_equals_cold": warm == cold}
+    log(f"config 1: prefill {prefill_ms:.2f} ms, decode {out['decode_tok_s']} tok/s, warm fed {fed}, "
+        f"warm == cold: {warm == cold}")
+    return out
 
 
 C5_REQ, C5_TRUNK, C5_SUFFIX, C5_GEN, C5_CHUNK = 64, 3968, 50, 32, 4
@@ -561,6 +617,7 @@ def main():
         "batch1_tok_s": round(g["batch1_tok_s"], 2),
         "step_ms_percentiles": g["step_ms_pct"],
         "config5": g["config5"],
+        "config1": g["config1"],
         "roofline": g["roofline"],
         "cpu_baseline": cpu,
     }
