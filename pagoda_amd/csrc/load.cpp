@@ -39,7 +39,9 @@ class MlxSource : public WeightSource {
     qmat_upload_a8(q, a.packed, a.scales, a.biases, s);
   }
 
-  void stacked(QMat& q, int n_in, const std::vector<std::pair<int, int>>& parts, int li, hipStream_t s) override {
+  bool stacked(QMat& q, int fmt, int n_in, const std::vector<std::pair<int, int>>& parts, int li,
+               hipStream_t s) override {
+    if (fmt != FMT_A8) return false;
     int n = 0;
     for (auto& p : parts) n += p.second;
     const size_t G = (size_t)n_in / 64;
@@ -55,6 +57,7 @@ class MlxSource : public WeightSource {
     }
     qmat_alloc(q, FMT_A8, n, n_in, s);
     qmat_upload_a8(q, packed.data(), scales.data(), biases.data(), s);
+    return true;
   }
 
   void vec(float* dst, size_t n, int li, int kind, hipStream_t s) override {
@@ -139,22 +142,33 @@ class GgufSource : public WeightSource {
     (void)fmt;
     const std::string nm = name(li, kind);
     const TensorView& t = f_.at(nm);
-    int f;
-    switch (t.dtype) {
-      case DType::Q4K: f = FMT_Q4K; break;
-      case DType::Q6K: f = FMT_Q6K; break;
-      case DType::Q8_0: f = FMT_Q8_0; break;
-      case DType::Q5_0: f = FMT_Q5_0; break;
-      default: bad(nm + " must be Q4_K, Q6_K, Q8_0 or Q5_0");
-    }
+    const int f = fmt_of(t, nm);
     if (t.shape.size() != 2 || t.shape[0] != (uint64_t)n_out || t.shape[1] != (uint64_t)n_in)
       bad(nm + ": expected " + std::to_string(n_out) + " x " + std::to_string(n_in));
     qmat_alloc(q, f, n_out, n_in, s);
     qmat_upload_kq(q, t.data, s);
   }
 
-  void stacked(QMat&, int, const std::vector<std::pair<int, int>>&, int, hipStream_t) override {
-    bad("stacked projections belong to the hybrid model");
+  // row-major GGML blocks of the same type concatenate into one matrix
+  bool stacked(QMat& q, int, int n_in, const std::vector<std::pair<int, int>>& parts, int li,
+               hipStream_t s) override {
+    std::vector<const TensorView*> ts;
+    int n = 0;
+    for (auto& p : parts) {
+      const std::string nm = name(li, p.first);
+      const TensorView& t = f_.at(nm);
+      if (t.shape.size() != 2 || t.shape[0] != (uint64_t)p.second || t.shape[1] != (uint64_t)n_in)
+        bad(nm + ": expected " + std::to_string(p.second) + " x " + std::to_string(n_in));
+      if (!ts.empty() && t.dtype != ts[0]->dtype) return false;
+      ts.push_back(&t);
+      n += p.second;
+    }
+    const int f = fmt_of(*ts[0], name(li, parts[0].first));
+    std::vector<uint8_t> blocks;
+    for (const TensorView* t : ts) blocks.insert(blocks.end(), t->data, t->data + t->bytes);
+    qmat_alloc(q, f, n, n_in, s);
+    qmat_upload_kq(q, blocks.data(), s);
+    return true;
   }
 
   void vec(float* dst, size_t n, int li, int kind, hipStream_t s) override {
@@ -166,6 +180,16 @@ class GgufSource : public WeightSource {
 
  private:
   const GgufFile& f_;
+
+  static int fmt_of(const TensorView& t, const std::string& nm) {
+    switch (t.dtype) {
+      case DType::Q4K: return FMT_Q4K;
+      case DType::Q6K: return FMT_Q6K;
+      case DType::Q8_0: return FMT_Q8_0;
+      case DType::Q5_0: return FMT_Q5_0;
+      default: bad(nm + " must be Q4_K, Q6_K, Q8_0 or Q5_0");
+    }
+  }
 
   static std::string name(int li, int kind) {
     if (li < 0) {

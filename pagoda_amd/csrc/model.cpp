@@ -154,6 +154,7 @@ void build_model(Model& m, WeightSource& src) {
     src.matrix(m.embed, FMT_A8, c.vocab, H, -1, K_EMBED, s);
   } else {
     m.q_out = c.heads * c.head_dim;
+    m.proj_full = m.q_out + 2 * m.kv_width;  // q | k | v outputs side by side
     src.matrix(m.embed, FMT_Q6K, c.vocab, H, -1, K_EMBED, s);
   }
   if (src.tied_head()) {
@@ -177,7 +178,9 @@ void build_model(Model& m, WeightSource& src) {
       if (!L.full) {
         L.lin_index = m.n_lin++;
         // [qkv | z | b | a] stacked, one launch
-        src.stacked(L.proj, H, {{K_QKV, m.conv_dim}, {K_Z, m.value_dim}, {K_B, c.v_heads}, {K_A, c.v_heads}}, i, s);
+        PGD_CHECK(src.stacked(L.proj, FMT_A8, H,
+                              {{K_QKV, m.conv_dim}, {K_Z, m.value_dim}, {K_B, c.v_heads}, {K_A, c.v_heads}}, i, s),
+                  kErrFormat, "GDN projections must share one format");
         src.matrix(L.out, FMT_A8, H, m.value_dim, i, K_OUT, s);
         L.conv = vec((size_t)m.conv_dim * c.conv_kernel, i, K_CONV);
         L.a_log = vec(c.v_heads, i, K_ALOG);
@@ -185,7 +188,8 @@ void build_model(Model& m, WeightSource& src) {
         L.gnorm = vec(c.v_dim, i, K_GNORM);
       } else {
         L.full_index = m.n_full++;
-        src.stacked(L.proj, H, {{K_Q, m.q_out}, {K_K, m.kv_width}, {K_V, m.kv_width}}, i, s);
+        PGD_CHECK(src.stacked(L.proj, FMT_A8, H, {{K_Q, m.q_out}, {K_K, m.kv_width}, {K_V, m.kv_width}}, i, s),
+                  kErrFormat, "attention projections must share one format");
         src.matrix(L.o, FMT_A8, H, c.heads * c.head_dim, i, K_O, s);
         L.q_norm = vec(c.head_dim, i, K_QNORM);
         L.k_norm = vec(c.head_dim, i, K_KNORM);
@@ -193,8 +197,11 @@ void build_model(Model& m, WeightSource& src) {
     } else {
       L.full = true;
       L.full_index = m.n_full++;
-      src.matrix(L.q, FMT_Q4K, m.q_out, H, i, K_Q, s);
-      src.matrix(L.k, FMT_Q4K, m.kv_width, H, i, K_K, s);
+      // q and k in one matrix (one launch) when they share a format
+      if (!src.stacked(L.proj, FMT_Q4K, H, {{K_Q, m.q_out}, {K_K, m.kv_width}}, i, s)) {
+        src.matrix(L.q, FMT_Q4K, m.q_out, H, i, K_Q, s);
+        src.matrix(L.k, FMT_Q4K, m.kv_width, H, i, K_K, s);
+      }
       src.matrix(L.v, FMT_Q6K, m.kv_width, H, i, K_V, s);
       src.matrix(L.o, FMT_Q4K, H, c.heads * c.head_dim, i, K_O, s);
       src.matrix(L.gate, FMT_Q4K, c.intermediate, H, i, K_GATE, s);
@@ -235,15 +242,17 @@ class SynthSource : public WeightSource {
     qmat_alloc(q, fmt, n_out, n_in, s);
     qmat_synth(q, seed_, tkey(li, kind), 0.02f, s);
   }
-  void stacked(QMat& q, int n_in, const std::vector<std::pair<int, int>>& parts, int li, hipStream_t s) override {
+  bool stacked(QMat& q, int fmt, int n_in, const std::vector<std::pair<int, int>>& parts, int li,
+               hipStream_t s) override {
     int n = 0;
     for (auto& p : parts) n += p.second;
-    qmat_alloc(q, FMT_A8, n, n_in, s);
+    qmat_alloc(q, fmt, n, n_in, s);
     int r = 0;
     for (auto& p : parts) {  // each range keeps its own tensor key
       qmat_synth_rows(q, r, p.second, seed_, tkey(li, p.first), 0.02f, s);
       r += p.second;
     }
+    return true;
   }
   void vec(float* p, size_t n, int li, int kind, hipStream_t s) override {
     switch (kind) {
@@ -486,14 +495,18 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       }
     } else {
       rmsnorm_rows(w.x, H, nullptr, rows, H, L.in_norm, eps, norm_mode, w.xn, H, st);
-      qmat_gemv(L.q, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
-      qmat_gemv(L.k, w.xn, 0, H, rows, w.B, (int)w.ldb, nullptr, 0, st);
-      qmat_gemv(L.v, w.xn, 0, H, rows, w.C0, (int)w.ldb, nullptr, 0, st);
+      // q | k | v side by side in A (q and k from one stacked launch when they share a format)
+      if (L.proj.base) {
+        qmat_gemv(L.proj, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
+      } else {
+        qmat_gemv(L.q, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
+        qmat_gemv(L.k, w.xn, 0, H, rows, w.A + m.q_out, (int)w.lda, nullptr, 0, st);
+      }
+      qmat_gemv(L.v, w.xn, 0, H, rows, w.A + m.q_out + m.kv_width, (int)w.lda, nullptr, 0, st);
       q_raw = w.A;
-      k_raw = w.B;
-      v_raw = w.C0;
-      ld_q = (int)w.lda;
-      ld_kv = (int)w.ldb;
+      k_raw = w.A + m.q_out;
+      v_raw = w.A + m.q_out + m.kv_width;
+      ld_q = ld_kv = (int)w.lda;
     }
     if (!L.full) {
       // stacked rows: [qkv (conv_dim) | z (value_dim) | b (v_heads) | a (v_heads)]

@@ -115,8 +115,10 @@ struct WeightSource {
   // allocate q and fill it; fmt is the synthetic model's format, which a
   // checkpoint replaces by the stored one
   virtual void matrix(QMat& q, int fmt, int n_out, int n_in, int layer, int kind, hipStream_t s) = 0;
-  // one A8 matrix of row ranges taken from several tensors: parts = {kind, rows}
-  virtual void stacked(QMat& q, int n_in, const std::vector<std::pair<int, int>>& parts, int layer,
+  // one matrix of row ranges taken from several tensors: parts = {kind, rows};
+  // fmt as for matrix(). Returns false, allocating nothing, when the tensors
+  // cannot share one matrix (a checkpoint storing them in different formats).
+  virtual bool stacked(QMat& q, int fmt, int n_in, const std::vector<std::pair<int, int>>& parts, int layer,
                        hipStream_t s) = 0;
   // fill n device floats
   virtual void vec(float* dst, size_t n, int layer, int kind, hipStream_t s) = 0;

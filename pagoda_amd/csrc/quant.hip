@@ -289,7 +289,10 @@ __device__ inline float synth_w(uint64_t stream, float std, size_t r, int n_in, 
 }
 
 // Q4K quantizer (same choices as the CPU checker), one thread per block.
-__global__ void synth_q4k_kernel(uint8_t* qs, uint4* hdr, int n_out, int n_in, int nsb, uint64_t stream, float std) {
+// rows row0 .. row0 + n_out - 1 of the matrix; the stream is indexed by the row
+// within the window
+__global__ void synth_q4k_kernel(uint8_t* qs, uint4* hdr, int n_out, int n_in, int nsb, uint64_t stream, float std,
+                                 int row0) {
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (size_t)n_out * nsb) return;
   size_t r = t / nsb;
@@ -329,7 +332,7 @@ __global__ void synth_q4k_kernel(uint8_t* qs, uint4* hdr, int n_out, int n_in, i
   for (int i = 0; i < 3; ++i)
     sw[i] = (uint32_t)sc[4 * i] | ((uint32_t)sc[4 * i + 1] << 8) | ((uint32_t)sc[4 * i + 2] << 16) |
             ((uint32_t)sc[4 * i + 3] << 24);
-  *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(hdr) + q4k_hdr_off((int)r, b, nsb)) =
+  *reinterpret_cast<uint4*>(reinterpret_cast<uint8_t*>(hdr) + q4k_hdr_off((int)r + row0, b, nsb)) =
       make_uint4((uint32_t)dh | ((uint32_t)mh << 16), sw[0], sw[1], sw[2]);
   for (int grp = 0; grp < 4; ++grp) {
     int j0 = 2 * grp, j1 = 2 * grp + 1;
@@ -345,14 +348,14 @@ __global__ void synth_q4k_kernel(uint8_t* qs, uint4* hdr, int n_out, int n_in, i
         float q1 = ds1 > 0.0f ? clampf(rintf((v1 + dm1) / ds1), 0.0f, 15.0f) : 0.0f;
         word |= ((uint32_t)q0 | ((uint32_t)q1 << 4)) << (8 * e);
       }
-      *reinterpret_cast<uint32_t*>(qs + q4k_qs_off((int)r, b * 128 + 32 * grp + l4, nsb)) = word;
+      *reinterpret_cast<uint32_t*>(qs + q4k_qs_off((int)r + row0, b * 128 + 32 * grp + l4, nsb)) = word;
     }
   }
 }
 
 // Q6K quantizer, one thread per block.
 __global__ void synth_q6k_kernel(uint8_t* qlp, uint8_t* qhp, int8_t* scp, uint16_t* dp, int n_out, int n_in,
-                                 int nsb, uint64_t stream, float std) {
+                                 int nsb, uint64_t stream, float std, int row0) {
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (size_t)n_out * nsb) return;
   size_t r = t / nsb;
@@ -369,7 +372,7 @@ __global__ void synth_q6k_kernel(uint8_t* qlp, uint8_t* qhp, int8_t* scp, uint16
   }
   uint16_t dh = f32_to_f16(maxs / 127.0f);
   float d = f16_to_f32(dh);
-  const int row = (int)r;
+  const int row = (int)r + row0;
   dp[q6k_d_off(row, b, nsb)] = dh;
   int8_t scq[16];
   for (int j = 0; j < 16; ++j) {
@@ -689,12 +692,12 @@ void qmat_synth(QMat& m, uint64_t seed, uint64_t key, float std, hipStream_t s) 
   } else if (m.fmt == FMT_Q4K) {
     size_t n = (size_t)m.n_out * m.nsb;
     hipLaunchKernelGGL(synth_q4k_kernel, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, s, m.p0,
-                       reinterpret_cast<uint4*>(m.p1), m.n_out, m.n_in, m.nsb, stream, std);
+                       reinterpret_cast<uint4*>(m.p1), m.n_out, m.n_in, m.nsb, stream, std, 0);
   } else if (m.fmt == FMT_Q6K) {
     size_t n = (size_t)m.n_out * m.nsb;
     hipLaunchKernelGGL(synth_q6k_kernel, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, s, m.p0, m.p1,
                        reinterpret_cast<int8_t*>(m.p2), reinterpret_cast<uint16_t*>(m.p3), m.n_out, m.n_in, m.nsb,
-                       stream, std);
+                       stream, std, 0);
   } else {
     throw Error{kErrFormat, "no synthetic generator for this format"};
   }
@@ -702,9 +705,22 @@ void qmat_synth(QMat& m, uint64_t seed, uint64_t key, float std, hipStream_t s) 
 }
 
 void qmat_synth_rows(QMat& m, int row0, int rows, uint64_t seed, uint64_t key, float std, hipStream_t s) {
-  PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "row-window synthesis is for A8 matrices");
   PGD_CHECK(row0 >= 0 && rows >= 0 && row0 + rows <= m.n_out, kErrShape, "synth row window");
   if (!rows) return;
+  if (m.fmt == FMT_Q4K || m.fmt == FMT_Q6K) {
+    const size_t n = (size_t)rows * m.nsb;
+    const uint64_t stream = synth_stream(seed, key);
+    if (m.fmt == FMT_Q4K)
+      hipLaunchKernelGGL(synth_q4k_kernel, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, s, m.p0,
+                         reinterpret_cast<uint4*>(m.p1), rows, m.n_in, m.nsb, stream, std, row0);
+    else
+      hipLaunchKernelGGL(synth_q6k_kernel, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, s, m.p0, m.p1,
+                         reinterpret_cast<int8_t*>(m.p2), reinterpret_cast<uint16_t*>(m.p3), rows, m.n_in, m.nsb,
+                         stream, std, row0);
+    PGD_HIP(hipGetLastError());
+    return;
+  }
+  PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "no row-window synthesis for this format");
   size_t n = (size_t)rows * (m.n_in / 64);
   hipLaunchKernelGGL(synth_a8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, m.p0,
                      reinterpret_cast<uint32_t*>(m.p1), row0, rows, m.n_in, synth_stream(seed, key), std);

@@ -102,7 +102,8 @@ def test_block_swiglu(dev, name):
 def test_gguf_fallback_block_types_match_oracle(dev, tmp_path):
     """The Q4_K_M layout of a model whose hidden size is not a multiple of
     256 (Qwen2.5-0.5B: 896): the 320-wide rows (embedding, q/k/v/o, gate/up)
-    are Q5_0 / Q8_0, the 512-wide ffn_down rows keep Q4_K / Q6_K."""
+    are Q5_0 / Q8_0, the 512-wide ffn_down rows keep Q4_K / Q6_K. Layer 0's q
+    and k share a type (one stacked matrix), layer 1's do not."""
     from pagoda_amd.engine import Model
 
     cfg = small2(hidden=320, heads=5, kv_heads=1, head_dim=64, intermediate=512, n_layers=2)
@@ -111,7 +112,9 @@ def test_gguf_fallback_block_types_match_oracle(dev, tmp_path):
     H, kvw, qw = cfg.hidden, cfg.kv_heads * cfg.head_dim, cfg.heads * cfg.head_dim
     types = {(-1, K_EMBED): GGML_Q8_0}
     for i in range(cfg.n_layers):
-        types.update({(i, K_Q): GGML_Q5_0, (i, K_K): GGML_Q5_0, (i, K_V): GGML_Q8_0, (i, K_O): GGML_Q5_0,
+        # layer 0: q and k in one type (one stacked matrix); layer 1: different types (two matrices)
+        types.update({(i, K_Q): GGML_Q5_0, (i, K_K): GGML_Q5_0 if i == 0 else GGML_Q8_0, (i, K_V): GGML_Q8_0,
+                      (i, K_O): GGML_Q5_0,
                       (i, K_GATE): GGML_Q5_0, (i, K_UP): GGML_Q5_0})
     shapes = {K_EMBED: (cfg.vocab, H), K_Q: (qw, H), K_K: (kvw, H), K_V: (kvw, H), K_O: (H, qw),
               K_GATE: (cfg.intermediate, H), K_UP: (cfg.intermediate, H)}
