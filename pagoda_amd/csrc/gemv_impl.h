@@ -61,6 +61,13 @@ struct GemvArgs {
   a8act::Dst nact;
   const float* nw;
   float* nrss;
+  // one-row store launches only (cout null: none): outputs n < conv_n also go
+  // through the causal conv step of channel n (weights cw [conv_n][conv_k],
+  // state cst [conv_n][conv_k - 1], updated) into cout[n]
+  const float* cw;
+  float* cst;
+  float* cout;
+  int conv_n, conv_k;
 };
 
 // 1/rms of one deferred-norm row from its partial sums of squares: lane l adds

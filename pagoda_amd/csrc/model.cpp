@@ -479,6 +479,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   for (size_t li = 0; li < m.layers.size(); ++li) {
     auto& L = m.layers[li];
     A8Act post_in;  // the post-mixer norm's deferred input
+    bool conv_done = false;  // the projection GEMV ran the causal conv
     // ---- projections of the normed input ----
     const float *q_raw = nullptr, *k_raw = nullptr, *v_raw = nullptr;
     int ld_q = 0, ld_kv = 0;
@@ -486,7 +487,13 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       // the input norm's deferred operands: written by the previous layer's down
       // projection, or prepared here for the first layer; one GEMV for all projections
       A8Act act = have_next_in ? next_in : a8_gnorm_prep(w.x, H, rows, H, L.in_norm, eps, w.act, st);
-      qmat_gemv_a8(L.proj, act, w.A, (int)w.lda, nullptr, 0, st);
+      // one token of one sequence: the GEMV's epilogue also runs the causal conv
+      conv_done = !L.full && rows == 1 && nseq == 1;
+      if (conv_done)
+        qmat_gemv_a8_conv1(L.proj, act, w.A, (int)w.lda, L.conv, sess[0]->rec + (size_t)L.lin_index * per_lin,
+                           m.conv_dim, c.conv_kernel, w.D, st);
+      else
+        qmat_gemv_a8(L.proj, act, w.A, (int)w.lda, nullptr, 0, st);
       if (L.full) {
         q_raw = w.A;
         k_raw = w.A + m.q_out;
@@ -512,8 +519,9 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       // stacked rows: [qkv (conv_dim) | z (value_dim) | b (v_heads) | a (v_heads)]
       const float* P = w.A;
       const int ldp = (int)w.lda;
-      conv_step(P, ldp, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb, (size_t)L.lin_index * per_lin, sm,
-                nseq, st);
+      if (!conv_done)
+        conv_step(P, ldp, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb, (size_t)L.lin_index * per_lin,
+                  sm, nseq, st);
       GdnParams gp{};
       gp.k_heads = c.k_heads;
       gp.v_heads = c.v_heads;
