@@ -61,14 +61,31 @@ struct GemvArgs {
   a8act::Dst nact;
   const float* nw;
   float* nrss;
-  // one-row store launches only (cout null: none): outputs n < conv_n also go
+  // split-K store launches of 1..4 rows, every row one sequence's only token
+  // (cout null: none): outputs n < conv_n of row r (absolute, row0 + launch row) also go
   // through the causal conv step of channel n (weights cw [conv_n][conv_k],
-  // state cst [conv_n][conv_k - 1], updated) into cout[n]
+  // state at cbase[r] + coff, [conv_n][conv_k - 1], updated) into
+  // cout[r * ldc + n]
   const float* cw;
-  float* cst;
+  float* const* cbase;
+  size_t coff;
   float* cout;
-  int conv_n, conv_k;
+  int ldc, conv_n, conv_k;
 };
+
+// the causal conv step of one channel for one row: conv_step_kernel's
+// arithmetic and order, the state shifted in place
+__device__ inline void conv_channel(const GemvArgs& a, int row, int n, float xv) {
+  const int hist = a.conv_k - 1;
+  float* cs = a.cbase[row] + a.coff + (size_t)n * hist;
+  const float* wt = a.cw + (size_t)n * a.conv_k;
+  float acc = 0.0f;
+  for (int k = 0; k < hist; ++k) acc += cs[k] * wt[k];
+  acc += xv * wt[hist];
+  a.cout[(size_t)row * a.ldc + n] = acc / (1.0f + expf(-acc));
+  for (int k = 0; k + 1 < hist; ++k) cs[k] = cs[k + 1];
+  if (hist > 0) cs[hist - 1] = xv;
+}
 
 // 1/rms of one deferred-norm row from its partial sums of squares: lane l adds
 // partials l, l + 64, ... in turn, then a xor butterfly (each step adds the

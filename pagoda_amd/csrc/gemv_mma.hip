@@ -551,19 +551,7 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
         const size_t o = (size_t)b * a.ldy + n;
         if constexpr (EPI == EPI_STORE) {
           a.y[o] = Y[st][bt][r];
-          if (a.cout && n < a.conv_n) {
-            // causal conv step of channel n (conv_step_kernel's order), state shifted in place
-            const int hist = a.conv_k - 1;
-            float* cs = a.cst + (size_t)n * hist;
-            const float* wt = a.cw + (size_t)n * a.conv_k;
-            const float xv = Y[st][bt][r];
-            float acc = 0.0f;
-            for (int k = 0; k < hist; ++k) acc += cs[k] * wt[k];
-            acc += xv * wt[hist];
-            a.cout[n] = acc / (1.0f + expf(-acc));
-            for (int k = 0; k + 1 < hist; ++k) cs[k] = cs[k + 1];
-            if (hist > 0) cs[hist - 1] = xv;
-          }
+          if (a.cout && n < a.conv_n) conv_channel(a, a.row0 + b, n, Y[st][bt][r]);
         }
         if constexpr (EPI == EPI_RES) {
           const float h = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];

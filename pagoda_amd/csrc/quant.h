@@ -160,12 +160,14 @@ A8Act a8_gnorm_prep(const float* x, int ldx, int rows, int n, const float* w, fl
 A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps, float* y,
                    int ldy, void* buf, hipStream_t s);
 void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const float* res, int ldres, hipStream_t s);
-// One-row qmat_gemv_a8 (store) whose outputs n < conv_n also take the causal
-// conv step of channel n (the conv_step arithmetic for one row of one
-// sequence): weights conv_w [conv_n][kernel], state [conv_n][kernel - 1]
-// (updated), SiLU output to conv_out[n].
-void qmat_gemv_a8_conv1(const QMat& m, const A8Act& act, float* y, int ldy, const float* conv_w, float* conv_state,
-                        int conv_n, int kernel, float* conv_out, hipStream_t s);
+// qmat_gemv_a8 (store) of 1..4 rows for a step where row r is the only token
+// of sequence r: outputs n < conv_n of row r also take the causal conv step of channel n
+// (the conv_step arithmetic): weights conv_w [conv_n][kernel], state at
+// state_base[r] + state_off, [conv_n][kernel - 1] (updated), SiLU output to
+// conv_out[r * ldc + n].
+void qmat_gemv_a8_conv(const QMat& m, const A8Act& act, float* y, int ldy, const float* conv_w,
+                       float* const* state_base, size_t state_off, int conv_n, int kernel, float* conv_out, int ldc,
+                       hipStream_t s);
 // mid (nullable when mid_act is given): silu(gate x) * (up x) in f32;
 // mid_act (nullable): the same product written as prepared activations
 void qmat_gemv_a8_swiglu(const QMat& gate, const QMat& up, const A8Act& act, float* mid, int ldm, hipStream_t s,

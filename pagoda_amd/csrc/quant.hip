@@ -645,19 +645,23 @@ void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const floa
   run_a8_mma(a, act, res ? EPI_RES : EPI_STORE, s);
 }
 
-void qmat_gemv_a8_conv1(const QMat& m, const A8Act& act, float* y, int ldy, const float* conv_w, float* conv_state,
-                        int conv_n, int kernel, float* conv_out, hipStream_t s) {
+void qmat_gemv_a8_conv(const QMat& m, const A8Act& act, float* y, int ldy, const float* conv_w,
+                       float* const* state_base, size_t state_off, int conv_n, int kernel, float* conv_out, int ldc,
+                       hipStream_t s) {
   PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "prepared activations feed A8 matrices");
-  PGD_CHECK(act.rows == 1, kErrShape, "the conv epilogue is for one-row launches");
-  PGD_CHECK(conv_n <= m.n_out && kernel >= 1 && kernel <= 8 && conv_w && conv_state && conv_out, kErrShape,
+  PGD_CHECK(conv_n <= m.n_out && kernel >= 1 && kernel <= 8 && conv_w && state_base && conv_out, kErrShape,
             "conv epilogue arguments");
+  // 1..4 rows run one launch of the split-K kernel, whose epilogue holds the outputs
+  PGD_CHECK(act.rows >= 1 && act.rows <= 4, kErrShape, "the conv epilogue is for launches of 1..4 rows");
   GemvArgs a = make_args(m);
   a.y = y;
   a.ldy = ldy;
   PGD_CHECK(!a8_sk_wanted(a, EPI_STORE), kErrShape, "the conv epilogue needs the split-K kernel");
   a.cw = conv_w;
-  a.cst = conv_state;
+  a.cbase = state_base;
+  a.coff = state_off;
   a.cout = conv_out;
+  a.ldc = ldc;
   a.conv_n = conv_n;
   a.conv_k = kernel;
   run_a8_mma(a, act, EPI_STORE, s);
