@@ -129,6 +129,32 @@ def test_ragged_batch_bitwise_equals_serial(which, request):
     assert [s.context_len() for s in batched] == [s.context_len() for s in serial]
 
 
+def test_small_decode_batch_bitwise_equals_serial(m35):
+    """Steps of 2..4 decode rows, one per sequence: the projection GEMV runs
+    each row's causal conv in its epilogue on that sequence's state. Three
+    sequences stepped together equal each stepped alone (one-row launches),
+    bitwise, over two steps."""
+    model, _ = m35
+    rng = np.random.default_rng(13)
+    prompts = [rng.integers(0, model.cfg.vocab, n) for n in (3, 6, 2)]
+    batched = [model.new_session() for _ in prompts]
+    serial = []
+    try:
+        for s, p in zip(batched, prompts):
+            s.forward(p)
+        serial = [s.fork() for s in batched]
+        toks = [int(t) for t in rng.integers(0, model.cfg.vocab, 3)]
+        for _ in range(2):
+            _, bl = model.step_ragged(batched, [[t] for t in toks], want_logits=True)
+            sl = [s.forward([t]) for s, t in zip(serial, toks)]
+            for i in range(3):
+                np.testing.assert_array_equal(bl[i].view(np.uint32), sl[i].view(np.uint32))
+            toks = [int(np.argmax(x)) for x in sl]
+    finally:
+        for x in batched + serial:
+            x.free()
+
+
 def test_verify_equals_serial_greedy(m35):
     """forward_verify(4) == 4 serial greedy steps (pagoda-hf/examples/qwen3_8.rs:219-247)."""
     model, _ = m35
