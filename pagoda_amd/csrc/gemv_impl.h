@@ -259,79 +259,69 @@ struct Q6K {
   }
 };
 
-// Q8_0: chunk p = block p of the row (32 weights): weights 32p..32p+15 are
-// the low half, 32p+16..32p+31 the high half; y = q * d.
+// Q8_0: chunk p = half p % 2 of block p / 2 of the row (16 weights, so a
+// 896-wide row gives 56 chunks for the wave's 64 lanes); y = q * d.
 struct Q80 {
   struct W {
-    uint4 lo, hi;
+    uint4 q;
     float d;
   };
-  static __device__ inline int chunks(const GemvArgs& a) { return a.nsb; }
+  static __device__ inline int chunks(const GemvArgs& a) { return a.nsb * 2; }
   static __device__ inline bool pos(const GemvArgs& a, int p, int& lo, int& hi) {
-    lo = p << 5;
-    hi = lo + 16;
+    lo = p << 4;
+    hi = -1;
     return true;
   }
   static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t*, const uint8_t*,
                                   const GemvArgs& a, int row, int p) {
     W w;
-    const uint8_t* q = c0 + (size_t)row * a.n_in + (p << 5);
-    w.lo = *reinterpret_cast<const uint4*>(q);
-    w.hi = *reinterpret_cast<const uint4*>(q + 16);
-    w.d = f16_to_f32(reinterpret_cast<const uint16_t*>(c1)[(size_t)row * a.nsb + p]);
+    w.q = *reinterpret_cast<const uint4*>(c0 + (size_t)row * a.n_in + (p << 4));
+    w.d = f16_to_f32(reinterpret_cast<const uint16_t*>(c1)[(size_t)row * a.nsb + (p >> 1)]);
     return w;
   }
-  static __device__ inline float acc(float r, const W& w, const float* xl, const float* xh, float, float, int,
-                                     bool) {
-    float dl = 0.0f, dh = 0.0f;
+  static __device__ inline float acc(float r, const W& w, const float* xl, const float*, float, float, int, bool) {
+    float dl = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      dl = fmaf((float)(int8_t)byte_of(w.lo, i), xl[i], dl);
-      dh = fmaf((float)(int8_t)byte_of(w.hi, i), xh[i], dh);
-    }
-    r = fmaf(w.d, dl, r);
-    return fmaf(w.d, dh, r);
+    for (int i = 0; i < 16; ++i) dl = fmaf((float)(int8_t)byte_of(w.q, i), xl[i], dl);
+    return fmaf(w.d, dl, r);
   }
 };
 
-// Q5_0: chunk p = block p of the row; qs byte j holds weight j (low nibble)
-// and weight j + 16 (high nibble), qh bit j / j + 16 their fifth bit;
-// y = (q - 16) * d.
+// Q5_0: chunk p = half h = p % 2 of block p / 2; qs byte j holds weight j
+// (low nibble) and weight j + 16 (high nibble), qh bit j / j + 16 their fifth
+// bit; y = (q - 16) * d.
 struct Q50 {
   struct W {
     uint4 q;
     uint32_t qh;
     float d;
   };
-  static __device__ inline int chunks(const GemvArgs& a) { return a.nsb; }
+  static __device__ inline int chunks(const GemvArgs& a) { return a.nsb * 2; }
   static __device__ inline bool pos(const GemvArgs& a, int p, int& lo, int& hi) {
-    lo = p << 5;
-    hi = lo + 16;
+    lo = p << 4;
+    hi = -1;
     return true;
   }
   static __device__ inline W load(const uint8_t* c0, const uint8_t* c1, const uint8_t* c2, const uint8_t*,
                                   const GemvArgs& a, int row, int p) {
     W w;
-    const size_t b = (size_t)row * a.nsb + p;
+    const size_t b = (size_t)row * a.nsb + (p >> 1);
     w.q = *reinterpret_cast<const uint4*>(c0 + b * 16);
-    w.qh = reinterpret_cast<const uint32_t*>(c1)[b];
+    w.qh = reinterpret_cast<const uint32_t*>(c1)[b] >> (16 * (p & 1));
     w.d = f16_to_f32(reinterpret_cast<const uint16_t*>(c2)[b]);
     return w;
   }
-  static __device__ inline float acc(float r, const W& w, const float* xl, const float* xh, float sl, float sh, int,
+  static __device__ inline float acc(float r, const W& w, const float* xl, const float*, float sl, float, int p,
                                      bool) {
-    float dl = 0.0f, dh = 0.0f;
+    const int sh = 4 * (p & 1);  // low or high nibbles
+    float dl = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const uint32_t b = byte_of(w.q, i);
-      const uint32_t ql = (b & 15u) | (((w.qh >> i) & 1u) << 4);
-      const uint32_t qh = (b >> 4) | (((w.qh >> (i + 16)) & 1u) << 4);
-      dl = fmaf((float)ql, xl[i], dl);
-      dh = fmaf((float)qh, xh[i], dh);
+      const uint32_t q = ((byte_of(w.q, i) >> sh) & 15u) | (((w.qh >> i) & 1u) << 4);
+      dl = fmaf((float)q, xl[i], dl);
     }
     // sum (q - 16) x = sum q x - 16 sum x
-    r = fmaf(w.d, fmaf(-16.0f, sl, dl), r);
-    return fmaf(w.d, fmaf(-16.0f, sh, dh), r);
+    return fmaf(w.d, fmaf(-16.0f, sl, dl), r);
   }
 };
 
