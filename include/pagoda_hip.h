@@ -209,16 +209,37 @@ int pgd_forward_verify(pgd_session* s, const uint32_t* toks, int n, uint32_t* id
  * n_per_seq[i] >= 1 tokens from toks (concatenated). ids receive the greedy
  * id (first max, pagoda/src/sampler.rs:59-69) of each session's last position
  * (all_rows = 0) or of every fed position (all_rows = 1); 0xFFFFFFFF marks a
- * row whose logits are all non-finite. logits (nullable) receive the
- * matching rows [rows][vocab]. Atomic: on an argument error no session
- * advances. */
+ * row with any non-finite logit, which the engine faults
+ * (pagoda/src/engine.rs:1278-1280: only that request, its batch-mates are
+ * unaffected). logits (nullable) receive the matching rows [rows][vocab].
+ * Atomic on argument errors: no session advances. A device error after the
+ * step has begun writing (GDN state and KV pages are updated in place) marks
+ * every session of the step unusable: later calls on them return
+ * PGD_ERR_STATE instead of continuing from half-advanced state. */
 int pgd_step_ragged(pgd_model* m, pgd_session* const* sessions, const uint32_t* toks, const int* n_per_seq,
                     int nseq, int all_rows, uint32_t* ids, float* logits);
-/* Qwen35Cache::to_bytes / from_bytes, format v1 (pagoda-hf/src/qwen3_5.rs:
- * 177-255). Arch 0 only. export writes *len bytes when buf is large enough
- * (pass buf = NULL to query). */
+/* ModelSession::export_kv / ModelEngine::import_session (pagoda/src/model.rs:
+ * 137, 89). Hybrid model (arch 0): Qwen35Cache::to_bytes /
+ * from_bytes, cache format v1 (pagoda-hf/src/qwen3_5.rs:177-256). Qwen2 (arch
+ * 1): the SessionKv PD payload (CandleCausalLM::cache_export / cache_import,
+ * pagoda-hf/src/llama.rs:215-345) with the session's last logits, which an
+ * imported session replays on an empty feed (pagoda-hf/src/lib.rs:644-667).
+ * export writes *len bytes when buf is large enough (pass buf = NULL to
+ * query). */
 int pgd_session_export(const pgd_session* s, uint8_t* buf, size_t cap, size_t* len);
 int pgd_session_import(pgd_model* m, const uint8_t* buf, size_t len, pgd_session** out);
+/* set_kv_wire_f16 (pagoda-hf/src/llama.rs:128-136): process-wide choice of the
+ * SessionKv export's K/V encoding, f32 (0, default) or f16 (1). */
+int pgd_set_kv_wire_f16(int on);
+/* CandleCausalLM::cache_prefix (pagoda-hf/src/lib.rs:219-226;
+ * qwen2_gguf.rs:183-185 -> SessionKv::prefix, llama.rs:81-101), used by
+ * graft_session (lib.rs:603-616): a new session holding the first n
+ * positions of s. KV pages below n are shared; the partial last page is
+ * copied on the new session's first write, so appends never disturb s.
+ * Cached logits are not carried (a graft has none, lib.rs:613).
+ * PGD_ERR_STATE for the hybrid model: GDN state cannot be cut to a prefix
+ * (the trait's default None, lib.rs:224). */
+int pgd_session_fork_prefix(const pgd_session* s, int n, pgd_session** out);
 
 #ifdef __cplusplus
 }

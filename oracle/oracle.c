@@ -1035,6 +1035,90 @@ size_t ora_qwen35_cache_to_bytes(const ora_qwen35_cache* c, uint8_t* buf, size_t
   return at;
 }
 
+static int take_bytes(const uint8_t* b, size_t n, size_t* at, void* dst, size_t k) {
+  if (*at + k > n) return -1;
+  memcpy(dst, b + *at, k);
+  *at += k;
+  return 0;
+}
+
+/* take_f32 (counted f32 vector): u32 count, then count f32 LE. Returns a
+ * malloc'd array (NULL for count 0) through *out, -1 when truncated. */
+static int take_f32s(const uint8_t* b, size_t n, size_t* at, float** out, uint32_t* count) {
+  uint32_t c;
+  if (take_bytes(b, n, at, &c, 4)) return -1;
+  if ((size_t)c * 4 > n - *at) return -1;
+  *count = c;
+  *out = NULL;
+  if (c) {
+    *out = (float*)malloc((size_t)c * 4);
+    memcpy(*out, b + *at, (size_t)c * 4);
+  }
+  *at += (size_t)c * 4;
+  return 0;
+}
+
+/* pagoda-hf/src/qwen3_5.rs:208-256 (Qwen35Cache::from_bytes): version 1,
+ * tags 1 (linear: conv, state) and 2 (full: kv_len, kv_heads, head_dim, k,
+ * v with |k| == |v| == kv_len*kv_heads*head_dim), no trailing bytes. This
+ * cache keeps one conv/state/KV geometry for all layers, so it also rejects
+ * layers of differing sizes and a kv_len other than the cache length, which
+ * a model-written cache never has. Returns NULL on any error. */
+ora_qwen35_cache* ora_qwen35_cache_from_bytes(const uint8_t* b, size_t n) {
+  size_t at = 0;
+  uint32_t version, n_layers;
+  uint64_t len;
+  if (take_bytes(b, n, &at, &version, 4) || version != 1) return NULL;
+  if (take_bytes(b, n, &at, &len, 8) || take_bytes(b, n, &at, &n_layers, 4)) return NULL;
+  if (len > (1u << 30) || n_layers > (1u << 16)) return NULL;
+  ora_qwen35_cache* cc = (ora_qwen35_cache*)calloc(1, sizeof *cc);
+  cc->n_layers = (int)n_layers;
+  cc->len = (int)len;
+  cc->conv_n = cc->state_n = cc->kv_heads = cc->head_dim = -1;
+  cc->layers = (q35_cache_layer*)calloc(n_layers ? n_layers : 1, sizeof(q35_cache_layer));
+  for (uint32_t i = 0; i < n_layers; ++i) {
+    q35_cache_layer* L = &cc->layers[i];
+    uint8_t tag;
+    if (take_bytes(b, n, &at, &tag, 1)) goto bad;
+    if (tag == 2) {
+      uint32_t kv_len, kvh, hd, nk, nv;
+      if (take_bytes(b, n, &at, &kv_len, 4) || take_bytes(b, n, &at, &kvh, 4) ||
+          take_bytes(b, n, &at, &hd, 4))
+        goto bad;
+      L->full = 1;
+      if (take_f32s(b, n, &at, &L->k, &nk) || take_f32s(b, n, &at, &L->v, &nv)) goto bad;
+      if ((uint64_t)kv_len * kvh * hd != nk || nk != nv) goto bad;
+      if (kv_len != len) goto bad;
+      if (cc->kv_heads < 0) {
+        cc->kv_heads = (int)kvh;
+        cc->head_dim = (int)hd;
+      } else if (cc->kv_heads != (int)kvh || cc->head_dim != (int)hd) {
+        goto bad;
+      }
+      L->cap = (int)kv_len;
+    } else if (tag == 1) {
+      uint32_t nc, ns;
+      if (take_f32s(b, n, &at, &L->conv, &nc) || take_f32s(b, n, &at, &L->state, &ns)) goto bad;
+      if (cc->conv_n < 0) {
+        cc->conv_n = (int)nc;
+        cc->state_n = (int)ns;
+      } else if (cc->conv_n != (int)nc || cc->state_n != (int)ns) {
+        goto bad;
+      }
+    } else {
+      goto bad;
+    }
+  }
+  if (at != n) goto bad;
+  if (cc->kv_heads < 0) cc->kv_heads = cc->head_dim = 0;
+  if (cc->conv_n < 0) cc->conv_n = cc->state_n = 0;
+  cc->kv_width = cc->kv_heads * cc->head_dim;
+  return cc;
+bad:
+  ora_qwen35_cache_free(cc);
+  return NULL;
+}
+
 /* pagoda-hf/src/qwen3_5.rs:1313-1385 (LinearAttn::forward). */
 static void q35_linear_attn(const ora_qwen35* m, const q35_layer* L, const float* x, int seq,
                             q35_cache_layer* cl, float* y) {
@@ -1339,6 +1423,113 @@ void ora_qwen2_cache_free(ora_qwen2_cache* c) {
   free(c->k);
   free(c->v);
   free(c);
+}
+
+int ora_qwen2_cache_len(const ora_qwen2_cache* c) { return c->len; }
+
+#define Q2_WIRE_MAGIC 0x50444B56u
+
+/* pagoda-hf/src/llama.rs:215-266 (SessionKv::export_bytes): magic, version
+ * 2, token count, layer count, logits (count + f32), then per layer a
+ * present flag (0 before the first forward), kv_heads, head_dim, the wire
+ * dtype (0 f32, 1 f16 with llama.rs:139-172's rounding) and K then V as
+ * [kv_heads, len, head_dim] (candle's [1, kv_heads, seq, hd] flattened). */
+size_t ora_qwen2_cache_export(const ora_qwen2* m, const ora_qwen2_cache* c, const float* logits, int n_logits,
+                              int f16, uint8_t* buf, size_t cap) {
+  size_t at = 0;
+  const int kvh = m->cfg.kv_heads, hd = m->cfg.head_dim;
+  put_u32(buf, &at, cap, Q2_WIRE_MAGIC);
+  put_u32(buf, &at, cap, 2);
+  put_u32(buf, &at, cap, (uint32_t)c->len);
+  put_u32(buf, &at, cap, (uint32_t)c->n_layers);
+  put_f32s(buf, &at, cap, logits, (uint32_t)(logits ? n_logits : 0));
+  for (int l = 0; l < c->n_layers; ++l) {
+    if (c->len == 0) {
+      put_u32(buf, &at, cap, 0);
+      continue;
+    }
+    put_u32(buf, &at, cap, 1);
+    put_u32(buf, &at, cap, (uint32_t)kvh);
+    put_u32(buf, &at, cap, (uint32_t)hd);
+    put_u32(buf, &at, cap, f16 ? 1u : 0u);
+    for (int which = 0; which < 2; ++which) {
+      const float* src = which ? c->v[l] : c->k[l];
+      for (int h = 0; h < kvh; ++h)
+        for (int p = 0; p < c->len; ++p)
+          for (int d = 0; d < hd; ++d) {
+            float x = src[((size_t)p * kvh + h) * hd + d];
+            if (f16) {
+              uint16_t b = ora_f32_to_f16(x);
+              if (buf && at + 2 <= cap) memcpy(buf + at, &b, 2);
+              at += 2;
+            } else {
+              if (buf && at + 4 <= cap) memcpy(buf + at, &x, 4);
+              at += 4;
+            }
+          }
+    }
+  }
+  return at;
+}
+
+/* pagoda-hf/src/llama.rs:268-345 (SessionKv::import_bytes) into a cache of
+ * model m: magic, version 1 (payload f32 whatever the dtype field says) or
+ * 2 (dtype field 1 = f16 payload), logits handed back through logits_out
+ * (capacity logits_cap, count in *n_logits). Also requires what this cache
+ * can hold: every layer present (or none when len is 0) with the model's
+ * kv_heads/head_dim. Trailing bytes are ignored, as the reference reader
+ * does. Returns NULL on a malformed payload. */
+ora_qwen2_cache* ora_qwen2_cache_import(const ora_qwen2* m, const uint8_t* b, size_t n, float* logits_out,
+                                        int logits_cap, int* n_logits) {
+  size_t at = 0;
+  uint32_t magic, version, len, n_layers, nl;
+  const int kvh = m->cfg.kv_heads, hd = m->cfg.head_dim;
+  if (take_bytes(b, n, &at, &magic, 4) || magic != Q2_WIRE_MAGIC) return NULL;
+  if (take_bytes(b, n, &at, &version, 4) || (version != 1 && version != 2)) return NULL;
+  if (take_bytes(b, n, &at, &len, 4) || take_bytes(b, n, &at, &n_layers, 4)) return NULL;
+  if (take_bytes(b, n, &at, &nl, 4) || (size_t)nl * 4 > n - at) return NULL;
+  if ((int)n_layers != m->cfg.n_layers || len > (uint32_t)m->cfg.max_pos) return NULL;
+  if (n_logits) *n_logits = (int)nl;
+  if (logits_out) memcpy(logits_out, b + at, (size_t)(nl < (uint32_t)logits_cap ? nl : (uint32_t)logits_cap) * 4);
+  at += (size_t)nl * 4;
+  ora_qwen2_cache* c = ora_qwen2_cache_new(m);
+  c->len = (int)len;
+  c->cap = (int)len;
+  for (uint32_t l = 0; l < n_layers; ++l) {
+    uint32_t present, h, d, dt;
+    if (take_bytes(b, n, &at, &present, 4)) goto bad;
+    if (present == 0) {
+      if (len) goto bad;
+      continue;
+    }
+    if (take_bytes(b, n, &at, &h, 4) || take_bytes(b, n, &at, &d, 4) || take_bytes(b, n, &at, &dt, 4)) goto bad;
+    if ((int)h != kvh || (int)d != hd) goto bad;
+    int f16 = version >= 2 && dt == 1;
+    size_t count = (size_t)kvh * len * hd, es = f16 ? 2 : 4;
+    if (count * es * 2 > n - at) goto bad;
+    for (int which = 0; which < 2; ++which) {
+      float* dst = (float*)malloc(sizeof(float) * (count ? count : 1));
+      if (which) c->v[l] = dst; else c->k[l] = dst;
+      for (int hh = 0; hh < kvh; ++hh)
+        for (uint32_t p = 0; p < len; ++p)
+          for (int dd = 0; dd < hd; ++dd) {
+            float x;
+            if (f16) {
+              uint16_t u;
+              memcpy(&u, b + at, 2);
+              x = ora_f16_to_f32(u);
+            } else {
+              memcpy(&x, b + at, 4);
+            }
+            at += es;
+            dst[((size_t)p * kvh + hh) * hd + dd] = x;
+          }
+    }
+  }
+  return c;
+bad:
+  ora_qwen2_cache_free(c);
+  return NULL;
 }
 
 /* candle_nn RmsNorm as used at pagoda-hf/src/qwen2_gguf.rs:92,109,117:

@@ -106,6 +106,8 @@ int ora_qwen35_forward_all(ora_qwen35* m, const uint32_t* toks, int n, ora_qwen3
                            float* logits_all);
 /* Cache v1 bytes (pagoda-hf/src/qwen3_5.rs:177-206). Returns size; writes if buf != NULL. */
 size_t ora_qwen35_cache_to_bytes(const ora_qwen35_cache* c, uint8_t* buf, size_t cap);
+/* Cache v1 bytes -> cache (pagoda-hf/src/qwen3_5.rs:208-256); NULL on a malformed blob. */
+ora_qwen35_cache* ora_qwen35_cache_from_bytes(const uint8_t* buf, size_t len);
 /* Quantized tensor accessors for tests (pointers into the model). */
 const void* ora_qwen35_tensor(const ora_qwen35* m, int layer, int kind, int part);
 
@@ -113,6 +115,14 @@ ora_qwen2* ora_qwen2_new(const ora_qwen2_config* cfg, uint64_t seed);
 void ora_qwen2_free(ora_qwen2* m);
 ora_qwen2_cache* ora_qwen2_cache_new(const ora_qwen2* m);
 void ora_qwen2_cache_free(ora_qwen2_cache* c);
+int ora_qwen2_cache_len(const ora_qwen2_cache* c);
+/* SessionKv wire payload (pagoda-hf/src/llama.rs:215-345). export returns the
+ * size and writes when buf != NULL; f16 selects the f16 wire (version 2,
+ * dtype 1). import returns NULL on a malformed payload. */
+size_t ora_qwen2_cache_export(const ora_qwen2* m, const ora_qwen2_cache* c, const float* logits, int n_logits,
+                              int f16, uint8_t* buf, size_t cap);
+ora_qwen2_cache* ora_qwen2_cache_import(const ora_qwen2* m, const uint8_t* buf, size_t len, float* logits_out,
+                                        int logits_cap, int* n_logits);
 int ora_qwen2_forward(ora_qwen2* m, const uint32_t* toks, int n, ora_qwen2_cache* c,
                       float* logits);
 const void* ora_qwen2_tensor(const ora_qwen2* m, int layer, int kind, int part);

@@ -76,6 +76,16 @@ def lib():
             getattr(_lib, n).argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p]
         _lib.ora_qwen35_cache_to_bytes.restype = C.c_size_t
         _lib.ora_qwen35_cache_to_bytes.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        _lib.ora_qwen35_cache_from_bytes.restype = C.c_void_p
+        _lib.ora_qwen35_cache_from_bytes.argtypes = [C.c_void_p, C.c_size_t]
+        _lib.ora_qwen2_cache_len.restype = C.c_int
+        _lib.ora_qwen2_cache_len.argtypes = [C.c_void_p]
+        _lib.ora_qwen2_cache_export.restype = C.c_size_t
+        _lib.ora_qwen2_cache_export.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                                C.c_size_t]
+        _lib.ora_qwen2_cache_import.restype = C.c_void_p
+        _lib.ora_qwen2_cache_import.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_int,
+                                                C.c_void_p]
         _lib.ora_qwen35_cache_len.restype = C.c_int
         _lib.ora_qwen35_cache_len.argtypes = [C.c_void_p]
         _lib.ora_argmax_first.restype = C.c_uint32
@@ -324,6 +334,15 @@ class Qwen35Cache:
     def __len__(self):
         return lib().ora_qwen35_cache_len(self.h)
 
+    @classmethod
+    def from_bytes(cls, blob: bytes, model=None):
+        """Cache v1 bytes -> oracle cache (qwen3_5.rs:208-256); ValueError if malformed."""
+        buf = np.frombuffer(bytes(blob), np.uint8).copy()
+        h = lib().ora_qwen35_cache_from_bytes(_p(buf) if buf.size else None, buf.size)
+        if not h:
+            raise ValueError("malformed cache v1 bytes")
+        return cls(model, h)
+
     def to_bytes(self) -> bytes:
         n = lib().ora_qwen35_cache_to_bytes(self.h, None, 0)
         buf = np.zeros(n, np.uint8)
@@ -346,7 +365,7 @@ class Qwen2:
         self.h = lib().ora_qwen2_new(C.byref(self._c), seed)
 
     def new_cache(self):
-        return _Q2Cache(lib().ora_qwen2_cache_new(self.h))
+        return Qwen2Cache(lib().ora_qwen2_cache_new(self.h), self)
 
     def forward(self, toks, cache) -> np.ndarray:
         t = np.ascontiguousarray(toks, np.uint32)
@@ -372,12 +391,37 @@ class Qwen2:
             pass
 
 
-class _Q2Cache:
-    def __init__(self, h):
-        self.h = h
+class Qwen2Cache:
+    def __init__(self, h, model=None):
+        self.h, self.model = h, model
+
+    def __len__(self):
+        return lib().ora_qwen2_cache_len(self.h)
+
+    def export_bytes(self, logits=None, f16: bool = False) -> bytes:
+        """SessionKv::export_bytes (pagoda-hf/src/llama.rs:215-266)."""
+        lg = None if logits is None else np.ascontiguousarray(logits, np.float32)
+        args = (self.model.h, self.h, _p(lg) if lg is not None else None, 0 if lg is None else lg.size, int(f16))
+        n = lib().ora_qwen2_cache_export(*args, None, 0)
+        buf = np.zeros(n, np.uint8)
+        lib().ora_qwen2_cache_export(*args, _p(buf), n)
+        return buf.tobytes()
+
+    @classmethod
+    def import_bytes(cls, model, blob: bytes):
+        """SessionKv::import_bytes (llama.rs:268-345) -> (cache, logits or None)."""
+        buf = np.frombuffer(bytes(blob), np.uint8).copy()
+        lg = np.zeros(model.cfg.vocab, np.float32)
+        nl = C.c_int(0)
+        h = lib().ora_qwen2_cache_import(model.h, _p(buf) if buf.size else None, buf.size, _p(lg), lg.size,
+                                         C.byref(nl))
+        if not h:
+            raise ValueError("malformed SessionKv payload")
+        return cls(h, model), (lg[:nl.value].copy() if nl.value else None)
 
     def __del__(self):
         try:
             lib().ora_qwen2_cache_free(self.h)
         except Exception:
             pass
+_Q2Cache = Qwen2Cache

@@ -57,6 +57,8 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_model_info": (c_int, [c_void_p, P(c_size_t), P(c_double), P(c_int)]),
     "pgd_session_new": (c_int, [c_void_p, P(c_void_p)]),
     "pgd_session_fork": (c_int, [c_void_p, P(c_void_p)]),
+    "pgd_session_fork_prefix": (c_int, [c_void_p, c_int, P(c_void_p)]),
+    "pgd_set_kv_wire_f16": (c_int, [c_int]),
     "pgd_session_free": (c_int, [c_void_p]),
     "pgd_session_len": (c_int, [c_void_p, P(c_int)]),
     "pgd_forward": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),

@@ -8,6 +8,7 @@
 // qwen2_gguf.rs:142-266, llama.rs:734-886).
 #include "model.h"
 
+#include <atomic>
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -335,6 +336,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     for (int i = 0; i < nseq; ++i) {
       PGD_CHECK(sess[i] && sess[i]->model == &m, kErrArg, "session does not belong to this model");
       PGD_CHECK(seen.insert(sess[i]).second, kErrArg, "a session appears twice in one step");
+      PGD_CHECK(!sess[i]->poisoned, kErrState, "session state is undefined after a failed step");
       PGD_CHECK(n[i] >= 1, kErrArg, "every session must feed at least one token");
       PGD_CHECK((long long)sess[i]->len + n[i] <= c.max_pos, kErrShape,
                 "context " + std::to_string(sess[i]->len) + " + " + std::to_string(n[i]) + " exceeds max_pos");
@@ -344,6 +346,20 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       PGD_CHECK(toks[r] < (uint32_t)c.vocab, kErrArg, "token " + std::to_string(toks[r]) + " out of vocab");
   }
   const int lrows = out.all_rows ? rows : nseq;
+  // From here on the step writes session state in place (KV pages, the GDN
+  // recurrent and conv state). A device error past this point leaves that
+  // state half-advanced, so the sessions are marked unusable instead of
+  // silently continuing from it (a batched step commits all or nothing,
+  // pagoda-hf/src/llama.rs:750-778).
+  struct PoisonOnThrow {
+    Session* const* s;
+    int n;
+    bool armed = true;
+    ~PoisonOnThrow() {
+      if (armed)
+        for (int i = 0; i < n; ++i) s[i]->poisoned = true;
+    }
+  } poison{sess, nseq};
   // ---- KV pages: count, then allocate (copy-on-write for a shared tail) ----
   if (m.n_full > 0) {
     size_t need = 0;
@@ -621,9 +637,15 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   PGD_HIP(hipStreamSynchronize(st));
   const uint32_t* h_ids = (const uint32_t*)m.out_host;
   const float* h_vals = (const float*)(h_ids + lrows);
-  if (out.ids) memcpy(out.ids, h_ids, (size_t)lrows * 4);
+  const int* h_nf = (const int*)(h_vals + lrows);
+  if (out.ids) {
+    // the engine faults a request on any non-finite logit
+    // (pagoda/src/engine.rs:1278-1280): such a row returns no token
+    for (int r = 0; r < lrows; ++r) out.ids[r] = h_nf[r] > 0 ? 0xFFFFFFFFu : h_ids[r];
+  }
   if (out.vals) memcpy(out.vals, h_vals, (size_t)lrows * 4);
   for (int i = 0; i < nseq; ++i) sess[i]->len += n[i];
+  poison.armed = false;
 }
 
 }  // namespace pgd
@@ -706,6 +728,7 @@ int pgd_session_fork(const pgd_session* ps, pgd_session** out) {
   int rc = guard([&] {
     PGD_CHECK(ps && out, kErrArg, "null argument");
     const Session& s = ps->s;
+    PGD_CHECK(!s.poisoned, kErrState, "session state is undefined after a failed step");
     Model& m = *s.model;
     DeviceScope scope(m.dev);
     held = new pgd_session();
@@ -730,6 +753,35 @@ int pgd_session_fork(const pgd_session* ps, pgd_session** out) {
   return rc;
 }
 
+int pgd_session_fork_prefix(const pgd_session* ps, int n, pgd_session** out) {
+  pgd_session* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(ps && out, kErrArg, "null argument");
+    const Session& s = ps->s;
+    PGD_CHECK(!s.poisoned, kErrState, "session state is undefined after a failed step");
+    Model& m = *s.model;
+    // recurrent (GDN) state summarizes the whole context and cannot be cut
+    // back to a shorter prefix; such backends offer no prefix graft
+    // (CandleCausalLM::cache_prefix default None, pagoda-hf/src/lib.rs:224)
+    PGD_CHECK(m.rec_floats == 0, kErrState, "a recurrent-state session cannot be sliced to a prefix");
+    PGD_CHECK(n >= 0 && n <= s.len, kErrArg, "prefix length " + std::to_string(n) + " outside 0.." +
+                                                 std::to_string(s.len));
+    held = new pgd_session();
+    held->s.model = &m;
+    m.live_sessions++;
+    held->s.len = n;
+    // pages wholly or partly below n are shared; the partial last page is
+    // copied on the first write (step's copy-on-write of a shared tail), and
+    // its slots at or past n are never read before they are rewritten
+    const size_t keep = ((size_t)n + m.cfg.kv_block - 1) / m.cfg.kv_block;
+    held->s.blocks.assign(s.blocks.begin(), s.blocks.begin() + keep);
+    for (int b : held->s.blocks) m.refcount[b]++;
+    *out = held;
+  });
+  if (rc && held) delete held;
+  return rc;
+}
+
 int pgd_session_free(pgd_session* s) {
   return guard([&] { delete s; });
 }
@@ -747,6 +799,7 @@ int pgd_forward(pgd_session* ps, const uint32_t* toks, int n, float* logits) {
     Session& s = ps->s;
     Model& m = *s.model;
     if (n == 0) {
+      PGD_CHECK(!s.poisoned, kErrState, "session state is undefined after a failed step");
       PGD_CHECK(s.has_logits, kErrState, "empty feed before any forward");
       memcpy(logits, s.last_logits.data(), (size_t)m.cfg.vocab * 4);
       return;
@@ -870,17 +923,142 @@ struct Reader {
     return v;
   }
 };
+
+// IEEE binary16 with round to nearest even; NaN -> quiet NaN keeping the
+// sign, overflow -> infinity (the f16 wire encoding of
+// pagoda-hf/src/llama.rs:139-172).
+uint16_t f32_to_f16_rne(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  const uint32_t sign = (b >> 16) & 0x8000u;
+  const int e32 = (int)((b >> 23) & 0xffu);
+  uint32_t man = b & 0x7fffffu;
+  if (e32 == 0xff) return (uint16_t)(sign | (man ? 0x7e00u : 0x7c00u));
+  const int e = e32 - 112;  // rebias 127 -> 15
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {  // subnormal half (or zero)
+    if (e < -10) return (uint16_t)sign;
+    man |= 0x800000u;
+    const int sh = 14 - e;
+    uint32_t h = man >> sh, rest = man & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    if (rest > half || (rest == half && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = ((uint32_t)e << 10) | (man >> 13);
+  const uint32_t rest = man & 0x1fffu;
+  if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) ++h;  // a carry into the exponent is correct
+  return (uint16_t)(sign | h);
+}
+
+float f16_to_f32_exact(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu;
+  uint32_t man = h & 0x3ffu, bits;
+  if (e == 0) {
+    if (!man) {
+      bits = sign;
+    } else {
+      int k = 0;
+      while (!(man & 0x400u)) {
+        man <<= 1;
+        ++k;
+      }
+      bits = sign | ((uint32_t)(113 - k) << 23) | ((man & 0x3ffu) << 13);
+    }
+  } else if (e == 31) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else {
+    bits = sign | ((e + 112) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+// process-wide wire dtype of the SessionKv export (llama.rs:128-136)
+std::atomic<int> g_kv_wire_f16{0};
+
+constexpr uint32_t kKvWireMagic = 0x50444B56u;
+
+// One KV pool as [kv_heads][len][head_dim] f32 on the host.
+std::vector<float> gather_kv_head_major(const Model& m, const Session& s, const float* pool) {
+  const pgd_model_config& c = m.cfg;
+  const size_t per_blk = (size_t)c.kv_heads * c.kv_block * c.head_dim;
+  std::vector<float> out((size_t)c.kv_heads * s.len * c.head_dim), page(per_blk);
+  for (size_t bi = 0; bi < s.blocks.size(); ++bi) {
+    PGD_HIP(hipMemcpy(page.data(), pool + (size_t)s.blocks[bi] * per_blk, per_blk * 4, hipMemcpyDeviceToHost));
+    for (int h = 0; h < c.kv_heads; ++h)
+      for (int sl = 0; sl < c.kv_block; ++sl) {
+        const size_t p = bi * c.kv_block + sl;
+        if (p >= (size_t)s.len) break;
+        memcpy(&out[((size_t)h * s.len + p) * c.head_dim], &page[((size_t)h * c.kv_block + sl) * c.head_dim],
+               (size_t)c.head_dim * 4);
+      }
+  }
+  return out;
+}
+
+// SessionKv::export_bytes (pagoda-hf/src/llama.rs:215-266)
+std::vector<uint8_t> export_sessionkv(const Model& m, const Session& s) {
+  const pgd_model_config& c = m.cfg;
+  const bool f16 = g_kv_wire_f16.load() != 0;
+  std::vector<uint8_t> b;
+  put_u32(b, kKvWireMagic);
+  put_u32(b, 2);
+  put_u32(b, (uint32_t)s.len);
+  put_u32(b, (uint32_t)c.n_layers);
+  if (s.has_logits)
+    put_vec(b, s.last_logits.data(), s.last_logits.size());
+  else
+    put_u32(b, 0);
+  for (const Layer& L : m.layers) {
+    if (s.len == 0) {  // no forward yet: the reference's layers are None
+      put_u32(b, 0);
+      continue;
+    }
+    put_u32(b, 1);
+    put_u32(b, (uint32_t)c.kv_heads);
+    put_u32(b, (uint32_t)c.head_dim);
+    put_u32(b, f16 ? 1u : 0u);
+    for (const float* pool : {L.k_pool, L.v_pool}) {
+      const std::vector<float> kv = gather_kv_head_major(m, s, pool);
+      if (f16) {
+        for (float x : kv) {
+          const uint16_t h = f32_to_f16_rne(x);
+          put(b, &h, 2);
+        }
+      } else {
+        put(b, kv.data(), kv.size() * 4);
+      }
+    }
+  }
+  return b;
+}
 }  // namespace
+
+int pgd_set_kv_wire_f16(int on) {
+  g_kv_wire_f16.store(on ? 1 : 0);
+  return 0;
+}
 
 int pgd_session_export(const pgd_session* ps, uint8_t* buf, size_t cap, size_t* len) {
   return guard([&] {
     PGD_CHECK(ps && len, kErrArg, "null argument");
     const Session& s = ps->s;
+    PGD_CHECK(!s.poisoned, kErrState, "session state is undefined after a failed step");
     const Model& m = *s.model;
     const pgd_model_config& c = m.cfg;
-    PGD_CHECK(c.arch == PGD_ARCH_QWEN35, kErrArg, "cache bytes v1 are defined for the hybrid model only");
     DeviceScope scope(m.dev);
     PGD_HIP(hipStreamSynchronize(m.dev->stream));
+    if (c.arch == PGD_ARCH_QWEN2) {
+      const std::vector<uint8_t> b = export_sessionkv(m, s);
+      *len = b.size();
+      if (buf) {
+        PGD_CHECK(cap >= b.size(), kErrArg, "export buffer too small");
+        memcpy(buf, b.data(), b.size());
+      }
+      return;
+    }
     std::vector<uint8_t> b;
     put_u32(b, 1);
     uint64_t L64 = (uint64_t)s.len;
@@ -930,13 +1108,109 @@ int pgd_session_export(const pgd_session* ps, uint8_t* buf, size_t cap, size_t* 
   });
 }
 
+namespace {
+// SessionKv::import_bytes (pagoda-hf/src/llama.rs:268-345): version 1
+// (payload f32 whatever the dtype field says) or 2 (dtype 1 = f16 payload);
+// the logits become the session's cached last logits (replayed on an empty
+// feed, lib.rs:644-667). This cache needs every layer present with the
+// model's kv_heads/head_dim (or none, at length 0) and logits of vocab
+// entries or none. Trailing bytes are ignored, as in the reference reader.
+pgd_session* import_sessionkv(Model& m, const uint8_t* buf, size_t len) {
+  const pgd_model_config& c = m.cfg;
+  Reader rd{buf, len};
+  PGD_CHECK(rd.u32() == kKvWireMagic, kErrFormat, "bad kv payload magic");
+  const uint32_t version = rd.u32();
+  PGD_CHECK(version == 1 || version == 2, kErrFormat, "unsupported kv payload version " + std::to_string(version));
+  const uint32_t slen = rd.u32();
+  PGD_CHECK(rd.u32() == (uint32_t)c.n_layers, kErrFormat, "layer count mismatch");
+  PGD_CHECK(slen <= (uint32_t)c.max_pos, kErrFormat, "length exceeds max_pos");
+  const uint32_t nl = rd.u32();
+  PGD_CHECK(nl == 0 || nl == (uint32_t)c.vocab, kErrFormat, "logits count is neither 0 nor vocab");
+  rd.need((size_t)nl * 4);
+  std::vector<float> logits(nl);
+  if (nl) memcpy(logits.data(), buf + rd.at, (size_t)nl * 4);
+  rd.at += (size_t)nl * 4;
+  const size_t count = (size_t)c.kv_heads * slen * c.head_dim;
+  std::vector<std::vector<float>> kv((size_t)m.n_full * 2);
+  for (const Layer& L : m.layers) {
+    const uint32_t present = rd.u32();
+    if (!present) {
+      PGD_CHECK(slen == 0, kErrFormat, "missing layer in a non-empty kv payload");
+      continue;
+    }
+    const uint32_t kvh = rd.u32(), hd = rd.u32(), dt = rd.u32();
+    PGD_CHECK(kvh == (uint32_t)c.kv_heads && hd == (uint32_t)c.head_dim, kErrFormat, "kv shape");
+    const bool f16 = version >= 2 && dt == 1;
+    for (int which = 0; which < 2; ++which) {
+      std::vector<float>& dst = kv[(size_t)L.full_index * 2 + which];
+      dst.resize(count);
+      rd.need(count * (f16 ? 2 : 4));
+      if (f16) {
+        for (size_t i = 0; i < count; ++i) {
+          uint16_t h;
+          memcpy(&h, buf + rd.at + 2 * i, 2);
+          dst[i] = f16_to_f32_exact(h);
+        }
+        rd.at += count * 2;
+      } else {
+        memcpy(dst.data(), buf + rd.at, count * 4);
+        rd.at += count * 4;
+      }
+    }
+  }
+  const size_t nblk = ((size_t)slen + c.kv_block - 1) / c.kv_block;
+  PGD_CHECK(nblk <= m.free_blocks.size(), kErrAlloc, "KV page pool exhausted");
+  DeviceScope scope(m.dev);
+  pgd_session* held = new pgd_session();
+  Session& s = held->s;
+  s.model = &m;
+  m.live_sessions++;
+  try {
+    for (size_t i = 0; i < nblk; ++i) s.blocks.push_back(m.alloc_block());
+    const size_t per_blk = (size_t)c.kv_heads * c.kv_block * c.head_dim;
+    std::vector<float> page(per_blk);
+    for (const Layer& L : m.layers) {
+      if (slen == 0) break;
+      for (int which = 0; which < 2; ++which) {
+        const std::vector<float>& src = kv[(size_t)L.full_index * 2 + which];
+        float* pool = which == 0 ? L.k_pool : L.v_pool;
+        for (size_t bi = 0; bi < nblk; ++bi) {
+          std::fill(page.begin(), page.end(), 0.0f);
+          for (int h = 0; h < c.kv_heads; ++h)
+            for (int sl = 0; sl < c.kv_block; ++sl) {
+              const size_t p = bi * c.kv_block + sl;
+              if (p >= slen) break;
+              memcpy(&page[((size_t)h * c.kv_block + sl) * c.head_dim], &src[((size_t)h * slen + p) * c.head_dim],
+                     (size_t)c.head_dim * 4);
+            }
+          PGD_HIP(hipMemcpy(pool + (size_t)s.blocks[bi] * per_blk, page.data(), per_blk * 4, hipMemcpyHostToDevice));
+        }
+      }
+    }
+  } catch (...) {
+    delete held;
+    throw;
+  }
+  s.len = (int)slen;
+  if (nl) {
+    s.last_logits = std::move(logits);
+    s.has_logits = true;
+  }
+  return held;
+}
+}  // namespace
+
 int pgd_session_import(pgd_model* pm, const uint8_t* buf, size_t len, pgd_session** out) {
   pgd_session* held = nullptr;
   int rc = guard([&] {
     PGD_CHECK(pm && buf && out, kErrArg, "null argument");
     Model& m = pm->m;
     const pgd_model_config& c = m.cfg;
-    PGD_CHECK(c.arch == PGD_ARCH_QWEN35, kErrArg, "cache bytes v1 are defined for the hybrid model only");
+    if (c.arch == PGD_ARCH_QWEN2) {
+      held = import_sessionkv(m, buf, len);
+      *out = held;
+      return;
+    }
     Reader rd{buf, len};
     PGD_CHECK(rd.u32() == 1, kErrFormat, "kv version");
     uint64_t slen = rd.u64();

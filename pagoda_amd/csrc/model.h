@@ -94,6 +94,9 @@ struct Session {
   float* rec = nullptr;  // [n_lin][conv_floats + state_floats]
   std::vector<float> last_logits;
   bool has_logits = false;
+  // a step failed after it began writing this session's state in place
+  // (GDN state, KV pages): every later use is refused
+  bool poisoned = false;
   ~Session();
 };
 

@@ -199,12 +199,25 @@ class Session:
         call("pgd_session_fork", self.handle, C.byref(h))
         return Session(self.model, h)
 
+    def fork_prefix(self, n: int) -> "Session":
+        """CandleCausalLM::cache_prefix (pagoda-hf/src/lib.rs:219-226): the
+        first n positions as a new session (Qwen2 only)."""
+        h = C.c_void_p()
+        call("pgd_session_fork_prefix", self.handle, int(n), C.byref(h))
+        return Session(self.model, h)
+
     def export_kv(self) -> bytes:
         n = C.c_size_t()
         call("pgd_session_export", self.handle, None, C.c_size_t(0), C.byref(n))
         buf = np.zeros(n.value, np.uint8)
         call("pgd_session_export", self.handle, _p(buf), C.c_size_t(buf.size), C.byref(n))
         return buf.tobytes()
+
+
+def set_kv_wire_f16(on: bool) -> None:
+    """set_kv_wire_f16 (pagoda-hf/src/llama.rs:133-136): the SessionKv
+    export's K/V encoding, process-wide."""
+    call("pgd_set_kv_wire_f16", int(bool(on)))
 
 
 def argmax_first(logits: np.ndarray) -> int:
@@ -256,6 +269,17 @@ class HipEngine:
             self.errors.append(str(e))
             return None
         return [logits[i] for i in range(len(sessions))]
+
+    def graft_session(self, session: Session, covered: int):
+        """ModelEngine::graft_session (pagoda-hf/src/lib.rs:603-616) once the
+        prefix store has found `session` covering `covered` prompt tokens:
+        the session sliced to exactly that prefix, or None when the backend
+        cannot slice (the hybrid model's recurrent state)."""
+        try:
+            return session.fork_prefix(covered)
+        except PagodaError as e:
+            self.errors.append(str(e))
+            return None
 
     def import_session(self, tokens, kv: bytes):
         try:

@@ -2,7 +2,8 @@
 
 Config 1: Qwen2.5-0.5B architecture, Q4_K_M-style
 GGUF weights, 81-token random prompt, 32 greedy tokens; then the warm rerun
-where the prefix cache supplies 80 prompt tokens and only 32 are fed
+where the prefix graft slices the cold session to 80 prompt tokens and only
+32 are fed
 (pagoda/docs/BENCHMARK-METAL.md:25-33; examples/qwen2_gguf.rs:121-136: cold
 and warm token streams are identical).
 
@@ -60,11 +61,13 @@ def test_config1_qwen2_05b_greedy_32_cold_and_warm(dev):
         ref = oracle.forward([tr], oc)
         assert rel(got, ref) < LOGIT_TOL, f"step {step}: {rel(got, ref)}"
     print("config1: min top-2 margin", min(margins), flush=True)
-    # warm rerun: a session holding the first 80 prompt tokens (the graft) feeds
-    # the last prompt token, then the 31 generated tokens it samples itself
-    warm = model.new_session()
-    warm.forward(prompt[:80])
-    w2 = warm.fork()
+    # warm rerun: graft_session(prompt, len - 1) slices the cold session's
+    # cache (81 prompt + 31 generated positions) to the 80 covered prompt
+    # tokens (pagoda-hf/src/lib.rs:603-616); it feeds the last prompt token,
+    # then the 31 tokens it samples itself
+    assert s.context_len() == 112
+    w2 = s.fork_prefix(80)
+    assert w2.context_len() == 80
     fed = 0
     logits = w2.forward(prompt[80:])
     fed += 1

@@ -6,6 +6,8 @@ import pytest
 
 from oracle import pyoracle as ora
 
+import cachev1
+
 pytestmark = pytest.mark.gpu
 
 LOGIT_TOL = 1e-3  # max |diff| / max |ref| per logits vector
@@ -200,10 +202,32 @@ def test_fork_continues_independently(m35):
     f.free()
 
 
+def _assert_cache_bytes_close(g: bytes, r: bytes, tol: float = 1e-3):
+    """Tags, counts and integers identical; every float vector within tol of
+    its reference, max-normalized and elementwise (|d| <= tol*|ref| + atol
+    with atol = 1e-4 * max|ref| of that vector)."""
+    G, R = cachev1.parse(g), cachev1.parse(r)
+    assert G["len"] == R["len"] and len(G["layers"]) == len(R["layers"])
+    for i, (a, b) in enumerate(zip(G["layers"], R["layers"])):
+        assert a["tag"] == b["tag"], i
+        keys = ("conv", "state") if a["tag"] == 1 else ("k", "v")
+        if a["tag"] == 2:
+            assert (a["kv_len"], a["kv_heads"], a["head_dim"]) == (b["kv_len"], b["kv_heads"], b["head_dim"]), i
+        for key in keys:
+            x, y = a[key].astype(np.float64), b[key].astype(np.float64)
+            assert x.size == y.size, (i, key)
+            scale = max(np.abs(y).max(), 1e-30) if y.size else 1.0
+            assert np.abs(x - y).max(initial=0) <= tol * scale, (i, key)
+            assert np.all(np.abs(x - y) <= tol * np.abs(y) + 1e-4 * scale), (i, key)
+
+
 def test_export_import_round_trip(m35):
-    """Cache bytes v1 (pagoda-hf/src/qwen3_5.rs:177-255): same layout as the
-    oracle's to_bytes, values within tolerance, and an imported session
-    continues exactly like the exported one."""
+    """Cache bytes v1 (pagoda-hf/src/qwen3_5.rs:177-256). The GPU export and
+    the oracle's to_bytes of the same prompt have identical tags, counts and
+    shapes and floats within 1e-3; bytes the ORACLE wrote import into the GPU
+    and decode 4 greedy steps like the oracle; bytes the GPU wrote import
+    into the oracle and decode like the GPU session. So a layout shared by
+    export and import but different from the reference's fails."""
     model, oracle = m35
     rng = np.random.default_rng(7)
     prompt = rng.integers(0, model.cfg.vocab, 19)
@@ -211,17 +235,51 @@ def test_export_import_round_trip(m35):
     s.forward(prompt)
     blob = s.export_kv()
     oc = oracle.new_cache()
-    oracle.forward(prompt, oc)
+    ref_logits = oracle.forward(prompt, oc)
     ref = oc.to_bytes()
     assert len(blob) == len(ref)
-    assert blob[:16] == ref[:16]
-    g = np.frombuffer(blob[16:], np.uint8)
-    r = np.frombuffer(ref[16:], np.uint8)
-    # tags and counts identical; float payloads within tolerance
+    _assert_cache_bytes_close(blob, ref)
+    # the GPU's own bytes round-trip bitwise
     t = model.import_session(blob)
     assert t.context_len() == 19
+    assert t.export_kv() == blob
     np.testing.assert_array_equal(t.forward([1]), s.forward([1]))
-    assert g.size == r.size
+    # oracle bytes -> GPU, 4 greedy steps against the oracle continuing
+    u = model.import_session(ref)
+    assert u.context_len() == 19
+    tok = ora.argmax_first(ref_logits)
+    oc2 = oc.clone()
+    for k in range(4):
+        g = u.forward([tok])
+        r = oracle.forward([tok], oc2)
+        assert rel(g, r) < LOGIT_TOL, k
+        assert ora.argmax_first(g) == ora.argmax_first(r), k
+        tok = ora.argmax_first(r)
+    # GPU bytes -> oracle, 4 greedy steps against the GPU session continuing
+    v = model.import_session(blob)
+    od = ora.Qwen35Cache.from_bytes(blob, oracle)
+    tok = 5
+    for k in range(4):
+        g = v.forward([tok])
+        r = oracle.forward([tok], od)
+        assert rel(g, r) < LOGIT_TOL, k
+        assert ora.argmax_first(g) == ora.argmax_first(r), k
+        tok = ora.argmax_first(r)
+    for x in (s, t, u, v):
+        x.free()
+
+
+def test_import_rejects_malformed_bytes(m35):
+    from pagoda_amd import PagodaError
+
+    model, oracle = m35
+    s = model.new_session()
+    s.forward([1, 2, 3])
+    blob = s.export_kv()
+    for bad in (b"\x02" + blob[1:], blob + b"\x00", blob[:-4], blob[:16] + b"\x07" + blob[17:]):
+        with pytest.raises(PagodaError):
+            model.import_session(bad)
+    s.free()
 
 
 def test_argument_errors_are_atomic(m35):
