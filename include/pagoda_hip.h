@@ -114,6 +114,18 @@ int pgd_matrix_gemv_act_dev(const pgd_matrix* m, const void* act, int nrows, flo
                             int ldres);
 int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up, const void* act, int nrows,
                                    float* mid, int ldm);
+/* No counterpart in the reference. pgd_matrix_gemv_act_dev for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the same kernels and results, with
+ * their scratch (split-K / stream-K partial sums) taken from one fixed
+ * pgd_noalloc_scratch_bytes() (40 MiB) device array per GPU, held until the
+ * process ends; calls no hipMalloc / hipFree. A launch needing more scratch
+ * (37..64-row launches of matrices over ~41000 rows) is PGD_ERR_SHAPE before anything
+ * runs. Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other threads, other device handles' streams) race. */
+size_t pgd_noalloc_scratch_bytes(void);
+int pgd_matrix_gemv_act_dev_noalloc(const pgd_matrix* m, const void* act, int nrows, float* y, int ldy,
+                                    const float* res, int ldres);
 
 /* ---- decode-step kernels (device pointers, queued on the device stream) ----
  * Gated-DeltaNet recurrence over a ragged batch: sequence i owns rows

@@ -2,6 +2,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -386,6 +388,71 @@ int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up,
     DeviceScope scope(gate->dev);
     A8Act a = a8_act_view(const_cast<void*>(act), nrows, gate->m.n_in);
     qmat_gemv_a8_swiglu(gate->m, up->m, a, mid, ldm, gate->dev->stream);
+  });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free A8 GEMV: the kernels' scratch (split-K and stream-K partial
+// sums, per-row scales) comes from one fixed device array per GPU instead of
+// the growing per-stream buffers, for callers that cannot allocate device
+// memory (code under graph capture, tight serving loops).
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScratchBytes = (size_t)40 << 20;
+// host-side name of the per-GPU array; its device address comes from
+// hipGetSymbolAddress on each device
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::map<int, uint8_t*> g_scratch_ptr;  // device ordinal -> that GPU's copy of scratch
+
+// the current device's copy of scratch, looked up once per device
+uint8_t* scratch_on_current_device() {
+  int dev = 0;
+  PGD_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it != g_scratch_ptr.end()) return it->second;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  PGD_CHECK(e == hipSuccess && p, kErrState, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+  g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  return static_cast<uint8_t*>(p);
+}
+
+struct ArenaScope {
+  gemv::ScratchArena arena;
+  gemv::ScratchArena* prev;
+  explicit ArenaScope(uint8_t* base, size_t cap) {
+    arena.base = base;
+    arena.cap = cap;
+    prev = gemv::set_scratch_arena(&arena);
+  }
+  ~ArenaScope() { gemv::set_scratch_arena(prev); }
+};
+}  // namespace
+
+extern "C" {
+
+size_t pgd_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int pgd_matrix_gemv_act_dev_noalloc(const pgd_matrix* m, const void* act, int nrows, float* y, int ldy,
+                                    const float* res, int ldres) {
+  return guard([&] {
+    PGD_CHECK(m && act && y && nrows > 0, kErrArg, "bad argument");
+    PGD_CHECK(m->m.fmt == FMT_A8, kErrFormat, "prepared activations feed A8 matrices");
+    PGD_CHECK(ldy >= m->m.n_out && (!res || ldres >= m->m.n_out), kErrShape, "gemv output stride");
+    const size_t need = qmat_gemv_a8_scratch(m->m, nrows, res != nullptr);
+    PGD_CHECK(need <= kScratchBytes, kErrShape,
+              std::to_string(nrows) + " rows of a " + std::to_string(m->m.n_out) + " x " + std::to_string(m->m.n_in) +
+                  " matrix need " + std::to_string(need) + " bytes of scratch, above the fixed " +
+                  std::to_string(kScratchBytes >> 20) + " MiB");
+    DeviceScope scope(m->dev);
+    ArenaScope arena(scratch_on_current_device(), kScratchBytes);
+    A8Act a = a8_act_view(const_cast<void*>(act), nrows, m->m.n_in);
+    qmat_gemv_a8(m->m, a, y, ldy, res, ldres, m->dev->stream);
   });
 }
 

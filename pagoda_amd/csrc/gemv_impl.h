@@ -442,12 +442,17 @@ bool q4k_mma_ok(const GemvArgs& a);
 void run_q4k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
 bool q6k_mma_ok(const GemvArgs& a, int epi);
 void run_q6k_mma(const GemvArgs& a, int nrows, int x_f16, int epi, hipStream_t s);
-// Per-stream device scratch for GEMV activation prep (grows, never shrinks;
-// growing drains the stream first).
-// per-stream device scratch that grows on demand (the stream is synchronized
+// Per-stream device scratch that grows on demand (the stream is synchronized
 // before a buffer is replaced). Slots are independent buffers: 0 for prepared
-// activations and small reductions, 1 for split-K partial sums.
+// activations and small reductions, 1 for split-K partial sums, 3 for
+// stream-K partial sums, 4 for attention chunk states, 5 for per-row scales.
 void* gemv_scratch(hipStream_t s, size_t bytes, int slot = 0);
+// device scratch bytes (with per-slot alignment) one prepared-activation A8
+// GEMV of `rows` rows takes through run_a8_mma (epi EPI_STORE or EPI_RES, no
+// norm emission), following launch_prepped's choice of kernels
+size_t a8_scratch_need(const GemvArgs& a, int rows, int epi);
+// stream-K scratch of one 5..32-row chunk (slots 3 and 5, unaligned sizes)
+void sk_scratch_need(const GemvArgs& a, int nb, int epi, size_t* slot3, size_t* slot5);
 // A8 on the matrix cores (f32 activations)
 void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s);
 // Stream-K A8 kernel: whether a matrix takes it for 5..32-row launches, and

@@ -999,6 +999,38 @@ void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s) {
   else launch_prepped<EPI_STORE>(a, act, s);
 }
 
+size_t a8_scratch_need(const GemvArgs& a, int rows, int epi) {
+  PGD_CHECK(epi != EPI_SWIGLU && !a.nact.XA, kErrArg, "scratch bound covers plain and residual GEMVs");
+  size_t slot[8] = {};
+  auto need = [&](int i, size_t b) { slot[i] = std::max(slot[i], b); };
+  const bool sk = a8_sk_wanted(a, epi);
+  const bool pairs = !sk && a.n_out % 4 == 0;
+  const int tiles = (a.n_out + 31) / 32, G = a.n_in / 64, KS = split_ranges(a);
+  // the chunk loop and kernel choice of launch_prepped / launch_chunk_ks
+  for (; rows > 0;) {
+    int nb;
+    if (pairs && rows > 36) {
+      nb = rows < 64 ? rows : 64;
+      need(1, (size_t)KS * nb * a.n_out * sizeof(float));
+    } else {
+      nb = rows < 32 ? rows : 32;
+      if (sk && nb >= 5) {
+        size_t s3 = 0, s5 = 0;
+        sk_scratch_need(a, nb, epi, &s3, &s5);
+        need(3, s3);
+        need(5, s5);
+      } else if (nb > 4 && a.n_out % 4 == 0 && !(nb <= 16 && tiles < 256 && G < 256)) {
+        need(1, (size_t)KS * nb * a.n_out * sizeof(float));
+      }
+    }
+    rows -= nb;
+  }
+  size_t total = 0;
+  for (size_t b : slot)
+    if (b) total = ((total + 255) & ~(size_t)255) + b;
+  return total;
+}
+
 }  // namespace gemv
 
 // operands | constants | deferred-norm row sums ([rows][K / 32], 256 B aligned)

@@ -441,6 +441,20 @@ bool a8_sk_wanted(const GemvArgs& a, int epi) {
   return epi == EPI_SWIGLU || (a.n_out + 31) / 32 >= 2048;
 }
 
+void sk_scratch_need(const GemvArgs& a, int nb, int epi, size_t* slot3, size_t* slot5) {
+  static_assert(Geo<1, false>::NF == 4 && Geo<2, false>::NF == 8 && Geo<1, true>::NF == 4 && Geo<2, true>::NF == 8 &&
+                    Geo<1, true>::TPB == kWaves && Geo<1, false>::TPB == 2 * kWaves,
+                "scratch bound follows Geo");
+  const bool dual = epi == EPI_SWIGLU;
+  // launch_chunk_sk: MODE 1 up to 16 rows, MODE 2 above
+  const int TPB = kWaves * (dual ? 1 : 2), NF = 4 * (nb <= 16 ? 1 : 2);
+  const long long nblocks = ((a.n_out + 31) / 32 + TPB - 1) / TPB;
+  const long long U = nblocks * (a.n_in / 64);
+  const long long nwg = std::min<long long>(cu_count(), U);
+  *slot3 = (size_t)nwg * 2 * kWaves * NF * 64 * sizeof(f4);
+  *slot5 = a.rss ? 32 * sizeof(float) : 0;
+}
+
 void run_a8_sk_chunk(const GemvArgs& a_in, const uint4* XA, const float* CA, int nb, int epi, hipStream_t s) {
   PGD_CHECK(nb >= 5 && nb <= 32, kErrArg, "stream-K A8 GEMV takes 5..32 rows per launch");
   GemvArgs a = a_in;

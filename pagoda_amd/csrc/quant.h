@@ -160,6 +160,8 @@ A8Act a8_gnorm_prep(const float* x, int ldx, int rows, int n, const float* w, fl
 A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps, float* y,
                    int ldy, void* buf, hipStream_t s);
 void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const float* res, int ldres, hipStream_t s);
+// device scratch bytes qmat_gemv_a8 takes for `rows` rows (res: residual form)
+size_t qmat_gemv_a8_scratch(const QMat& m, int rows, bool res);
 // qmat_gemv_a8 (store) of 1..4 rows for a step where row r is the only token
 // of sequence r: outputs n < conv_n of row r also take the causal conv step of channel n
 // (the conv_step arithmetic): weights conv_w [conv_n][kernel], state at
@@ -188,5 +190,20 @@ void qmat_synth_rows(QMat& m, int row0, int rows, uint64_t seed, uint64_t key, f
 void synth_normal_f32(float* out, size_t n, uint64_t seed, uint64_t key, float scale, hipStream_t s);
 void synth_uniform_f32(float* out, size_t n, uint64_t seed, uint64_t key, float scale, hipStream_t s);
 void fill_f32(float* out, size_t n, float v, hipStream_t s);
+
+namespace gemv {
+// A caller-provided device region that gemv::gemv_scratch carves its slots from,
+// on the calling thread only, instead of allocating: each slot gets one
+// 256-byte aligned range on first use and keeps it while it is large enough
+// (launches on one stream run in order, so reusing a slot is safe as with the
+// allocating path). Exhausting the region throws kErrShape.
+struct ScratchArena {
+  uint8_t* base = nullptr;
+  size_t cap = 0, used = 0;
+  size_t off[8] = {}, len[8] = {};
+};
+// install (nullptr: back to allocating); returns the previous arena
+ScratchArena* set_scratch_arena(ScratchArena* a);
+}  // namespace gemv
 
 }  // namespace pgd

@@ -413,7 +413,29 @@ __global__ void fill_kernel(float* out, size_t n, float v) {
 
 // ---------------------------------------------------------------------------
 namespace gemv {
+namespace {
+thread_local ScratchArena* t_arena = nullptr;
+}
+
+ScratchArena* set_scratch_arena(ScratchArena* a) {
+  ScratchArena* old = t_arena;
+  t_arena = a;
+  return old;
+}
+
 void* gemv_scratch(hipStream_t s, size_t bytes, int slot) {
+  if (ScratchArena* ar = t_arena) {
+    PGD_CHECK(slot >= 0 && slot < 8, kErrArg, "scratch slot");
+    if (ar->len[slot] < bytes) {
+      const size_t at = (ar->used + 255) & ~(size_t)255;
+      PGD_CHECK(at + bytes <= ar->cap, kErrShape,
+                "launch needs more than the " + std::to_string(ar->cap >> 20) + " MiB of fixed scratch");
+      ar->off[slot] = at;
+      ar->len[slot] = bytes;
+      ar->used = at + bytes;
+    }
+    return ar->base + ar->off[slot];
+  }
   static std::mutex mu;
   static std::map<std::pair<hipStream_t, int>, std::pair<void*, size_t>> bufs;
   std::lock_guard<std::mutex> lock(mu);
@@ -643,6 +665,11 @@ void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const floa
   a.res = res;
   a.ldres = ldres;
   run_a8_mma(a, act, res ? EPI_RES : EPI_STORE, s);
+}
+
+size_t qmat_gemv_a8_scratch(const QMat& m, int rows, bool res) {
+  PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "prepared activations feed A8 matrices");
+  return rows > 0 ? a8_scratch_need(make_args(m), rows, res ? EPI_RES : EPI_STORE) : 0;
 }
 
 void qmat_gemv_a8_conv(const QMat& m, const A8Act& act, float* y, int ldy, const float* conv_w,
