@@ -676,6 +676,167 @@ uint32_t ora_argmax_first(const float* x, int n) {
 }
 
 /* ------------------------------------------------------------------ */
+/* candle's CPU k-quant matmul: activations quantized to Q8_K            */
+/* ------------------------------------------------------------------ */
+/* On the CPU the reference keeps candle's quantized matmul for the Q4_K /
+ * Q6_K weights (pagoda-hf/src/qwen2_gguf.rs:280-289, QMatMul::from_qtensor):
+ * each activation row is quantized to the weight type's vec_dot_type, Q8_K
+ * (block_q8_K { f32 d; i8 qs[256]; i16 bsums[16]; }), and every output is an
+ * integer block dot scaled in f32. candle-core 0.8.4 (pagoda-hf/Cargo.lock:
+ * 165, not vendored here) restates GGML's published k-quant routines in
+ * quantized/k_quants.rs; this follows them:
+ *   BlockQ8K::from_float  = quantize_row_q8_K: amax = max|x| (first index
+ *     wins), max = the signed value there, iscale = -128/max,
+ *     q = min(127, round(iscale*x)) (round half away from zero, Rust's
+ *     f32::round), bsums = sums of 16, d = 1/iscale; amax 0 gives d 0, q 0.
+ *   BlockQ4K::vec_dot    = ggml_vec_dot_q4_K_q8_K (scalar form);
+ *   BlockQ6K::vec_dot    = ggml_vec_dot_q6_K_q8_K (scalar form).
+ * The integer parts are exact; SIMD builds (AVX2, NEON) sum the per-block f32
+ * terms in other orders, so a CPU build agrees with this to f32 rounding. */
+typedef struct {
+  float d;
+  int8_t qs[256];
+  int16_t bsums[16];
+} q8k_block;
+
+static void q8k_quantize_block(const float* x, q8k_block* y) {
+  float amax = 0.0f, max = 0.0f;
+  for (int j = 0; j < 256; ++j) {
+    float ax = fabsf(x[j]);
+    if (amax < ax) {
+      amax = ax;
+      max = x[j];
+    }
+  }
+  if (amax == 0.0f) {
+    memset(y, 0, sizeof *y);
+    return;
+  }
+  float iscale = -128.0f / max;
+  for (int j = 0; j < 256; ++j) {
+    float v = roundf(iscale * x[j]);
+    y->qs[j] = (int8_t)(v < 127.0f ? v : 127.0f);
+  }
+  for (int j = 0; j < 16; ++j) {
+    int sum = 0;
+    for (int i = 0; i < 16; ++i) sum += y->qs[16 * j + i];
+    y->bsums[j] = (int16_t)sum;
+  }
+  y->d = 1.0f / iscale;
+}
+
+/* One row of n_in activations (tail past n_in as zeros) -> nb Q8_K blocks,
+ * written as d (f32), qs (256 i8), bsums (16 i16) per block, 292 bytes. */
+void ora_q8k_quantize(const float* x, int n_in, uint8_t* out) {
+  int nb = ora_kq_blocks(n_in);
+  for (int b = 0; b < nb; ++b) {
+    float t[256];
+    for (int i = 0; i < 256; ++i) t[i] = b * 256 + i < n_in ? x[b * 256 + i] : 0.0f;
+    q8k_block y;
+    q8k_quantize_block(t, &y);
+    memcpy(out + (size_t)b * 292, &y.d, 4);
+    memcpy(out + (size_t)b * 292 + 4, y.qs, 256);
+    memcpy(out + (size_t)b * 292 + 260, y.bsums, 32);
+  }
+}
+
+static void q8k_unpack(const uint8_t* in, q8k_block* y) {
+  memcpy(&y->d, in, 4);
+  memcpy(y->qs, in + 4, 256);
+  memcpy(y->bsums, in + 260, 32);
+}
+
+static float vec_dot_q4k_q8k(const uint8_t* xb, const q8k_block* y, int nb) {
+  float sums[8] = {0}, sumf = 0.0f;
+  for (int i = 0; i < nb; ++i) {
+    const uint8_t* blk = xb + (size_t)i * ORA_Q4K_BYTES;
+    const uint8_t* q4 = blk + 16;
+    const int8_t* q8 = y[i].qs;
+    int8_t aux8[256];
+    int32_t aux32[8] = {0};
+    for (int j = 0; j < 4; ++j) {
+      for (int l = 0; l < 32; ++l) aux8[64 * j + l] = (int8_t)(q4[32 * j + l] & 0xF);
+      for (int l = 0; l < 32; ++l) aux8[64 * j + 32 + l] = (int8_t)(q4[32 * j + l] >> 4);
+    }
+    uint8_t scales[8], mins[8];
+    for (int j = 0; j < 8; ++j) q4k_get_scale_min(j, blk + 4, &scales[j], &mins[j]);
+    int sumi = 0;
+    for (int j = 0; j < 16; ++j) sumi += y[i].bsums[j] * mins[j / 2];
+    const int8_t* a = aux8;
+    for (int j = 0; j < 8; ++j) {
+      int32_t scale = scales[j];
+      for (int part = 0; part < 4; ++part) {
+        for (int l = 0; l < 8; ++l) aux32[l] += scale * (int16_t)(q8[l] * a[l]);
+        q8 += 8;
+        a += 8;
+      }
+    }
+    float d = ora_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8))) * y[i].d;
+    for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux32[l];
+    float dmin = ora_f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8))) * y[i].d;
+    sumf -= dmin * (float)sumi;
+  }
+  for (int l = 0; l < 8; ++l) sumf += sums[l];
+  return sumf;
+}
+
+static float vec_dot_q6k_q8k(const uint8_t* xb, const q8k_block* y, int nb) {
+  float sums[8] = {0}, sumf = 0.0f;
+  for (int i = 0; i < nb; ++i) {
+    const uint8_t* blk = xb + (size_t)i * ORA_Q6K_BYTES;
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    const int8_t* q8 = y[i].qs;
+    int8_t aux8[256];
+    int32_t aux32[8] = {0};
+    for (int h = 0; h < 2; ++h) {
+      int8_t* a = aux8 + 128 * h;
+      const uint8_t* q4 = ql + 64 * h;
+      const uint8_t* qq = qh + 32 * h;
+      for (int l = 0; l < 32; ++l) {
+        a[l + 0] = (int8_t)(((q4[l + 0] & 0xF) | (((qq[l] >> 0) & 3) << 4)) - 32);
+        a[l + 32] = (int8_t)(((q4[l + 32] & 0xF) | (((qq[l] >> 2) & 3) << 4)) - 32);
+        a[l + 64] = (int8_t)(((q4[l + 0] >> 4) | (((qq[l] >> 4) & 3) << 4)) - 32);
+        a[l + 96] = (int8_t)(((q4[l + 32] >> 4) | (((qq[l] >> 6) & 3) << 4)) - 32);
+      }
+    }
+    const int8_t* a = aux8;
+    for (int j = 0; j < 16; ++j) {
+      int scale = sc[j];
+      for (int part = 0; part < 2; ++part) {
+        for (int l = 0; l < 8; ++l) aux32[l] += scale * (int16_t)(q8[l] * a[l]);
+        q8 += 8;
+        a += 8;
+      }
+    }
+    uint16_t dh;
+    memcpy(&dh, blk + 208, 2);
+    float d = ora_f16_to_f32(dh) * y[i].d;
+    for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux32[l];
+  }
+  for (int l = 0; l < 8; ++l) sumf += sums[l];
+  return sumf;
+}
+
+/* fmt 1 (Q4_K) / 2 (Q6_K): y[r] = vec_dot(row r's blocks, q8k) for rows rows. */
+void ora_kq_vec_dot_q8k(int fmt, const uint8_t* blocks, int rows, int n_in, const uint8_t* q8k, float* y) {
+  int nb = ora_kq_blocks(n_in);
+  q8k_block* yb = (q8k_block*)malloc(sizeof(q8k_block) * (size_t)nb);
+  for (int b = 0; b < nb; ++b) q8k_unpack(q8k + (size_t)b * 292, &yb[b]);
+  size_t bb = fmt == 1 ? ORA_Q4K_BYTES : ORA_Q6K_BYTES;
+  for (int r = 0; r < rows; ++r)
+    y[r] = fmt == 1 ? vec_dot_q4k_q8k(blocks + (size_t)r * nb * bb, yb, nb)
+                    : vec_dot_q6k_q8k(blocks + (size_t)r * nb * bb, yb, nb);
+  free(yb);
+}
+
+/* 0: f32 dequant-then-dot (the Metal/hybrid arithmetic, config 2's check);
+ * 1: Q4_K/Q6_K matrices through candle's CPU Q8_K kernel above. */
+static int g_kquant_mode = 0;
+void ora_set_kquant_mode(int mode) { g_kquant_mode = mode; }
+
+/* ------------------------------------------------------------------ */
 /* quantized matrices                                                   */
 /* ------------------------------------------------------------------ */
 enum { FMT_A8 = 0, FMT_Q4K = 1, FMT_Q6K = 2, FMT_Q8_0 = 3, FMT_Q5_0 = 4 };
@@ -751,6 +912,25 @@ static const void* qmat_part(const qmat* m, int part) {
  * loop; linear() at 1163-1179 goes through a dequantized f32 matmul). */
 static void qmat_linear(const qmat* m, const float* x, int seq, float* y) {
   const int chunk = 256;
+  if (g_kquant_mode == 1 && (m->fmt == FMT_Q4K || m->fmt == FMT_Q6K)) {
+    int nb = ora_kq_blocks(m->n_in);
+    size_t bb = m->fmt == FMT_Q4K ? ORA_Q4K_BYTES : ORA_Q6K_BYTES;
+    for (int t = 0; t < seq; ++t) {
+      q8k_block* yb = (q8k_block*)malloc(sizeof(q8k_block) * (size_t)nb);
+      const float* xv = x + (size_t)t * m->n_in;
+      for (int b = 0; b < nb; ++b) {
+        float tb[256];
+        for (int i = 0; i < 256; ++i) tb[i] = b * 256 + i < m->n_in ? xv[b * 256 + i] : 0.0f;
+        q8k_quantize_block(tb, &yb[b]);
+      }
+#pragma omp parallel for schedule(static)
+      for (int r = 0; r < m->n_out; ++r)
+        y[(size_t)t * m->n_out + r] = m->fmt == FMT_Q4K ? vec_dot_q4k_q8k(m->blocks + (size_t)r * nb * bb, yb, nb)
+                                                        : vec_dot_q6k_q8k(m->blocks + (size_t)r * nb * bb, yb, nb);
+      free(yb);
+    }
+    return;
+  }
   int n_out = m->n_out, n_in = m->n_in;
 #pragma omp parallel
   {

@@ -130,6 +130,13 @@ const void* ora_qwen2_tensor(const ora_qwen2* m, int layer, int kind, int part);
  * 2 Q6_K, 3 Q8_0, 4 Q5_0), rows x n_in as before; returns 0 or -1 */
 int ora_qwen2_set_matrix(ora_qwen2* m, int layer, int kind, int fmt, const uint8_t* blocks);
 
+/* candle's CPU Q4_K/Q6_K matmul (activations quantized to Q8_K, integer
+ * block dots): q8k blocks are 292 bytes (f32 d, 256 i8, 16 i16 bsums). */
+void ora_q8k_quantize(const float* x, int n_in, uint8_t* out);
+void ora_kq_vec_dot_q8k(int fmt, const uint8_t* blocks, int rows, int n_in, const uint8_t* q8k, float* y);
+/* 0: f32 dequant GEMV for every format (default); 1: Q4_K / Q6_K through Q8_K. */
+void ora_set_kquant_mode(int mode);
+
 /* greedy tie rule of the engine sampler: first max over finite values
  * (pagoda/src/sampler.rs:59-69). */
 uint32_t ora_argmax_first(const float* x, int n);

@@ -90,6 +90,9 @@ def lib():
         _lib.ora_qwen35_cache_len.argtypes = [C.c_void_p]
         _lib.ora_argmax_first.restype = C.c_uint32
         _lib.ora_argmax_first.argtypes = [C.c_void_p, C.c_int]
+        _lib.ora_q8k_quantize.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
+        _lib.ora_kq_vec_dot_q8k.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+        _lib.ora_set_kquant_mode.argtypes = [C.c_int]
         _lib.ora_num_threads.restype = C.c_int
         _lib.ora_rope_cos_sin.argtypes = [C.c_int, C.c_int, C.c_float, C.c_void_p, C.c_void_p]
     return _lib
@@ -179,6 +182,31 @@ def f32_to_bf16(x: float) -> int:
 
 def bf16_to_f32(h: int) -> float:
     return lib().ora_bf16_to_f32(h)
+
+
+Q8K_DTYPE = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16)])
+
+
+def q8k_quantize(x: np.ndarray) -> np.ndarray:
+    """candle's BlockQ8K::from_float of one activation row (tail padded with
+    zeros) -> structured array of blocks (d, qs, bsums)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(kq_blocks(x.size) * 292, np.uint8)
+    lib().ora_q8k_quantize(_p(x), x.size, _p(out))
+    return out.view(Q8K_DTYPE)
+
+
+def kq_vec_dot_q8k(fmt: int, blocks: np.ndarray, n_out: int, n_in: int, q8k: np.ndarray) -> np.ndarray:
+    """candle's CPU Q4_K (fmt 1) / Q6_K (fmt 2) x Q8_K block dot per weight row."""
+    y = np.empty(n_out, np.float32)
+    q = np.ascontiguousarray(q8k).view(np.uint8)
+    lib().ora_kq_vec_dot_q8k(fmt, _p(np.ascontiguousarray(blocks, np.uint8)), n_out, n_in, _p(q), _p(y))
+    return y
+
+
+def set_kquant_mode(mode: int) -> None:
+    """0: f32 dequant GEMV (default); 1: Q4_K / Q6_K through candle's Q8_K CPU kernel."""
+    lib().ora_set_kquant_mode(int(mode))
 
 
 def f32_to_f16(x: float) -> int:
