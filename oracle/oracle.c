@@ -200,14 +200,15 @@ void ora_a8_dequant(const uint32_t* packed, const uint16_t* scales, const uint16
     const uint16_t* srow = scales + (size_t)(row0 + r) * groups;
     const uint16_t* brow = biases + (size_t)(row0 + r) * groups;
     float* o = out + (size_t)r * n_in;
-    int i = 0;
-    for (int wi = 0; wi < words; ++wi) {
-      for (int k = 0; k < 4; ++k) {
-        float code = (float)((row[wi] >> (8 * k)) & 255u);
-        int g = i / A8_GROUP;
-        o[i] = ora_bf16_to_f32(brow[g]) + ora_bf16_to_f32(srow[g]) * code;
-        ++i;
-      }
+    (void)words;
+    /* code i is byte i % 4 of word i / 4, little-endian: on this
+     * (little-endian) host, byte i of the row */
+    const uint8_t* codes = (const uint8_t*)row;
+    for (int g = 0; g < groups; ++g) {
+      const float sc = ora_bf16_to_f32(srow[g]), bi = ora_bf16_to_f32(brow[g]);
+      const uint8_t* cg = codes + (size_t)g * A8_GROUP;
+      float* og = o + (size_t)g * A8_GROUP;
+      for (int j = 0; j < A8_GROUP; ++j) og[j] = bi + sc * (float)cg[j];
     }
   }
 }
@@ -932,23 +933,45 @@ static void qmat_linear(const qmat* m, const float* x, int seq, float* y) {
     return;
   }
   int n_out = m->n_out, n_in = m->n_in;
+  /* R output rows at a time: their dequantized weights transposed to
+   * [n_in][R] so the R dot products advance together (one SIMD lane
+   * each). Every output is still the sequential sum over i = 0..n_in-1 of
+   * x[i]*w[i], rounded after each product and each add, in that order. */
+  (void)chunk;
+  /* 32 rows (16 for long rows, to stay in L2): several independent 8-wide
+   * accumulator chains per i */
+  const int R = n_in <= 8192 ? 32 : 16;
 #pragma omp parallel
   {
-    float* rows = (float*)malloc(sizeof(float) * (size_t)chunk * n_in);
-#pragma omp for schedule(static)
-    for (int c0 = 0; c0 < n_out; c0 += chunk) {
-      int n = n_out - c0 < chunk ? n_out - c0 : chunk;
+    float* rows = (float*)malloc(sizeof(float) * (size_t)R * n_in);
+    float* wt = (float*)malloc(sizeof(float) * (size_t)R * n_in);
+#pragma omp for schedule(dynamic, 16)
+    for (int c0 = 0; c0 < n_out; c0 += R) {
+      int n = n_out - c0 < R ? n_out - c0 : R;
       qmat_dequant(m, c0, n, rows);
-      for (int t = 0; t < seq; ++t)
-        for (int r = 0; r < n; ++r) {
-          const float* w = rows + (size_t)r * n_in;
-          const float* xv = x + (size_t)t * n_in;
-          float dot = 0.0f;
-          for (int i = 0; i < n_in; ++i) dot += xv[i] * w[i];
-          y[(size_t)t * n_out + c0 + r] = dot;
+      for (int i = 0; i < n_in; ++i)
+        for (int r = 0; r < R; ++r) wt[(size_t)i * R + r] = r < n ? rows[(size_t)r * n_in + i] : 0.0f;
+      for (int t = 0; t < seq; ++t) {
+        const float* xv = x + (size_t)t * n_in;
+        float acc[32] = {0};
+        if (R == 32) {
+          for (int i = 0; i < n_in; ++i) {
+            const float xi = xv[i];
+            const float* w = wt + (size_t)i * 32;
+            for (int r = 0; r < 32; ++r) acc[r] += xi * w[r];
+          }
+        } else {
+          for (int i = 0; i < n_in; ++i) {
+            const float xi = xv[i];
+            const float* w = wt + (size_t)i * 16;
+            for (int r = 0; r < 16; ++r) acc[r] += xi * w[r];
+          }
         }
+        for (int r = 0; r < n; ++r) y[(size_t)t * n_out + c0 + r] = acc[r];
+      }
     }
     free(rows);
+    free(wt);
   }
 }
 

@@ -104,3 +104,68 @@ def test_config4_widths_one_layer_group(dev):
         got = s.forward([t])
         ref = oracle.forward([t], oc)
         assert rel(got, ref) < LOGIT_TOL, (step, rel(got, ref))
+
+
+def _elementwise_ok(got, ref, tol=1e-3):
+    """|d| <= tol*|ref| + atol per logit, atol = 0.1 * tol * max|ref|."""
+    g, r = got.astype(np.float64), ref.astype(np.float64)
+    return bool(np.all(np.abs(g - r) <= tol * np.abs(r) + 0.1 * tol * np.abs(r).max()))
+
+
+def test_config4_full_depth_greedy_32_and_batch32(dev, capsys):
+    """Config 4 at full size (64 layers, vocab 151936) against the oracle on
+    the same seeded weights: 19-token prompt, 32 greedy tokens at batch 1,
+    logits within 1e-3 at every step (the reference's own check,
+    examples/qwen3_8.rs:219-247, 314-326). Then one batch-32 decode step
+    whose rows equal their batch-1 counterparts within the 1e-5 class with
+    the same greedy ids."""
+    import time
+    from dataclasses import replace
+
+    from pagoda_amd.engine import QWEN35_27B, Model, argmax_first
+
+    def say(msg):
+        with capsys.disabled():
+            print(f"\n[config4 full depth] {msg}", flush=True)
+
+    cfg = replace(QWEN35_27B, max_pos=512, kv_blocks=256)
+    seed = 4
+    t0 = time.time()
+    model = Model.synth(dev, cfg, seed)
+    say(f"device model built ({time.time() - t0:.1f} s)")
+    oracle = ora.Qwen35(ora.Qwen35Config(), seed)
+    say(f"oracle model built ({time.time() - t0:.1f} s, {ora.lib().ora_num_threads()} threads)")
+    prompt = np.random.default_rng(19).integers(0, cfg.vocab, 19)
+    s = model.new_session()
+    oc = oracle.new_cache()
+    got, ref = s.forward(prompt), oracle.forward(prompt, oc)
+    margins = []
+    for step in range(32):
+        assert rel(got, ref) < LOGIT_TOL, (step, rel(got, ref))
+        assert _elementwise_ok(got, ref), step
+        tg, tr = argmax_first(got), ora.argmax_first(ref)
+        margins.append(margin(ref))
+        assert tg == tr, f"step {step}: gpu {tg} oracle {tr} (margin {margins[-1]:.3g})"
+        if step == 31:
+            break
+        got, ref = s.forward([tg]), oracle.forward([tr], oc)
+        if step % 8 == 7:
+            say(f"step {step + 1}/32 equal ({time.time() - t0:.1f} s)")
+    say(f"32 greedy ids equal, min top-2 margin {min(margins):.4g}")
+    s.free()
+    del oracle, oc
+    # batch 32: distinct prompts, then one decode step batched vs alone
+    rng = np.random.default_rng(32)
+    sess = [model.new_session() for _ in range(32)]
+    ids, _ = model.step_ragged(sess, [rng.integers(0, cfg.vocab, 19) for _ in range(32)])
+    alone = [x.fork() for x in sess]
+    feed = [[int(t)] for t in ids]
+    bid, blog = model.step_ragged(sess, feed, want_logits=True)
+    for i in range(32):
+        lg = alone[i].forward(feed[i])
+        assert rel(blog[i], lg) < 1e-5, i
+        assert int(bid[i]) == argmax_first(lg), i
+    for x in sess + alone:
+        x.free()
+    model.free()
+    say(f"batch-32 step rows match batch 1 ({time.time() - t0:.1f} s)")
