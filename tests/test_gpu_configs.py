@@ -153,19 +153,33 @@ def test_config4_full_depth_greedy_32_and_batch32(dev, capsys):
             say(f"step {step + 1}/32 equal ({time.time() - t0:.1f} s)")
     say(f"32 greedy ids equal, min top-2 margin {min(margins):.4g}")
     s.free()
-    del oracle, oc
-    # batch 32: distinct prompts, then one decode step batched vs alone
+    # batch 32: distinct prompts, then one decode step batched vs alone. The
+    # 32-row launches take other kernels (split-K shared-operand, stream-K)
+    # than 1-row launches; each is within fp32 rounding of the other per
+    # layer, which over 64 layers stays below 1e-4 of the logits' scale.
     rng = np.random.default_rng(32)
+    prompts = [rng.integers(0, cfg.vocab, 19) for _ in range(32)]
     sess = [model.new_session() for _ in range(32)]
-    ids, _ = model.step_ragged(sess, [rng.integers(0, cfg.vocab, 19) for _ in range(32)])
+    ids, _ = model.step_ragged(sess, prompts)
     alone = [x.fork() for x in sess]
     feed = [[int(t)] for t in ids]
     bid, blog = model.step_ragged(sess, feed, want_logits=True)
+    worst = 0.0
     for i in range(32):
         lg = alone[i].forward(feed[i])
-        assert rel(blog[i], lg) < 1e-5, i
+        worst = max(worst, rel(blog[i], lg))
+        assert rel(blog[i], lg) < 1e-4, i
         assert int(bid[i]) == argmax_first(lg), i
+    say(f"batch-32 rows vs batch 1: max rel {worst:.2e}")
+    # two batch-32 rows against the oracle
+    for i in (0, 31):
+        c = oracle.new_cache()
+        r = oracle.forward(prompts[i], c)
+        assert ora.argmax_first(r) == int(ids[i]), i
+        r = oracle.forward(feed[i], c)
+        assert rel(blog[i], r) < LOGIT_TOL and _elementwise_ok(blog[i], r), i
+        assert ora.argmax_first(r) == int(bid[i]), i
     for x in sess + alone:
         x.free()
     model.free()
-    say(f"batch-32 step rows match batch 1 ({time.time() - t0:.1f} s)")
+    say(f"batch-32 step checked ({time.time() - t0:.1f} s)")
