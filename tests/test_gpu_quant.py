@@ -18,7 +18,12 @@ GEMV_TOL = 1e-3
 
 
 def rel_err(y, ref):
-    return float(np.abs(y.astype(np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+    """The larger of max|d| / max|ref| and the elementwise ratio
+    max_i |d_i| / (|ref_i| + 0.1 max|ref|): below tol means every output is
+    within tol of itself plus an absolute 0.1 * tol * max|ref|."""
+    d = np.abs(y.astype(np.float64) - ref)
+    scale = max(np.abs(ref).max(), 1e-30)
+    return float(max(d.max() / scale, (d / (np.abs(ref) + 0.1 * scale)).max()))
 
 
 def make(dev, fmt, w):
