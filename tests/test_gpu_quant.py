@@ -167,7 +167,7 @@ def test_shared_x_two_matrices_and_residual(dev):
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
-@pytest.mark.parametrize("shape", [(4864, 896), (896, 4864), (1152, 896)])
+@pytest.mark.parametrize("shape", [(4864, 896), (896, 4864), (1152, 896), (151936, 896)])
 @pytest.mark.parametrize("rows", [1, 4, 8, 16, 32, 64])
 def test_config2_sweep_f16_activations(dev, fmt, shape, rows):
     """Config 2: Q4K/Q6K, x fp16 N(0,1), ragged rows, vs CPU-dequant fp32 GEMV
