@@ -832,8 +832,74 @@ void ora_kq_vec_dot_q8k(int fmt, const uint8_t* blocks, int rows, int n_in, cons
   free(yb);
 }
 
+/* The 32-weight types' vec_dot_type is Q8_0 (block_q8_0 { f16 d; i8 qs[32]; }):
+ * BlockQ8_0::from_float = quantize_row_q8_0: amax = max|x|, d = amax/127,
+ * id = 1/d (0 when d is 0), q = round(x*id) (half away from zero), d stored
+ * as f16. vec_dot_q8_0_q8_0 / vec_dot_q5_0_q8_0 (scalar forms): per block
+ * sumi = integer dot (Q5_0 codes are the nibble with its qh bit as bit 4,
+ * minus 16), then sumf += sumi * d_w * d_x in f32 over the blocks in order. */
+static void q8_0_quantize_block(const float* x, uint16_t* dh, int8_t* qs) {
+  float amax = 0.0f;
+  for (int j = 0; j < 32; ++j) {
+    float ax = fabsf(x[j]);
+    if (ax > amax) amax = ax;
+  }
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  for (int j = 0; j < 32; ++j) qs[j] = (int8_t)roundf(x[j] * id);
+  *dh = ora_f32_to_f16(d);
+}
+
+/* One row (n_in % 32 == 0) -> n_in/32 blocks of 34 bytes (f16 d, 32 i8). */
+void ora_q8_0_quantize_act(const float* x, int n_in, uint8_t* out) {
+  for (int b = 0; b < n_in / 32; ++b) {
+    uint16_t dh;
+    q8_0_quantize_block(x + 32 * b, &dh, (int8_t*)(out + (size_t)b * 34 + 2));
+    memcpy(out + (size_t)b * 34, &dh, 2);
+  }
+}
+
+static float vec_dot_q8_0_q8_0(const uint8_t* xb, const uint8_t* yb, int nb) {
+  float sumf = 0.0f;
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* x = xb + (size_t)b * ORA_Q8_0_BYTES;
+    const uint8_t* y = yb + (size_t)b * 34;
+    int sumi = 0;
+    for (int j = 0; j < 32; ++j) sumi += (int)(int8_t)x[2 + j] * (int)(int8_t)y[2 + j];
+    sumf += (float)sumi * ora_f16_to_f32((uint16_t)(x[0] | (x[1] << 8))) * ora_f16_to_f32((uint16_t)(y[0] | (y[1] << 8)));
+  }
+  return sumf;
+}
+
+static float vec_dot_q5_0_q8_0(const uint8_t* xb, const uint8_t* yb, int nb) {
+  float sumf = 0.0f;
+  for (int b = 0; b < nb; ++b) {
+    const uint8_t* x = xb + (size_t)b * ORA_Q5_0_BYTES;
+    const uint8_t* y = yb + (size_t)b * 34;
+    const uint32_t qh = (uint32_t)x[2] | ((uint32_t)x[3] << 8) | ((uint32_t)x[4] << 16) | ((uint32_t)x[5] << 24);
+    int sumi = 0;
+    for (int j = 0; j < 16; ++j) {
+      const int x0 = (int)((x[6 + j] & 15u) | (((qh >> j) & 1u) << 4)) - 16;
+      const int x1 = (int)((x[6 + j] >> 4) | (((qh >> (j + 16)) & 1u) << 4)) - 16;
+      sumi += x0 * (int)(int8_t)y[2 + j] + x1 * (int)(int8_t)y[2 + j + 16];
+    }
+    sumf += (float)sumi * ora_f16_to_f32((uint16_t)(x[0] | (x[1] << 8))) * ora_f16_to_f32((uint16_t)(y[0] | (y[1] << 8)));
+  }
+  return sumf;
+}
+
+/* fmt 3 (Q8_0) / 4 (Q5_0): y[r] = vec_dot(row r's blocks, q8_0 activation blocks). */
+void ora_q8_0_vec_dot(int fmt, const uint8_t* blocks, int rows, int n_in, const uint8_t* q8, float* y) {
+  const int nb = n_in / 32;
+  const size_t bb = fmt == 3 ? ORA_Q8_0_BYTES : ORA_Q5_0_BYTES;
+  for (int r = 0; r < rows; ++r)
+    y[r] = fmt == 3 ? vec_dot_q8_0_q8_0(blocks + (size_t)r * nb * bb, q8, nb)
+                    : vec_dot_q5_0_q8_0(blocks + (size_t)r * nb * bb, q8, nb);
+}
+
 /* 0: f32 dequant-then-dot (the Metal/hybrid arithmetic, config 2's check);
- * 1: Q4_K/Q6_K matrices through candle's CPU Q8_K kernel above. */
+ * 1: candle's CPU quantized matmul: Q4_K/Q6_K through Q8_K activations,
+ *    Q8_0/Q5_0 through Q8_0 activations. */
 static int g_kquant_mode = 0;
 void ora_set_kquant_mode(int mode) { g_kquant_mode = mode; }
 
@@ -930,6 +996,20 @@ static void qmat_linear(const qmat* m, const float* x, int seq, float* y) {
                                                         : vec_dot_q6k_q8k(m->blocks + (size_t)r * nb * bb, yb, nb);
       free(yb);
     }
+    return;
+  }
+  if (g_kquant_mode == 1 && (m->fmt == FMT_Q8_0 || m->fmt == FMT_Q5_0)) {
+    const int nb = m->n_in / 32;
+    const size_t bb = m->fmt == FMT_Q8_0 ? ORA_Q8_0_BYTES : ORA_Q5_0_BYTES;
+    uint8_t* q8 = (uint8_t*)malloc((size_t)nb * 34);
+    for (int t = 0; t < seq; ++t) {
+      ora_q8_0_quantize_act(x + (size_t)t * m->n_in, m->n_in, q8);
+#pragma omp parallel for schedule(static)
+      for (int r = 0; r < m->n_out; ++r)
+        y[(size_t)t * m->n_out + r] = m->fmt == FMT_Q8_0 ? vec_dot_q8_0_q8_0(m->blocks + (size_t)r * nb * bb, q8, nb)
+                                                         : vec_dot_q5_0_q8_0(m->blocks + (size_t)r * nb * bb, q8, nb);
+    }
+    free(q8);
     return;
   }
   int n_out = m->n_out, n_in = m->n_in;

@@ -134,7 +134,12 @@ int ora_qwen2_set_matrix(ora_qwen2* m, int layer, int kind, int fmt, const uint8
  * block dots): q8k blocks are 292 bytes (f32 d, 256 i8, 16 i16 bsums). */
 void ora_q8k_quantize(const float* x, int n_in, uint8_t* out);
 void ora_kq_vec_dot_q8k(int fmt, const uint8_t* blocks, int rows, int n_in, const uint8_t* q8k, float* y);
-/* 0: f32 dequant GEMV for every format (default); 1: Q4_K / Q6_K through Q8_K. */
+/* Q8_0 activations (34-byte blocks: f16 d, 32 i8) and the Q8_0 (fmt 3) /
+ * Q5_0 (fmt 4) x Q8_0 block dots of the same kernel family. */
+void ora_q8_0_quantize_act(const float* x, int n_in, uint8_t* out);
+void ora_q8_0_vec_dot(int fmt, const uint8_t* blocks, int rows, int n_in, const uint8_t* q8, float* y);
+/* 0: f32 dequant GEMV for every format (default); 1: candle's CPU quantized
+ * matmul (Q4_K / Q6_K through Q8_K, Q8_0 / Q5_0 through Q8_0 activations). */
 void ora_set_kquant_mode(int mode);
 
 /* greedy tie rule of the engine sampler: first max over finite values

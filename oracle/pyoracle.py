@@ -93,6 +93,8 @@ def lib():
         _lib.ora_q8k_quantize.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
         _lib.ora_kq_vec_dot_q8k.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
         _lib.ora_set_kquant_mode.argtypes = [C.c_int]
+        _lib.ora_q8_0_quantize_act.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
+        _lib.ora_q8_0_vec_dot.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
         _lib.ora_num_threads.restype = C.c_int
         _lib.ora_rope_cos_sin.argtypes = [C.c_int, C.c_int, C.c_float, C.c_void_p, C.c_void_p]
     return _lib
@@ -201,6 +203,25 @@ def kq_vec_dot_q8k(fmt: int, blocks: np.ndarray, n_out: int, n_in: int, q8k: np.
     y = np.empty(n_out, np.float32)
     q = np.ascontiguousarray(q8k).view(np.uint8)
     lib().ora_kq_vec_dot_q8k(fmt, _p(np.ascontiguousarray(blocks, np.uint8)), n_out, n_in, _p(q), _p(y))
+    return y
+
+
+Q8_0_ACT_DTYPE = np.dtype([("d", "<u2"), ("qs", "i1", 32)])
+
+
+def q8_0_quantize_act(x: np.ndarray) -> np.ndarray:
+    """candle's BlockQ8_0::from_float of one activation row -> blocks (d f16 bits, qs)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(x.size // 32 * 34, np.uint8)
+    lib().ora_q8_0_quantize_act(_p(x), x.size, _p(out))
+    return out.view(Q8_0_ACT_DTYPE)
+
+
+def q8_0_vec_dot(fmt: int, blocks: np.ndarray, n_out: int, n_in: int, q8: np.ndarray) -> np.ndarray:
+    """candle's CPU Q8_0 (fmt 3) / Q5_0 (fmt 4) x Q8_0 block dot per weight row."""
+    y = np.empty(n_out, np.float32)
+    q = np.ascontiguousarray(q8).view(np.uint8)
+    lib().ora_q8_0_vec_dot(fmt, _p(np.ascontiguousarray(blocks, np.uint8)), n_out, n_in, _p(q), _p(y))
     return y
 
 

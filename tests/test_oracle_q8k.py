@@ -91,3 +91,44 @@ def test_model_switch_to_q8k_mode():
     np.testing.assert_array_equal(a, c)
     assert not np.array_equal(a, b)
     assert np.abs(a - b).max() < 0.05 * np.abs(a).max()
+
+
+# ------------------------------------------------ Q8_0 activations (32-weight types)
+def test_q8_0_activation_known_answers():
+    # amax 127 -> d = 1, id = 1: q = round(x), halves away from zero
+    x = np.zeros(32, np.float32)
+    x[:8] = [0.5, 1.5, 2.5, -0.5, -2.5, 126.49, -3.5, 127.0]
+    b = ora.q8_0_quantize_act(x)[0]
+    assert b["d"] == np.float16(1.0).view(np.uint16)
+    np.testing.assert_array_equal(b["qs"][:8], [1, 2, 3, -1, -3, 126, -4, 127])
+    # d = amax / 127 stored as f16; an all-zero block has d 0 and q 0
+    x = np.concatenate([np.full(32, 2.54, np.float32), np.zeros(32, np.float32)])
+    q = ora.q8_0_quantize_act(x)
+    assert q[0]["d"] == np.float16(np.float32(2.54) / np.float32(127)).view(np.uint16)
+    assert (q[0]["qs"] == 127).all() and q[1]["d"] == 0 and not q[1]["qs"].any()
+
+
+def test_q8_0_q5_0_dots():
+    from test_oracle_formats import q5_0_block, q8_0_block
+
+    w = np.frombuffer(q8_0_block(0.5, [2] * 32), np.uint8)
+    act = np.zeros(1, ora.Q8_0_ACT_DTYPE)
+    act["d"], act["qs"] = np.float16(1.0).view(np.uint16), 3
+    assert ora.q8_0_vec_dot(3, w, 1, 32, act)[0] == 96.0
+    j = np.arange(16)
+    w5 = np.frombuffer(q5_0_block(1.0, 0xFFFF0000, j | (j << 4)), np.uint8)  # weights 0..31 -> -16..15
+    act["qs"] = 1
+    assert ora.q8_0_vec_dot(4, w5, 1, 32, act)[0] == float(np.arange(32).sum() - 16 * 32)
+    # random blocks: the dot equals the fp64 value of the same integers
+    from checkpoints import GGML_Q5_0, GGML_Q8_0, random_blocks
+
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, 320).astype(np.float32)
+    q8 = ora.q8_0_quantize_act(x)
+    xq = np.concatenate([np.float16(0).view(np.uint16).dtype.type(b["d"]).view(np.float16).astype(np.float64)
+                         * b["qs"].astype(np.float64) for b in q8])
+    for fmt, gt, deq in ((3, GGML_Q8_0, ora.q8_0_dequant), (4, GGML_Q5_0, ora.q5_0_dequant)):
+        blk = random_blocks(rng, gt, 16, 320, d_std=0.01)
+        got = ora.q8_0_vec_dot(fmt, blk, 16, 320, q8)
+        ref = deq(blk, 16, 320).astype(np.float64) @ xq
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
