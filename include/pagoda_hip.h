@@ -114,6 +114,13 @@ int pgd_matrix_gemv_act_dev(const pgd_matrix* m, const void* act, int nrows, flo
                             int ldres);
 int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up, const void* act, int nrows,
                                    float* mid, int ldm);
+/* candle's CPU QMatMul::forward for GGUF weights (called at
+ * pagoda-hf/src/qwen2_gguf.rs:271-278, kept on the CPU by qweight at 280-289):
+ * each f32 activation row (stride ldx) is quantized to Q8_K (Q4_K / Q6_K
+ * weights) or Q8_0 (Q8_0 / Q5_0 weights), every output an integer block dot
+ * scaled in f32. res (nullable) adds a residual as in pgd_matrix_gemv_dev. */
+int pgd_matrix_gemv_q8act_dev(const pgd_matrix* m, const float* x, int ldx, int nrows, float* y, int ldy,
+                              const float* res, int ldres);
 /* No counterpart in the reference. pgd_matrix_gemv_act_dev for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): the same kernels and results, with
@@ -195,6 +202,14 @@ int pgd_model_load_gguf(pgd_dev* dev, const char* path, int max_pos, int kv_bloc
 int pgd_checkpoint_config(const char* path, int max_pos, int kv_blocks, pgd_model_config* cfg);
 /* The configuration of a model (synthetic or loaded). */
 int pgd_model_config_get(const pgd_model* m, pgd_model_config* cfg);
+/* Arithmetic of a model's GGML-format matrices (the Qwen2 GGUF path). The
+ * reference computes them two ways: candle's CPU quantized matmul
+ * (PGD_ARITH_CPU_Q8, activations quantized to Q8_K / Q8_0; the default for
+ * Qwen2 models, matching the reference CPU path's tokens) or dequantized
+ * weights (Metal, qwen2_gguf.rs:280-289), here f32 dequant-then-dot
+ * (PGD_ARITH_DEQUANT_F32). A8 (hybrid model) matrices are unaffected. */
+enum { PGD_ARITH_DEQUANT_F32 = 0, PGD_ARITH_CPU_Q8 = 1 };
+int pgd_model_set_kquant_arith(pgd_model* m, int mode);
 int pgd_model_free(pgd_model* m);
 /* weight bytes on the device, algorithmic weight bytes per decode step, KV pages free */
 int pgd_model_info(const pgd_model* m, size_t* weight_bytes, double* algo_bytes_per_token, int* kv_free);

@@ -901,7 +901,6 @@ void ora_q8_0_vec_dot(int fmt, const uint8_t* blocks, int rows, int n_in, const 
  * 1: candle's CPU quantized matmul: Q4_K/Q6_K through Q8_K activations,
  *    Q8_0/Q5_0 through Q8_0 activations. */
 static int g_kquant_mode = 0;
-void ora_set_kquant_mode(int mode) { g_kquant_mode = mode; }
 
 /* ------------------------------------------------------------------ */
 /* quantized matrices                                                   */
@@ -1555,6 +1554,7 @@ typedef struct {
 
 struct ora_qwen2 {
   ora_qwen2_config cfg;
+  int kquant_mode; /* qmat_linear arithmetic of this model's GGML matrices (see g_kquant_mode) */
   qmat embed; /* token_embd (Q6K), also the tied lm_head */
   float* final_norm;
   q2_layer* layers;
@@ -1838,7 +1838,19 @@ static void q2_rope(float* x, const float* cs, const float* sn, int hd) {
 /* pagoda-hf/src/qwen2_gguf.rs:142-166 (forward_tokens) and 206-266
  * (Block::forward, project, attend); SessionKv::push_kv appends K/V
  * (pagoda-hf/src/llama.rs:65). Matmuls use f32 dequantized weights. */
+void ora_qwen2_set_kquant_mode(ora_qwen2* m, int mode) { m->kquant_mode = mode; }
+
+static int q2_forward(ora_qwen2* m, const uint32_t* toks, int n, ora_qwen2_cache* cc, float* logits);
+
 int ora_qwen2_forward(ora_qwen2* m, const uint32_t* toks, int n, ora_qwen2_cache* cc, float* logits) {
+  const int saved = g_kquant_mode;
+  g_kquant_mode = m->kquant_mode;
+  const int rc = q2_forward(m, toks, n, cc, logits);
+  g_kquant_mode = saved;
+  return rc;
+}
+
+static int q2_forward(ora_qwen2* m, const uint32_t* toks, int n, ora_qwen2_cache* cc, float* logits) {
   const ora_qwen2_config* c = &m->cfg;
   int H = c->hidden, hd = c->head_dim, NH = c->heads, KVH = c->kv_heads, I = c->intermediate;
   int kvw = KVH * hd, half = hd / 2;

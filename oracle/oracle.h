@@ -140,7 +140,7 @@ void ora_q8_0_quantize_act(const float* x, int n_in, uint8_t* out);
 void ora_q8_0_vec_dot(int fmt, const uint8_t* blocks, int rows, int n_in, const uint8_t* q8, float* y);
 /* 0: f32 dequant GEMV for every format (default); 1: candle's CPU quantized
  * matmul (Q4_K / Q6_K through Q8_K, Q8_0 / Q5_0 through Q8_0 activations). */
-void ora_set_kquant_mode(int mode);
+void ora_qwen2_set_kquant_mode(ora_qwen2* m, int mode);
 
 /* greedy tie rule of the engine sampler: first max over finite values
  * (pagoda/src/sampler.rs:59-69). */

@@ -92,7 +92,7 @@ def lib():
         _lib.ora_argmax_first.argtypes = [C.c_void_p, C.c_int]
         _lib.ora_q8k_quantize.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
         _lib.ora_kq_vec_dot_q8k.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
-        _lib.ora_set_kquant_mode.argtypes = [C.c_int]
+        _lib.ora_qwen2_set_kquant_mode.argtypes = [C.c_void_p, C.c_int]
         _lib.ora_q8_0_quantize_act.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
         _lib.ora_q8_0_vec_dot.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
         _lib.ora_num_threads.restype = C.c_int
@@ -223,11 +223,6 @@ def q8_0_vec_dot(fmt: int, blocks: np.ndarray, n_out: int, n_in: int, q8: np.nda
     q = np.ascontiguousarray(q8).view(np.uint8)
     lib().ora_q8_0_vec_dot(fmt, _p(np.ascontiguousarray(blocks, np.uint8)), n_out, n_in, _p(q), _p(y))
     return y
-
-
-def set_kquant_mode(mode: int) -> None:
-    """0: f32 dequant GEMV (default); 1: Q4_K / Q6_K through candle's Q8_K CPU kernel."""
-    lib().ora_set_kquant_mode(int(mode))
 
 
 def f32_to_f16(x: float) -> int:
@@ -408,10 +403,18 @@ class Qwen35Cache:
 class Qwen2:
     """CPU restatement of Qwen2Gguf (pagoda-hf/src/qwen2_gguf.rs) on synthetic weights."""
 
-    def __init__(self, cfg: Qwen2Config, seed: int):
+    def __init__(self, cfg: Qwen2Config, seed: int, kquant_mode: int = 1):
+        """kquant_mode 1 (default): the reference CPU path's arithmetic,
+        candle's quantized matmul (activations quantized to Q8_K / Q8_0);
+        0: f32 dequant-then-dot."""
         self.cfg = cfg
         self._c = cfg.ctype()
         self.h = lib().ora_qwen2_new(C.byref(self._c), seed)
+        self.set_kquant_mode(kquant_mode)
+
+    def set_kquant_mode(self, mode: int) -> None:
+        self.kquant_mode = int(mode)
+        lib().ora_qwen2_set_kquant_mode(self.h, self.kquant_mode)
 
     def new_cache(self):
         return Qwen2Cache(lib().ora_qwen2_cache_new(self.h), self)

@@ -379,6 +379,17 @@ int pgd_matrix_gemv_act_dev(const pgd_matrix* m, const void* act, int nrows, flo
   });
 }
 
+int pgd_matrix_gemv_q8act_dev(const pgd_matrix* m, const float* x, int ldx, int nrows, float* y, int ldy,
+                              const float* res, int ldres) {
+  return guard([&] {
+    PGD_CHECK(m && x && y && nrows > 0, kErrArg, "bad argument");
+    PGD_CHECK(m->m.fmt != FMT_A8, kErrFormat, "quantized activations are for GGML-format matrices");
+    PGD_CHECK(ldy >= m->m.n_out && (!res || ldres >= m->m.n_out), kErrShape, "gemv output stride");
+    DeviceScope scope(m->dev);
+    qmat_gemv_q8act(m->m, x, ldx, nrows, y, ldy, res, ldres, m->dev->stream);
+  });
+}
+
 int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up, const void* act, int nrows,
                                    float* mid, int ldm) {
   return guard([&] {

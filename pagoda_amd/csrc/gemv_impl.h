@@ -453,6 +453,9 @@ void* gemv_scratch(hipStream_t s, size_t bytes, int slot = 0);
 size_t a8_scratch_need(const GemvArgs& a, int rows, int epi);
 // stream-K scratch of one 5..32-row chunk (slots 3 and 5, unaligned sizes)
 void sk_scratch_need(const GemvArgs& a, int nb, int epi, size_t* slot3, size_t* slot5);
+// GGML formats with candle's CPU arithmetic (activations quantized to Q8_K /
+// Q8_0, integer block dots); f32 activations
+void run_q8act(int fmt, const GemvArgs& a, int nrows, int epi, hipStream_t s);
 // A8 on the matrix cores (f32 activations)
 void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s);
 // Stream-K A8 kernel: whether a matrix takes it for 5..32-row launches, and

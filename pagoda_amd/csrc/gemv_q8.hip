@@ -1,0 +1,492 @@
+// gemv_q8.hip — GGML-format GEMV with the arithmetic of candle's CPU
+// quantized matmul (the reference's CPU path keeps QMatMul for the Qwen2 GGUF
+// weights, pagoda-hf/src/qwen2_gguf.rs:280-289): every activation row is
+// quantized to the weight type's vec_dot_type and each output is an integer
+// block dot scaled in f32.
+//
+//   Q4_K, Q6_K  x  Q8_K  (256-element blocks: f32 d, 256 i8, 16 i16 sums)
+//   Q8_0, Q5_0  x  Q8_0  (32-element blocks: f16 d, 32 i8)
+//
+// Activation quantization (BlockQ8K / BlockQ8_0 ::from_float): Q8_K takes the
+// first element of largest magnitude as max, iscale = -128 / max,
+// q = min(127, round(iscale x)) (round half away from zero), d = 1 / iscale,
+// and the sums of each 16 q; Q8_0 takes d = amax / 127, q = round(x / d)
+// with d rounded to f16. Every workgroup quantizes the launch's rows into LDS
+// itself (no separate launch); all of them compute the same bytes.
+//
+// Block dots: integer products through v_dot4 (exact), per weight block
+//   Q4_K: d_w d_x sum_j sc_j dot_j - dmin_w d_x sum_j m_j bsum_j
+//   Q6_K: d_w d_x sum_j sc_j (dot_j(q) - 32 bsum_j)       (q = 6-bit code)
+//   Q8_0: sumi d_w d_x;  Q5_0: (dot(q) - 16 sum(x_q)) d_w d_x   (q = 5-bit code)
+// The f32 terms are added per wave over its blocks, then over the waves
+// in wave order: a fixed order for a given shape, whatever the row count, so
+// batched rows are bitwise equal to single-row launches.
+//
+// Work split: one workgroup of NW waves (4, 8 or 16, from the number of K
+// blocks) per 32-row tile of the weight matrix; wave w takes K blocks w,
+// w + NW, ... (256-element super-blocks, or 32-weight blocks). Weights are
+// read once per launch of up to RB activation rows.
+#include "common.h"
+#include "gemv_impl.h"
+#include "quant.h"
+
+namespace pgd {
+namespace gemv {
+
+namespace {
+
+
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+
+__device__ inline int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// activations in LDS: q [RB][Kp] i8 | d [RB][nb] f32 | sums [RB][nb][SUMS] i32
+template <int FMT, int RB, int NW>
+struct ActLds {
+  static constexpr bool K256 = FMT == FMT_Q4K || FMT == FMT_Q6K;
+  static constexpr int BLK = K256 ? 256 : 32;
+  static constexpr int SUMS = K256 ? 16 : 1;
+  int Kp, nb;
+  int8_t* q;
+  float* d;
+  int* s;
+  float* red;  // [NM][NW][RB][32] wave partials, over the activations once the dots are done
+  __device__ ActLds(char* base, int n_in) {
+    nb = (n_in + BLK - 1) / BLK;
+    Kp = nb * BLK;
+    q = reinterpret_cast<int8_t*>(base);
+    d = reinterpret_cast<float*>(base + (((size_t)RB * Kp + 15) & ~(size_t)15));
+    s = reinterpret_cast<int*>(d + RB * nb);
+    red = reinterpret_cast<float*>(base);
+  }
+  static size_t bytes(int n_in, int nm) {
+    const int nbh = (n_in + BLK - 1) / BLK, Kph = nbh * BLK;
+    const size_t act = (((size_t)RB * Kph + 15) & ~(size_t)15) + (size_t)RB * nbh * 4 + (size_t)RB * nbh * SUMS * 4;
+    const size_t red = (size_t)nm * NW * RB * 32 * 4;
+    return act > red ? act : red;
+  }
+};
+
+// Quantize rows [0, rows) of x (the launch's chunk) into LDS; the whole
+// workgroup calls it.
+template <int FMT, int RB, int NW>
+__device__ void quantize_rows(const float* __restrict__ x, int ldx, int rows, int n_in, ActLds<FMT, RB, NW>& L) {
+  const int tid = threadIdx.x;
+  if constexpr (ActLds<FMT, RB, NW>::K256) {
+    // eight lanes per 256-element block, 32 consecutive elements each
+    const int s = tid & 7;
+    const int units = rows * L.nb;
+    for (int u0 = 0; u0 < units; u0 += 8 * NW) {
+      const int u = u0 + (tid >> 3);
+      const bool live = u < units;
+      const int r = live ? u / L.nb : 0, b = live ? u % L.nb : 0;
+      const int e0 = b * 256 + s * 32;
+      float v[32];
+      float amax = 0.0f, mx = 0.0f;
+      int idx = 0x7fffffff;
+      const float* xr = x + (size_t)r * ldx + e0;
+      if (live && e0 + 32 <= n_in && (((uintptr_t)xr) & 15) == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float4 t = reinterpret_cast<const float4*>(xr)[i];
+          v[4 * i] = t.x;
+          v[4 * i + 1] = t.y;
+          v[4 * i + 2] = t.z;
+          v[4 * i + 3] = t.w;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = (live && e0 + i < n_in) ? xr[i] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int e = e0 + i;
+        const float ax = fabsf(v[i]);
+        if (ax > amax) {
+          amax = ax;
+          mx = v[i];
+          idx = e;
+        }
+      }
+      // the first element of largest magnitude over the block's 8 lanes
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) {
+        const float oa = __shfl_xor(amax, o, 64), om = __shfl_xor(mx, o, 64);
+        const int oi = __shfl_xor(idx, o, 64);
+        if (oa > amax || (oa == amax && oi < idx)) {
+          amax = oa;
+          mx = om;
+          idx = oi;
+        }
+      }
+      if (live) {
+        int8_t* q = L.q + (size_t)r * L.Kp + e0;
+        int* bs = L.s + (r * L.nb + b) * 16 + 2 * s;
+        if (amax == 0.0f) {
+#pragma unroll
+          for (int i = 0; i < 32; ++i) q[i] = 0;
+          bs[0] = bs[1] = 0;
+          if (s == 0) L.d[r * L.nb + b] = 0.0f;
+        } else {
+          const float iscale = -128.0f / mx;
+          int s0 = 0, s1 = 0;
+#pragma unroll
+          for (int i = 0; i < 32; ++i) {
+            const float t = roundf(iscale * v[i]);
+            const int qi = (int)(t < 127.0f ? t : 127.0f);
+            q[i] = (int8_t)qi;
+            if (i < 16) s0 += qi;
+            else s1 += qi;
+          }
+          bs[0] = s0;
+          bs[1] = s1;
+          if (s == 0) L.d[r * L.nb + b] = 1.0f / iscale;
+        }
+      }
+    }
+  } else {
+    // one lane per 32-element block
+    const int units = rows * L.nb;
+    for (int u = tid; u < units; u += blockDim.x) {
+      const int r = u / L.nb, b = u % L.nb;
+      const float* xr = x + (size_t)r * ldx + b * 32;
+      float v[32];
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        v[i] = xr[i];
+        amax = fmaxf(amax, fabsf(v[i]));
+      }
+      const float d = amax / 127.0f;
+      const float id = d != 0.0f ? 1.0f / d : 0.0f;
+      int8_t* q = L.q + (size_t)r * L.Kp + b * 32;
+      int sum = 0;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int qi = (int)roundf(v[i] * id);
+        q[i] = (int8_t)qi;
+        sum += qi;
+      }
+      L.s[r * L.nb + b] = sum;
+      L.d[r * L.nb + b] = (float)(_Float16)d;  // the f16 d of block_q8_0
+    }
+  }
+}
+
+// ---- per-format block dots of one wave over its blocks ----------------------
+// acc[m][r][i]: matrix m (0, or 1 = SwiGLU up), activation row r, the lane's
+// i-th output row of the tile (see each format's row map).
+
+// Q4_K: lane l = output row l >> 1, half h = l & 1 of each 32-byte run.
+template <int RB, int NW, int NM>
+__device__ void dots_q4k(const GemvArgs& a, int tile, int rows, const ActLds<FMT_Q4K, RB, NW>& L,
+                         float (&acc)[NM][RB][1]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int jr = lane >> 1, h = lane & 1, row = tile * 32 + jr;
+  for (int sb = w; sb < a.nsb; sb += NW) {
+    const int nj = min(4, (a.n_in - sb * 256 + 63) / 64);  // 64-element chunks present
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const uint8_t* p0 = m ? a.u0 : a.p0;
+      const uint8_t* p1 = m ? a.u1 : a.p1;
+      const uint4 hdr = *reinterpret_cast<const uint4*>(p1 + q4k_hdr_off(row, sb, a.nsb));
+      uint4 wq[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        wq[j] = j < nj ? *reinterpret_cast<const uint4*>(p0 + q4k_qs_off(row, 32 * (4 * sb + j) + 16 * h, a.nsb))
+                       : make_uint4(0, 0, 0, 0);
+      // 6-bit scales and mins of the 8 sub-blocks
+      const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};
+      auto byte = [&](int i) { return (sw[i >> 2] >> (8 * (i & 3))) & 255u; };
+      int sc[8], mn[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (k < 4) {
+          sc[k] = (int)(byte(k) & 63u);
+          mn[k] = (int)(byte(k + 4) & 63u);
+        } else {
+          sc[k] = (int)((byte(k + 4) & 0xFu) | ((byte(k - 4) >> 6) << 4));
+          mn[k] = (int)((byte(k + 4) >> 4) | ((byte(k) >> 6) << 4));
+        }
+      }
+      const float dw = f16_to_f32(hdr.x & 0xffffu), dmin = f16_to_f32(hdr.x >> 16);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        if (r >= rows) break;
+        const int8_t* xq = L.q + (size_t)r * L.Kp + sb * 256;
+        int isum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (j >= nj) break;
+          const uint4 xl = *reinterpret_cast<const uint4*>(xq + 64 * j + 16 * h);
+          const uint4 xh = *reinterpret_cast<const uint4*>(xq + 64 * j + 32 + 16 * h);
+          const uint32_t qw[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
+          const uint32_t lw[4] = {xl.x, xl.y, xl.z, xl.w}, hw[4] = {xh.x, xh.y, xh.z, xh.w};
+          int dl = 0, dh = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dl = dot4(qw[i] & 0x0F0F0F0Fu, lw[i], dl);
+            dh = dot4((qw[i] >> 4) & 0x0F0F0F0Fu, hw[i], dh);
+          }
+          isum += sc[2 * j] * dl + sc[2 * j + 1] * dh;
+        }
+        isum += __shfl_xor(isum, 1, 64);
+        const int* bs = L.s + (r * L.nb + sb) * 16;
+        int msum = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) msum += mn[k] * (bs[2 * k] + bs[2 * k + 1]);
+        const float d8 = L.d[r * L.nb + sb];
+        acc[m][r][0] += (dw * d8) * (float)isum;
+        acc[m][r][0] -= (dmin * d8) * (float)msum;
+      }
+    }
+  }
+}
+
+// Q6_K: lane l = dword k = l >> 4 of row 16 hh + (l & 15), for row halves hh
+// 0 and 1 (acc index hh).
+template <int RB, int NW, int NM>
+__device__ void dots_q6k(const GemvArgs& a, int tile, int rows, const ActLds<FMT_Q6K, RB, NW>& L,
+                         float (&acc)[NM][RB][2]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int k = lane >> 4, jr = lane & 15;
+  for (int sb = w; sb < a.nsb; sb += NW) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const uint8_t* p0 = m ? a.u0 : a.p0;
+      const uint8_t* p1 = m ? a.u1 : a.p1;
+      const uint8_t* p2 = m ? a.u2 : a.p2;
+      const uint8_t* p3 = m ? a.u3 : a.p3;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int row = tile * 32 + 16 * hh + jr;
+        const float dw = f16_to_f32(reinterpret_cast<const uint16_t*>(p3)[q6k_d_off(row, sb, a.nsb)]);
+        int iw[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) iw[r] = 0;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (sb * 256 + 128 * u >= a.n_in) break;
+          const uint4 ql = *reinterpret_cast<const uint4*>(p0 + q6k_ql_off(row, 64 * (2 * sb + u) + 4 * k, a.nsb));
+          const u2v qh = *reinterpret_cast<const u2v*>(p1 + q6k_qh_off(row, 32 * (2 * sb + u) + 4 * k, a.nsb));
+          const u2v scw = *reinterpret_cast<const u2v*>(p2 + q6k_sc_off(row, 16 * sb + 8 * u, a.nsb));
+          // codes of elements 4k + 16 m + (0..3) of this half, m = 0..7
+          const uint32_t qlw[4] = {ql.x, ql.y, ql.z, ql.w};
+          uint32_t v[8];
+#pragma unroll
+          for (int mm = 0; mm < 8; ++mm) {
+            const uint32_t lo = (qlw[mm & 3] >> (mm >= 4 ? 4 : 0)) & 0x0F0F0F0Fu;
+            const uint32_t hq = (mm & 1) ? qh.y : qh.x;
+            const uint32_t hb = (hq >> (2 * (mm >> 1))) & 0x03030303u;
+            v[mm] = lo | (hb << 4);
+          }
+          int sc[8];
+#pragma unroll
+          for (int mm = 0; mm < 8; ++mm) sc[mm] = (int)(int8_t)(((mm < 4 ? scw.x : scw.y) >> (8 * (mm & 3))) & 255u);
+#pragma unroll
+          for (int r = 0; r < RB; ++r) {
+            if (r >= rows) break;
+            const int8_t* xq = L.q + (size_t)r * L.Kp + sb * 256 + 128 * u + 4 * k;
+            int part = 0;
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm)
+              part += sc[mm] * dot4(v[mm], *reinterpret_cast<const uint32_t*>(xq + 16 * mm), 0);
+            // the four dword lanes of a row, then the -32 offset of the codes
+            part += __shfl_xor(part, 16, 64);
+            part += __shfl_xor(part, 32, 64);
+            const int* bs = L.s + (r * L.nb + sb) * 16 + 8 * u;
+            int corr = 0;
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm) corr += sc[mm] * bs[mm];
+            iw[r] += part - 32 * corr;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          if (r >= rows) break;
+          acc[m][r][hh] += (dw * L.d[r * L.nb + sb]) * (float)iw[r];
+        }
+      }
+    }
+  }
+}
+
+// Q8_0 / Q5_0 (row-major planes, no row padding): lane l = output row l >> 1,
+// half h = l & 1 of each block.
+template <int FMT, int RB, int NW, int NM>
+__device__ void dots_q32(const GemvArgs& a, int tile, int rows, const ActLds<FMT, RB, NW>& L, float (&acc)[NM][RB][1]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = lane & 1;
+  const int row = min(tile * 32 + (lane >> 1), a.n_out - 1);
+  const int nb = a.n_in / 32;
+  for (int b = w; b < nb; b += NW) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const uint8_t* p0 = m ? a.u0 : a.p0;
+      const uint8_t* p1 = m ? a.u1 : a.p1;
+      const uint8_t* p2 = m ? a.u2 : a.p2;
+      uint32_t v[4];
+      float dw;
+      if constexpr (FMT == FMT_Q8_0) {
+        const uint4 q = *reinterpret_cast<const uint4*>(p0 + (size_t)row * a.n_in + 32 * b + 16 * h);
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+        dw = f16_to_f32(reinterpret_cast<const uint16_t*>(p1)[(size_t)row * nb + b]);
+      } else {
+        // bytes 8h..8h+7 of the block's 16: low nibbles are weights 8h + i,
+        // high nibbles weights 16 + 8h + i; qh bit j is weight j's fifth bit
+        const u2v q = *reinterpret_cast<const u2v*>(p0 + (size_t)row * (a.n_in / 2) + 16 * b + 8 * h);
+        const uint32_t qh = reinterpret_cast<const uint32_t*>(p1)[(size_t)row * nb + b];
+        auto spread = [](uint32_t bits4) {  // 4 bits -> bit 4 of 4 bytes
+          return ((bits4 & 1u) | ((bits4 & 2u) << 7) | ((bits4 & 4u) << 14) | ((bits4 & 8u) << 21)) << 4;
+        };
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t wd = i ? q.y : q.x;
+          const int j0 = 8 * h + 4 * i;
+          v[i] = (wd & 0x0F0F0F0Fu) | spread((qh >> j0) & 15u);
+          v[2 + i] = ((wd >> 4) & 0x0F0F0F0Fu) | spread((qh >> (16 + j0)) & 15u);
+        }
+        dw = f16_to_f32(reinterpret_cast<const uint16_t*>(p2)[(size_t)row * nb + b]);
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        if (r >= rows) break;
+        const int8_t* xq = L.q + (size_t)r * L.Kp + 32 * b;
+        int sumi = 0;
+        if constexpr (FMT == FMT_Q8_0) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xq + 16 * h);
+          sumi = dot4(v[0], xv.x, sumi);
+          sumi = dot4(v[1], xv.y, sumi);
+          sumi = dot4(v[2], xv.z, sumi);
+          sumi = dot4(v[3], xv.w, sumi);
+          sumi += __shfl_xor(sumi, 1, 64);
+        } else {
+          const u2v xl = *reinterpret_cast<const u2v*>(xq + 8 * h);
+          const u2v xh = *reinterpret_cast<const u2v*>(xq + 16 + 8 * h);
+          sumi = dot4(v[0], xl.x, sumi);
+          sumi = dot4(v[1], xl.y, sumi);
+          sumi = dot4(v[2], xh.x, sumi);
+          sumi = dot4(v[3], xh.y, sumi);
+          sumi += __shfl_xor(sumi, 1, 64);
+          sumi -= 16 * L.s[r * L.nb + b];
+        }
+        acc[m][r][0] += (float)sumi * dw * L.d[r * L.nb + b];
+      }
+    }
+  }
+}
+
+template <int FMT, int RB, int NW, int EPI>
+__global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(GemvArgs a, int rows) {
+  extern __shared__ __attribute__((aligned(16))) char dsm[];
+  constexpr int NM = EPI == EPI_SWIGLU ? 2 : 1;
+  constexpr int NI = FMT == FMT_Q6K ? 2 : 1;  // output rows per lane
+  ActLds<FMT, RB, NW> L(dsm, a.n_in);
+  quantize_rows<FMT, RB, NW>(reinterpret_cast<const float*>(a.x), a.ldx, rows, a.n_in, L);
+  __syncthreads();
+  const int tile = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  float acc[NM][RB][NI];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int i = 0; i < NI; ++i) acc[m][r][i] = 0.0f;
+  if constexpr (FMT == FMT_Q4K) dots_q4k<RB, NW, NM>(a, tile, rows, L, acc);
+  else if constexpr (FMT == FMT_Q6K) dots_q6k<RB, NW, NM>(a, tile, rows, L, acc);
+  else dots_q32<FMT, RB, NW, NM>(a, tile, rows, L, acc);
+  // wave partials -> LDS [m][w][r][row] (over the activations: wait for every wave's dots)
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      if (r >= rows) break;
+      float* red = L.red + ((m * NW + w) * RB + r) * 32;
+      if constexpr (FMT == FMT_Q6K) {
+        if ((lane >> 4) == 0) {
+          red[lane & 15] = acc[m][r][0];
+          red[16 + (lane & 15)] = acc[m][r][1];
+        }
+      } else if ((lane & 1) == 0) {
+        red[lane >> 1] = acc[m][r][0];
+      }
+    }
+  __syncthreads();
+  if (w != 0 || lane >= 32) return;
+  const int n = tile * 32 + lane;
+  if (n >= a.n_out) return;
+  for (int r = 0; r < rows; ++r) {
+    float v[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const float* red = L.red + (m * NW * RB + r) * 32 + lane;
+      v[m] = red[0];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) v[m] += red[ww * RB * 32];
+    }
+    const size_t o = (size_t)r * a.ldy + n;
+    if constexpr (EPI == EPI_STORE) a.y[o] = v[0];
+    if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)r * a.ldres + n] + v[0];
+    if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(v[0]) * v[NM - 1];
+  }
+}
+
+template <int FMT, int RB, int NW, int EPI>
+void launch_q8(GemvArgs a, int nrows, hipStream_t s) {
+  const size_t lds = ActLds<FMT, RB, NW>::bytes(a.n_in, EPI == EPI_SWIGLU ? 2 : 1);
+  PGD_CHECK(lds <= 64 * 1024, kErrShape, "activation rows too wide for the quantized-activation GEMV");
+  const int tiles = (a.n_out + 31) / 32;
+  for (int r0 = 0; r0 < nrows; r0 += RB) {
+    const int rows = min(RB, nrows - r0);
+    hipLaunchKernelGGL((q8_gemv_kernel<FMT, RB, NW, EPI>), dim3(tiles), dim3(64 * NW), lds, s, a, rows);
+    PGD_HIP(hipGetLastError());
+    a.x = reinterpret_cast<const float*>(a.x) + (size_t)rows * a.ldx;
+    a.y += (size_t)rows * a.ldy;
+    if (a.res) a.res += (size_t)rows * a.ldres;
+  }
+}
+
+// waves per workgroup from the K blocks of a row (a shape property, so every
+// row count of one matrix sums in the same order)
+template <int FMT, int RB, int EPI>
+void launch_waves(const GemvArgs& a, int nrows, hipStream_t s) {
+  const int kb = (FMT == FMT_Q4K || FMT == FMT_Q6K) ? a.nsb : a.n_in / 128;  // in units of 4 Q8_0 blocks
+  if (kb <= 4) return launch_q8<FMT, RB, 4, EPI>(a, nrows, s);
+  if (kb <= 8) return launch_q8<FMT, RB, 8, EPI>(a, nrows, s);
+  launch_q8<FMT, RB, 16, EPI>(a, nrows, s);
+}
+
+template <int FMT, int EPI>
+void launch_rows(const GemvArgs& a, int nrows, hipStream_t s) {
+  if (nrows == 1) return launch_waves<FMT, 1, EPI>(a, nrows, s);
+  if (nrows <= 4) return launch_waves<FMT, 4, EPI>(a, nrows, s);
+  launch_waves<FMT, 8, EPI>(a, nrows, s);
+}
+
+template <int EPI>
+void dispatch(int fmt, const GemvArgs& a, int nrows, hipStream_t s) {
+  switch (fmt) {
+    case FMT_Q4K: return launch_rows<FMT_Q4K, EPI>(a, nrows, s);
+    case FMT_Q6K: return launch_rows<FMT_Q6K, EPI>(a, nrows, s);
+    case FMT_Q8_0: return launch_rows<FMT_Q8_0, EPI>(a, nrows, s);
+    case FMT_Q5_0: return launch_rows<FMT_Q5_0, EPI>(a, nrows, s);
+  }
+  throw Error{kErrFormat, "quantized-activation GEMV takes Q4_K, Q6_K, Q8_0 or Q5_0 matrices"};
+}
+
+}  // namespace
+
+void run_q8act(int fmt, const GemvArgs& a, int nrows, int epi, hipStream_t s) {
+  if (epi == EPI_SWIGLU) dispatch<EPI_SWIGLU>(fmt, a, nrows, s);
+  else if (epi == EPI_RES) dispatch<EPI_RES>(fmt, a, nrows, s);
+  else dispatch<EPI_STORE>(fmt, a, nrows, s);
+}
+
+}  // namespace gemv
+}  // namespace pgd

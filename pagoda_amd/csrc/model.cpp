@@ -136,6 +136,8 @@ Session::~Session() {
 // model build (from any weight source) and the synthetic source
 // ---------------------------------------------------------------------------
 void build_model(Model& m, WeightSource& src) {
+  // GGUF (Qwen2) models default to the reference CPU path's arithmetic
+  m.q8act = m.cfg.arch == PGD_ARCH_QWEN2 ? 1 : 0;
   const pgd_model_config& c = m.cfg;
   hipStream_t s = m.dev->stream;
   const int H = c.hidden;
@@ -360,6 +362,11 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
         for (int i = 0; i < n; ++i) s[i]->poisoned = true;
     }
   } poison{sess, nseq};
+  // GEMVs of f32 activations (the Qwen2 path) in the model's arithmetic
+  auto gemv = [&](const QMat& q, const float* x, int ldx, int nr, float* y, int ldy, const float* res, int ldres) {
+    if (m.q8act && q.fmt != FMT_A8) qmat_gemv_q8act(q, x, ldx, nr, y, ldy, res, ldres, st);
+    else qmat_gemv(q, x, 0, ldx, nr, y, ldy, res, ldres, st);
+  };
   // ---- KV pages: count, then allocate (copy-on-write for a shared tail) ----
   if (m.n_full > 0) {
     size_t need = 0;
@@ -484,7 +491,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   // ---- forward ----
   Ws w = carve_ws(m, rows, lrows);
   const int H = c.hidden;
-  const int norm_mode = c.arch == PGD_ARCH_QWEN35 ? 0 : 1;
+  const int norm_mode = c.arch == PGD_ARCH_QWEN35 ? 0 : m.q8act ? 2 : 1;
   const float eps = c.arch == PGD_ARCH_QWEN35 ? 1e-6f : c.eps;
   qmat_embed(m.embed, d_tok, rows, w.x, H, st);
   const size_t per_lin = m.conv_floats + m.state_floats;
@@ -523,12 +530,12 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       rmsnorm_rows(w.x, H, nullptr, rows, H, L.in_norm, eps, norm_mode, w.xn, H, st);
       // q | k | v side by side in A (q and k from one stacked launch when they share a format)
       if (L.proj.base) {
-        qmat_gemv(L.proj, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
+        gemv(L.proj, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
       } else {
-        qmat_gemv(L.q, w.xn, 0, H, rows, w.A, (int)w.lda, nullptr, 0, st);
-        qmat_gemv(L.k, w.xn, 0, H, rows, w.A + m.q_out, (int)w.lda, nullptr, 0, st);
+        gemv(L.q, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
+        gemv(L.k, w.xn, H, rows, w.A + m.q_out, (int)w.lda, nullptr, 0);
       }
-      qmat_gemv(L.v, w.xn, 0, H, rows, w.A + m.q_out + m.kv_width, (int)w.lda, nullptr, 0, st);
+      gemv(L.v, w.xn, H, rows, w.A + m.q_out + m.kv_width, (int)w.lda, nullptr, 0);
       q_raw = w.A;
       k_raw = w.A + m.q_out;
       v_raw = w.A + m.q_out + m.kv_width;
@@ -590,7 +597,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
         post_in = qmat_gemv_a8_res_norm(L.o, act, w.x, H, L.post_norm, eps, w.act3, st);
       } else {
         attn_decode(w.D, nullptr, w.E, al, rm, ap, rows, st);
-        qmat_gemv(L.o, w.E, 0, c.heads * c.head_dim, rows, w.x, H, w.x, H, st);
+        gemv(L.o, w.E, c.heads * c.head_dim, rows, w.x, H, w.x, H);
       }
     }
     // ---- SwiGLU MLP ----
@@ -608,8 +615,9 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       }
     } else {
       rmsnorm_rows(w.x, H, nullptr, rows, H, L.post_norm, eps, norm_mode, w.xn, H, st);
-      qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
-      qmat_gemv(L.down, w.G, 0, c.intermediate, rows, w.x, H, w.x, H, st);
+      if (m.q8act) qmat_gemv_swiglu_q8act(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
+      else qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
+      gemv(L.down, w.G, c.intermediate, rows, w.x, H, w.x, H);
     }
   }
   // ---- head ----
@@ -618,7 +626,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     qmat_gemv_a8(m.head, act, w.logits, c.vocab, nullptr, 0, st);
   } else {
     rmsnorm_rows(w.x, H, d_lr, lrows, H, m.final_norm, eps, norm_mode, w.xn, H, st);
-    qmat_gemv(m.head, w.xn, 0, H, lrows, w.logits, c.vocab, nullptr, 0, st);
+    gemv(m.head, w.xn, H, lrows, w.logits, c.vocab, nullptr, 0);
   }
   size_t out_bytes = (size_t)lrows * 12;
   if (m.out_dev.bytes < out_bytes) m.out_dev = DevBuf(out_bytes * 2);
@@ -672,6 +680,14 @@ int pgd_model_synth(pgd_dev* dev, const pgd_model_config* cfg, uint64_t seed, pg
   });
   if (rc && held) delete held;
   return rc;
+}
+
+int pgd_model_set_kquant_arith(pgd_model* pm, int mode) {
+  return guard([&] {
+    PGD_CHECK(pm, kErrArg, "null model");
+    PGD_CHECK(mode == PGD_ARITH_DEQUANT_F32 || mode == PGD_ARITH_CPU_Q8, kErrArg, "unknown arithmetic mode");
+    pm->m.q8act = mode == PGD_ARITH_CPU_Q8 ? 1 : 0;
+  });
 }
 
 int pgd_model_free(pgd_model* m) {

@@ -79,6 +79,9 @@ struct Model {
   void* out_host = nullptr;
   size_t out_host_cap = 0;
   int live_sessions = 0;
+  // arithmetic of the GGML-format (Qwen2) matrices: 1 = candle's CPU quantized
+  // matmul (activations quantized to Q8_K / Q8_0), 0 = f32 dequant-then-dot
+  int q8act = 0;
 
   ~Model();
   void ensure_rope(int pos);

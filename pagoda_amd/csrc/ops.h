@@ -15,6 +15,8 @@ namespace pgd {
 // y[r] = rmsnorm(x[src_row(r)]) * w, eps inside the sqrt.
 //   mode 0: x * (1/sqrt(mean(x^2)+eps)) * w   (rms_zero, qwen3_5.rs:1736-1745)
 //   mode 1: x / sqrt(mean(x^2)+eps) * w       (candle RmsNorm, qwen2_gguf.rs:92)
+//   mode 2: mode 1 with the squares summed left to right, candle's CPU order
+//           (n <= 8192)
 // rows_idx (device, nullable) selects the source rows.
 void rmsnorm_rows(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps,
                   int mode, float* y, int ldy, hipStream_t s);

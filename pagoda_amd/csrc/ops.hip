@@ -32,8 +32,33 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const int src = rows_idx ? rows_idx[r] : r;
   const float* xr = x + (size_t)src * ldx;
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < n; i += 256) ss += xr[i] * xr[i];
-  ss = block_sum256(ss, red);
+  if (mode != 2) {
+    for (int i = threadIdx.x; i < n; i += 256) ss += xr[i] * xr[i];
+    ss = block_sum256(ss, red);
+  } else {
+    // candle's CPU rms_norm sums the squares left to right in f32; the same
+    // order makes the normed values (and so their Q8 quantization, where an
+    // embedding row's grid values can sit exactly on a rounding tie) agree
+    // bit for bit. The squares are formed in parallel (each rounds the same
+    // wherever it is computed) and staged in LDS; one lane adds them in order.
+    __shared__ float sq[8192];
+    for (int i = threadIdx.x; i < n; i += 256) sq[i] = xr[i] * xr[i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int i = 0;
+      for (; i + 4 <= n; i += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(sq + i);
+        ss += v.x;
+        ss += v.y;
+        ss += v.z;
+        ss += v.w;
+      }
+      for (; i < n; ++i) ss += sq[i];
+      red[0] = ss;
+    }
+    __syncthreads();
+    ss = red[0];
+  }
   float* yr = y + (size_t)r * ldy;
   if (mode == 0) {
     float inv = 1.0f / sqrtf(ss / (float)n + eps);
@@ -366,6 +391,7 @@ __global__ void gather_kernel(const float* src, int lds, const int* idx, int n, 
 void rmsnorm_rows(const float* x, int ldx, const int* rows_idx, int rows, int n, const float* w, float eps, int mode,
                   float* y, int ldy, hipStream_t s) {
   if (rows <= 0) return;
+  PGD_CHECK(mode != 2 || n <= 8192, kErrShape, "ordered-sum RMSNorm rows are at most 8192 wide");
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, ldx, rows_idx, n, w, eps, mode, y, ldy);
   PGD_HIP(hipGetLastError());
 }

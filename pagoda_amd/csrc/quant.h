@@ -117,6 +117,15 @@ void qmat_dequant(const QMat& m, int row0, int rows, float* out, hipStream_t s);
 void qmat_gemv(const QMat& m, const void* x, int x_f16, int ldx, int nrows, float* y, int ldy,
                const float* res, int ldres, hipStream_t s);
 
+// The same products with candle's CPU arithmetic (the reference's CPU path,
+// pagoda-hf/src/qwen2_gguf.rs:280-289): each f32 activation row is quantized
+// to Q8_K (Q4_K / Q6_K weights) or Q8_0 (Q8_0 / Q5_0 weights) and every
+// output is an integer block dot scaled in f32.
+void qmat_gemv_q8act(const QMat& m, const float* x, int ldx, int nrows, float* y, int ldy, const float* res, int ldres,
+                     hipStream_t s);
+void qmat_gemv_swiglu_q8act(const QMat& gate, const QMat& up, const float* x, int ldx, int nrows, float* mid, int ldm,
+                            hipStream_t s);
+
 // fused SwiGLU: mid[r, n] = silu(gate.x) * (up.x)
 void qmat_gemv_swiglu(const QMat& gate, const QMat& up, const float* x, int ldx, int nrows, float* mid,
                       int ldm, hipStream_t s);

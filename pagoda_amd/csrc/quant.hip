@@ -656,6 +656,38 @@ void qmat_gemv_swiglu(const QMat& gate, const QMat& up, const float* x, int ldx,
   run_fmt(gate, a, nrows, 0, EPI_SWIGLU, s);
 }
 
+void qmat_gemv_q8act(const QMat& m, const float* x, int ldx, int nrows, float* y, int ldy, const float* res, int ldres,
+                     hipStream_t s) {
+  PGD_CHECK(nrows >= 0 && ldx >= m.n_in, kErrShape, "gemv rows / ldx");
+  if (nrows == 0) return;
+  GemvArgs a = make_args(m);
+  a.x = x;
+  a.ldx = ldx;
+  a.y = y;
+  a.ldy = ldy;
+  a.res = res;
+  a.ldres = ldres;
+  run_q8act(m.fmt, a, nrows, res ? EPI_RES : EPI_STORE, s);
+}
+
+void qmat_gemv_swiglu_q8act(const QMat& gate, const QMat& up, const float* x, int ldx, int nrows, float* mid, int ldm,
+                            hipStream_t s) {
+  PGD_CHECK(gate.fmt == up.fmt && gate.n_out == up.n_out && gate.n_in == up.n_in, kErrShape,
+            "swiglu gate/up shapes differ");
+  PGD_CHECK(nrows >= 0 && ldx >= gate.n_in, kErrShape, "gemv rows / ldx");
+  if (nrows == 0) return;
+  GemvArgs a = make_args(gate);
+  a.u0 = up.p0;
+  a.u1 = up.p1;
+  a.u2 = up.p2;
+  a.u3 = up.p3;
+  a.x = x;
+  a.ldx = ldx;
+  a.y = mid;
+  a.ldy = ldm;
+  run_q8act(gate.fmt, a, nrows, EPI_SWIGLU, s);
+}
+
 void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const float* res, int ldres, hipStream_t s) {
   PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "prepared activations feed A8 matrices");
   if (act.rows <= 0) return;

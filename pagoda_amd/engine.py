@@ -14,6 +14,7 @@ from ._lib import PagodaError, call, last_error, lib
 from .device import Device
 
 ARCH_QWEN35, ARCH_QWEN2 = 0, 1
+ARITH_DEQUANT_F32, ARITH_CPU_Q8 = 0, 1
 
 
 class _Cfg(C.Structure):
@@ -112,6 +113,11 @@ class Model:
         h = C.c_void_p()
         call("pgd_model_load_gguf", dev.handle, str(path).encode(), int(max_pos), int(kv_blocks), C.byref(h))
         return cls(dev, h, _config_of(h))
+
+    def set_kquant_arith(self, mode: int) -> None:
+        """ARITH_CPU_Q8 (the Qwen2 default: candle's CPU quantized matmul) or
+        ARITH_DEQUANT_F32 for the GGML-format matrices."""
+        call("pgd_model_set_kquant_arith", self.handle, int(mode))
 
     def info(self) -> dict:
         wb, ab, kf = C.c_size_t(), C.c_double(), C.c_int()

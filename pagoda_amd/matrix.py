@@ -98,6 +98,12 @@ class Matrix:
         call("pgd_matrix_gemv_dev", self.handle, C.c_void_p(x_ptr), int(x_f16), ldx, nrows, C.c_void_p(y_ptr), ldy,
              C.c_void_p(res_ptr or None), ldres)
 
+    def gemv_q8act_dev(self, x_ptr: int, ldx: int, nrows: int, y_ptr: int, ldy: int, res_ptr: int = 0,
+                       ldres: int = 0) -> None:
+        """candle's CPU quantized matmul arithmetic (activations quantized to Q8_K / Q8_0)."""
+        call("pgd_matrix_gemv_q8act_dev", self.handle, C.c_void_p(x_ptr), ldx, nrows, C.c_void_p(y_ptr), ldy,
+             C.c_void_p(res_ptr or None), ldres)
+
     def gemv_act_dev(self, act_ptr: int, nrows: int, y_ptr: int, ldy: int, res_ptr: int = 0, ldres: int = 0) -> None:
         call("pgd_matrix_gemv_act_dev", self.handle, C.c_void_p(act_ptr), nrows, C.c_void_p(y_ptr), ldy,
              C.c_void_p(res_ptr or None), ldres)

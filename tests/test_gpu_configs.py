@@ -32,41 +32,84 @@ def margin(x):
     return float(t[1] - t[0])
 
 
-def test_config1_qwen2_05b_greedy_32_cold_and_warm(dev):
-    from pagoda_amd.engine import QWEN2_05B, Model, argmax_first
+# cpu_q8 arithmetic: an activation sitting within an f32 rounding of a Q8
+# rounding tie can quantize one code apart on two correct implementations
+# that sum in different orders (the oracle's scalar order, the GPU's, candle's
+# NEON or AVX builds); on this random-init 24-layer model such a flip grows
+# to ~1e-2 of the logits' scale. Measured on MI355X over 144 teacher-forced
+# steps (6 prompts): max-normalized logit deviation median 3.0e-2, argmax
+# mismatches only at oracle top-2 margins <= 0.05.
+Q8_LOGIT_TOL = 0.1
+Q8_MARGIN = 0.1
+
+
+@pytest.mark.parametrize("arith", ["dequant_f32", "cpu_q8"])
+def test_config1_qwen2_05b_greedy_32_cold_and_warm(dev, arith, capsys):
+    """dequant_f32: f32 dequant-then-dot against the oracle in the same
+    arithmetic: logits within 1e-3 and 32 identical greedy ids, free running.
+    cpu_q8 (the Qwen2 default): candle's CPU quantized matmul against the
+    oracle's restatement of it, teacher-forced on the oracle's tokens: logits
+    within Q8_LOGIT_TOL and the same argmax wherever the oracle's top-2 margin
+    exceeds Q8_MARGIN (see above). Both: the warm rerun through the prefix
+    graft reproduces the GPU's own cold stream."""
+    from pagoda_amd.engine import ARITH_CPU_Q8, ARITH_DEQUANT_F32, QWEN2_05B, Model, argmax_first
 
     cfg = QWEN2_05B
     seed = 1
+    q8 = arith == "cpu_q8"
+    mode = ARITH_CPU_Q8 if q8 else ARITH_DEQUANT_F32
     print("config1: building device model", flush=True)
     model = Model.synth(dev, cfg, seed)
+    model.set_kquant_arith(mode)
     print("config1: building oracle model", flush=True)
-    oracle = ora.Qwen2(ora.Qwen2Config(), seed)
+    oracle = ora.Qwen2(ora.Qwen2Config(), seed, kquant_mode=mode)
     rng = np.random.default_rng(81)
     prompt = rng.integers(0, cfg.vocab, 81)
     s = model.new_session()
     oc = oracle.new_cache()
     got = s.forward(prompt)
     ref = oracle.forward(prompt, oc)
-    assert rel(got, ref) < LOGIT_TOL
-    gen_gpu, gen_ref, margins = [], [], []
+    tol = Q8_LOGIT_TOL if q8 else LOGIT_TOL
+    gen_gpu, margins, mism = [], [], []
+    t_gpu = None
+    if q8:
+        # the GPU's own free-running stream, for the warm check below
+        g = model.new_session()
+        lg = g.forward(prompt)
+        for step in range(32):
+            t_gpu = argmax_first(lg)
+            gen_gpu.append(t_gpu)
+            if step < 31:
+                lg = g.forward([t_gpu])
+        g.free()
     for step in range(32):
+        assert rel(got, ref) < tol, f"step {step}: {rel(got, ref)}"
         tg, tr = argmax_first(got), ora.argmax_first(ref)
         margins.append(margin(ref))
-        gen_gpu.append(tg)
-        gen_ref.append(tr)
-        assert tg == tr, f"step {step}: gpu {tg} oracle {tr} (margin {margins[-1]:.3g})"
+        if tg != tr:
+            mism.append((step, round(margins[-1], 4)))
+            assert q8 and margins[-1] <= Q8_MARGIN, f"step {step}: gpu {tg} oracle {tr} (margin {margins[-1]:.3g})"
+        if not q8:
+            gen_gpu.append(tg)
         if step == 31:
             break
-        got = s.forward([tg])
+        got = s.forward([tr])
         ref = oracle.forward([tr], oc)
-        assert rel(got, ref) < LOGIT_TOL, f"step {step}: {rel(got, ref)}"
-    print("config1: min top-2 margin", min(margins), flush=True)
-    # warm rerun: graft_session(prompt, len - 1) slices the cold session's
+    with capsys.disabled():
+        print(f"\n[config1 {arith}] min top-2 margin {min(margins):.4g}; argmax mismatches (step, margin): {mism}",
+              flush=True)
+    s.free()
+    # warm rerun: graft_session(prompt, len - 1) slices a cold session's
     # cache (81 prompt + 31 generated positions) to the 80 covered prompt
     # tokens (pagoda-hf/src/lib.rs:603-616); it feeds the last prompt token,
     # then the 31 tokens it samples itself
-    assert s.context_len() == 112
-    w2 = s.fork_prefix(80)
+    cold = model.new_session()
+    lg = cold.forward(prompt)
+    for t in gen_gpu[:31]:
+        assert argmax_first(lg) == t
+        lg = cold.forward([t])
+    assert cold.context_len() == 112
+    w2 = cold.fork_prefix(80)
     assert w2.context_len() == 80
     fed = 0
     logits = w2.forward(prompt[80:])

@@ -1,0 +1,93 @@
+"""GGML-format GEMV with candle's CPU arithmetic (pgd_matrix_gemv_q8act_dev):
+each activation row quantized to Q8_K (Q4_K / Q6_K) or Q8_0 (Q8_0 / Q5_0) and
+integer block dots, against the oracle's restatement of the same kernels
+(oracle.c: q8k_quantize_block, vec_dot_q4k_q8k, vec_dot_q6k_q8k,
+vec_dot_q8_0_q8_0, vec_dot_q5_0_q8_0). The integer parts are exact; the f32
+sums of the per-block terms run in another order, so outputs agree to f32
+rounding (1e-5 of the row's scale, elementwise)."""
+import numpy as np
+import pytest
+
+from checkpoints import GGML_Q5_0, GGML_Q8_0, random_blocks
+from oracle import pyoracle as ora
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def close(y, ref):
+    d = np.abs(y.astype(np.float64) - ref)
+    scale = np.abs(ref).max(axis=-1, keepdims=True)
+    return bool(np.all(d <= TOL * np.abs(ref) + TOL * scale))
+
+
+def oracle_rows(fmt, blocks, n_out, n_in, x):
+    out = []
+    for row in x:
+        if fmt in (1, 2):
+            out.append(ora.kq_vec_dot_q8k(fmt, blocks, n_out, n_in, ora.q8k_quantize(row)))
+        else:
+            out.append(ora.q8_0_vec_dot(fmt, blocks, n_out, n_in, ora.q8_0_quantize_act(row)))
+    return np.stack(out).astype(np.float64)
+
+
+def make(dev, fmt, n_out, n_in, seed):
+    from pagoda_amd import Matrix
+
+    rng = np.random.default_rng(seed)
+    if fmt in (1, 2):
+        w = rng.normal(0, 0.02, (n_out, n_in)).astype(np.float32)
+        blk = ora.q4k_quantize(w) if fmt == 1 else ora.q6k_quantize(w)
+    else:
+        blk = random_blocks(rng, GGML_Q8_0 if fmt == 3 else GGML_Q5_0, n_out, n_in, d_std=2e-3)
+    return Matrix.upload_kq(dev, fmt, blk, n_out, n_in), blk
+
+
+SHAPES = [(4864, 896), (896, 4864), (1152, 896), (151936, 896), (40, 320)]
+
+
+@pytest.mark.parametrize("fmt", [1, 2, 3, 4])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_q8act_gemv_matches_oracle(dev, fmt, shape):
+    n_out, n_in = shape
+    if fmt in (3, 4) and n_out == 151936:
+        n_out = 8192  # keeps the random 32-weight blocks small
+    m, blk = make(dev, fmt, n_out, n_in, 100 * fmt + n_in % 97)
+    rng = np.random.default_rng(n_out + fmt)
+    x = rng.normal(0, 1, (9, n_in)).astype(np.float32)
+    x[3, :] = 0.0  # an all-zero row: d = 0 blocks
+    x[4, 5] = 40.0  # one outlier sets its block's scale
+    xd = dev.upload(x)
+    ref = oracle_rows(fmt, blk, n_out, n_in, x)
+    outs = {}
+    for rows in (1, 4, 9):
+        yd = dev.alloc(rows * n_out * 4)
+        m.gemv_q8act_dev(xd, n_in, rows, yd, n_out)
+        outs[rows] = dev.download(yd, (rows, n_out), np.float32)
+        dev.free(yd)
+        assert close(outs[rows], ref[:rows]), (rows, np.abs(outs[rows] - ref[:rows]).max())
+    # a row's result does not depend on how many rows share its launch
+    np.testing.assert_array_equal(outs[4][0].view(np.uint32), outs[1][0].view(np.uint32))
+    np.testing.assert_array_equal(outs[9][:4].view(np.uint32), outs[4].view(np.uint32))
+    # residual form
+    res = rng.normal(0, 1, (4, n_out)).astype(np.float32)
+    rd = dev.upload(res)
+    m.gemv_q8act_dev(xd, n_in, 4, rd, n_out, rd, n_out)
+    got = dev.download(rd, (4, n_out), np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), (res + outs[4]).view(np.uint32))
+    dev.free(rd)
+    dev.free(xd)
+    m.free()
+
+
+def test_q8act_rejects_a8(dev):
+    from pagoda_amd import Matrix, PagodaError
+
+    m = Matrix.synth(dev, 0, 64, 256, 1, 1, 0.02)
+    xd = dev.upload(np.ones((1, 256), np.float32))
+    yd = dev.alloc(64 * 4)
+    with pytest.raises(PagodaError):
+        m.gemv_q8act_dev(xd, 256, 1, yd, 64)
+    dev.free(xd)
+    dev.free(yd)

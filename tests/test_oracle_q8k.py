@@ -80,13 +80,11 @@ def test_kq_q8k_dot_equals_fp64_of_the_integers():
 def test_model_switch_to_q8k_mode():
     cfg = ora.Qwen2Config(n_layers=2, hidden=256, intermediate=512, vocab=512, heads=4, kv_heads=2, head_dim=64,
                           max_pos=64, rope_theta=1e6, eps=1e-6)
-    m = ora.Qwen2(cfg, 9)
+    m = ora.Qwen2(cfg, 9, kquant_mode=0)
     a = m.forward([1, 2, 3], m.new_cache())
-    try:
-        ora.set_kquant_mode(1)
-        b = m.forward([1, 2, 3], m.new_cache())
-    finally:
-        ora.set_kquant_mode(0)
+    m.set_kquant_mode(1)
+    b = m.forward([1, 2, 3], m.new_cache())
+    m.set_kquant_mode(0)
     c = m.forward([1, 2, 3], m.new_cache())
     np.testing.assert_array_equal(a, c)
     assert not np.array_equal(a, b)
