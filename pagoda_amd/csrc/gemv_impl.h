@@ -458,6 +458,12 @@ void sk_scratch_need(const GemvArgs& a, int nb, int epi, size_t* slot3, size_t* 
 void run_q8act(int fmt, const GemvArgs& a, int nrows, int epi, hipStream_t s);
 // A8 on the matrix cores (f32 activations)
 void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s);
+// A8 GEMM for prefill-sized batches: rows [0, rows) of a prepared activation
+// (whose chunks there are in the full, not compact, layout), epilogue STORE,
+// RES or SWIGLU into a.y (no prepared-output emits, no conv)
+void run_a8_gemm(const GemvArgs& a, const uint4* XA, const float* CA, int rows, int epi, hipStream_t s);
+// workgroups of that GEMM (256 weight rows, or 128 SwiGLU pairs, by 128 batch rows each)
+int a8_gemm_workgroups(int n_out, int rows, int epi);
 // Stream-K A8 kernel: whether a matrix takes it for 5..32-row launches, and
 // one launch of 5..32 rows (operand chunk XA / CA of the prepared activations)
 bool a8_sk_wanted(const GemvArgs& a, int epi);

@@ -62,7 +62,8 @@ __device__ inline h8 codes8(uint32_t w0, uint32_t w1) {
 
 // ---- activation prep (layout: a8_act.h) ----------------------------------
 // one wave per (chunk, group, batch tile); lane = 4 * row + quarter
-__global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__ x, int ldx, a8act::Dst d) {
+__global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__ x, int ldx, a8act::Dst d,
+                                                       int rows_end) {
   const size_t item = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int bt = (int)(item & 1);
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
   const int jr = lane >> 2, q = lane & 3;
   const int row = 32 * c + 16 * bt + jr;
   float v[16];
-  if (row < d.rows) {
+  if (row < rows_end) {
     const float4* xp = reinterpret_cast<const float4*>(x + (size_t)row * ldx + (g << 6) + 16 * q);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -87,7 +88,8 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = 0.0f;
   }
-  const bool live = a8act::chunk_compact(d.rows, c) ? (jr < 4) : true;
+  // rows past rows_end keep what is there (another kernel writes them)
+  const bool live = (a8act::chunk_compact(d.rows, c) ? (jr < 4) : true) && (rows_end == d.rows || row < rows_end);
   a8act::emit_slice(d, row, g, q, v, live);
 }
 
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256) void a8_xprep_kernel(const float* __restrict__
 // lanes as a8_xprep_kernel; rss: [rows][K / 32].
 __global__ __launch_bounds__(256) void a8_gnorm_prep_kernel(const float* __restrict__ x, int ldx,
                                                             const float* __restrict__ w, a8act::Dst d,
-                                                            float* __restrict__ rss) {
+                                                            float* __restrict__ rss, int rows_end) {
   const size_t item = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int bt = (int)(item & 1);
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(256) void a8_gnorm_prep_kernel(const float* __restr
   const int jr = lane >> 2, q = lane & 3;
   const int row = 32 * c + 16 * bt + jr;
   float v[16], ss = 0.0f;
-  if (row < d.rows) {
+  if (row < rows_end) {
     const float4* xp = reinterpret_cast<const float4*>(x + (size_t)row * ldx + (g << 6) + 16 * q);
     const float4* wp = reinterpret_cast<const float4*>(w + (g << 6) + 16 * q);
 #pragma unroll
@@ -130,8 +132,8 @@ __global__ __launch_bounds__(256) void a8_gnorm_prep_kernel(const float* __restr
     for (int i = 0; i < 16; ++i) v[i] = 0.0f;
   }
   ss += __shfl_xor(ss, 1, 64);  // half group: quarters (0 + 1), (2 + 3)
-  const bool live = a8act::chunk_compact(d.rows, c) ? (jr < 4) : true;
-  if (live && (q & 1) == 0 && row < d.rows) rss[(size_t)row * 2 * d.G + 2 * g + (q >> 1)] = ss;
+  const bool live = (a8act::chunk_compact(d.rows, c) ? (jr < 4) : true) && (rows_end == d.rows || row < rows_end);
+  if (live && (q & 1) == 0 && row < rows_end) rss[(size_t)row * 2 * d.G + 2 * g + (q >> 1)] = ss;
   a8act::emit_slice(d, row, g, q, v, live);
 }
 
@@ -951,6 +953,40 @@ void launch_pair(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hi
   }
 }
 
+// batches of at least two 128-row blocks take the GEMM (weights read once per
+// 128 rows) when it has work for most of the chip; below that, the GEMV
+// kernels' K splits keep more compute units streaming (measured on MI355X:
+// the qkv projection at 128 rows 183 us as 56 GEMM workgroups against 91 us
+// as two 64-row GEMV launches; 160-row steps of config 5 ran 13% slower
+// through one full and one mostly empty GEMM block)
+constexpr int kGemmRows = 128;
+constexpr int kGemmMinWorkgroups = 128;
+
+// Rows [0, rows) of a launch through the GEMM, then the prepared-output emits
+// the GEMV epilogues would have fused (the next RMSNorm's deferred input, the
+// SwiGLU product as the down projection's operands), by the prep kernels.
+template <int EPI>
+void launch_gemm_rows(const GemvArgs& a, const uint4* XA, const float* CA, int rows, hipStream_t s) {
+  GemvArgs g = a;
+  g.nact = a8act::Dst{};
+  g.oact = a8act::Dst{};
+  if (EPI == EPI_SWIGLU && !a.y) {
+    g.y = static_cast<float*>(gemv_scratch(s, (size_t)rows * a.n_out * sizeof(float), 6));
+    g.ldy = a.n_out;
+  }
+  run_a8_gemm(g, XA, CA, rows, EPI, s);
+  const a8act::Dst& out = EPI == EPI_SWIGLU ? a.oact : a.nact;
+  if (!out.XA) return;
+  const size_t items = ((size_t)rows + 31) / 32 * out.G * 2;
+  // the Dst describes the whole activation; its first rows start at a.row0 == 0
+  if (EPI == EPI_SWIGLU)
+    hipLaunchKernelGGL(a8_xprep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, g.y, g.ldy, out, rows);
+  else
+    hipLaunchKernelGGL(a8_gnorm_prep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a.y, a.ldy, a.nw, out,
+                       a.nrss, rows);
+  PGD_HIP(hipGetLastError());
+}
+
 template <int EPI>
 void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   PGD_CHECK(act.K == a.n_in, kErrShape, "prepared activations have the wrong width");
@@ -968,7 +1004,21 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
   // plain matrices stream their weights once per 64 rows when the second
   // chunk of a pair holds more than 4 rows (full operand layout)
   const bool pairs = EPI != EPI_SWIGLU && !sk && a.n_out % 4 == 0;
-  for (int c = 0; rows > 0;) {
+  int c0 = 0;
+  // whole 128-row blocks through the GEMM (a partly filled block costs a
+  // full one), the rest through the GEMV kernels
+  const int gr = rows / kGemmRows * kGemmRows;
+  if (gr >= 2 * kGemmRows && !a.cout && a.row0 == 0 &&
+      a8_gemm_workgroups(a.n_out, gr, EPI) >= kGemmMinWorkgroups) {
+    launch_gemm_rows<EPI>(a, XA, act.CA, gr, s);
+    c0 = gr / 32;
+    rows -= gr;
+    if (a.y) a.y += (size_t)gr * a.ldy;
+    if (a.res) a.res += (size_t)gr * a.ldres;
+    if (a.rss) a.rss += (size_t)gr * a.rss_nh;
+    a.row0 += gr;
+  }
+  for (int c = c0; rows > 0;) {
     const uint4* xa = XA + (size_t)c * G * 2 * 256;
     const float* ca = act.CA + (size_t)c * G * 2 * 64;
     int nb;
@@ -1062,7 +1112,8 @@ A8Act a8_act_prep(const float* x, int ldx, int rows, int K, void* buf, hipStream
   A8Act a = a8_act_view(buf, rows, K);
   if (rows <= 0) return a;
   const size_t items = ((size_t)rows + 31) / 32 * (K / 64) * 2;
-  hipLaunchKernelGGL(gemv::a8_xprep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, x, ldx, a8_act_dst(a));
+  hipLaunchKernelGGL(gemv::a8_xprep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, x, ldx, a8_act_dst(a),
+                     rows);
   PGD_HIP(hipGetLastError());
   return a;
 }
@@ -1076,7 +1127,7 @@ A8Act a8_gnorm_prep(const float* x, int ldx, int rows, int n, const float* w, fl
   if (rows <= 0) return a;
   const size_t items = ((size_t)rows + 31) / 32 * (n / 64) * 2;
   hipLaunchKernelGGL(gemv::a8_gnorm_prep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, x, ldx, w,
-                     a8_act_dst(a), rss);
+                     a8_act_dst(a), rss, rows);
   PGD_HIP(hipGetLastError());
   return a;
 }

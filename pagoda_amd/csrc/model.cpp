@@ -898,6 +898,8 @@ int pgd_step_ragged(pgd_model* pm, pgd_session* const* sessions, const uint32_t*
 }
 
 // ---- cache bytes v1 (pagoda-hf/src/qwen3_5.rs:177-255) ----
+}  // extern "C"
+
 namespace {
 void put(std::vector<uint8_t>& b, const void* p, size_t n) {
   const uint8_t* c = (const uint8_t*)p;
@@ -1052,6 +1054,8 @@ std::vector<uint8_t> export_sessionkv(const Model& m, const Session& s) {
 }
 }  // namespace
 
+extern "C" {
+
 int pgd_set_kv_wire_f16(int on) {
   g_kv_wire_f16.store(on ? 1 : 0);
   return 0;
@@ -1123,6 +1127,8 @@ int pgd_session_export(const pgd_session* ps, uint8_t* buf, size_t cap, size_t* 
     }
   });
 }
+
+}  // extern "C"
 
 namespace {
 // SessionKv::import_bytes (pagoda-hf/src/llama.rs:268-345): version 1
@@ -1215,6 +1221,8 @@ pgd_session* import_sessionkv(Model& m, const uint8_t* buf, size_t len) {
   return held;
 }
 }  // namespace
+
+extern "C" {
 
 int pgd_session_import(pgd_model* pm, const uint8_t* buf, size_t len, pgd_session** out) {
   pgd_session* held = nullptr;

@@ -86,8 +86,16 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
   for (int k = 0; k < hist; ++k) win[k] = st[k];
   for (int k = 0; k < kernel; ++k) wt[k] = weight[(size_t)c * kernel + k];
   const int r0 = row_start[s], n = row_count[s];
+  // inputs loaded eight rows ahead (the steps are sequential; the loads are not)
+  constexpr int PF = 8;
+  float xr[PF];
+#pragma unroll
+  for (int k = 0; k < PF; ++k) xr[k] = k < n ? x[(size_t)(r0 + k) * ldx + c] : 0.0f;
   for (int t = 0; t < n; ++t) {
-    const float xv = x[(size_t)(r0 + t) * ldx + c];
+    const float xv = xr[0];
+#pragma unroll
+    for (int k = 0; k + 1 < PF; ++k) xr[k] = xr[k + 1];
+    xr[PF - 1] = t + PF < n ? x[(size_t)(r0 + t + PF) * ldx + c] : 0.0f;
     float acc = 0.0f;
     for (int k = 0; k < hist; ++k) acc += win[k] * wt[k];
     acc += xv * wt[hist];
@@ -138,13 +146,30 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
   // the gate input z and the norm weight are loaded with the step's other
   // inputs, not after the reductions that need them
   const float nw = tid < D ? p.norm[tid] : 0.0f;
+  // a step's inputs (gate z, v, this thread's q or k element, the a / b gate
+  // inputs) are loaded one step ahead, so a prefill's sequential steps do
+  // not wait for memory each
+  struct In {
+    float zg, vv, v, ar, br;
+  };
+  auto load_in = [&](int row) {
+    const float* cv = p.conv_out + (size_t)row * p.ld_conv;
+    In x;
+    x.zg = tid < D ? p.z[(size_t)row * p.ld_z + h * D + tid] : 0.0f;
+    x.vv = tid < D ? cv[2 * key_dim + h * D + tid] : 0.0f;
+    x.v = tid < D ? cv[kh * D + tid] : cv[key_dim + kh * D + (tid - D)];
+    x.ar = p.a[(size_t)row * p.ld_ab + h];
+    x.br = p.b[(size_t)row * p.ld_ab + h];
+    return x;
+  };
+  In nxt = load_in(r0);
   for (int t = 0; t < n; ++t) {
     const int row = r0 + t;
-    const float* cv = p.conv_out + (size_t)row * p.ld_conv;
-    const float zg = tid < D ? p.z[(size_t)row * p.ld_z + h * D + tid] : 0.0f;
-    const float vv = tid < D ? cv[2 * key_dim + h * D + tid] : 0.0f;
+    const In cur = nxt;
+    if (t + 1 < n) nxt = load_in(row + 1);
+    const float zg = cur.zg, vv = cur.vv;
     // q (threads 0..127) and k (128..255), L2-normalized per head
-    float v = tid < D ? cv[kh * D + tid] : cv[key_dim + kh * D + (tid - D)];
+    float v = cur.v;
     float ss = wave_sum(v * v);
     if ((tid & 63) == 0) part[tid >> 6] = ss;
     __syncthreads();
@@ -155,9 +180,9 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
       float inv = 1.0f / sqrtf(part[2] + part[3] + 1e-6f);
       ks[tid - D] = v * inv;
     }
-    const float g = -expf(a_log) * softplus_f(p.a[(size_t)row * p.ld_ab + h] + dtb);
+    const float g = -expf(a_log) * softplus_f(cur.ar + dtb);
     const float decay = expf(g);
-    const float beta = 1.0f / (1.0f + expf(-p.b[(size_t)row * p.ld_ab + h]));
+    const float beta = 1.0f / (1.0f + expf(-cur.br));
     __syncthreads();
     // S *= decay; mem = S^T k (partial over this thread's 16 rows)
     float m4[4] = {0.0f, 0.0f, 0.0f, 0.0f};

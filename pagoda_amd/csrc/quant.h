@@ -201,6 +201,8 @@ void synth_uniform_f32(float* out, size_t n, uint64_t seed, uint64_t key, float 
 void fill_f32(float* out, size_t n, float v, hipStream_t s);
 
 namespace gemv {
+// Per-stream device scratch buffers that grow on demand (slots: see gemv_impl.h).
+void* gemv_scratch(hipStream_t s, size_t bytes, int slot);
 // A caller-provided device region that gemv::gemv_scratch carves its slots from,
 // on the calling thread only, instead of allocating: each slot gets one
 // 256-byte aligned range on first use and keeps it while it is large enough

@@ -226,3 +226,31 @@ def test_config4_full_depth_greedy_32_and_batch32(dev, capsys):
         x.free()
     model.free()
     say(f"batch-32 step checked ({time.time() - t0:.1f} s)")
+
+
+def test_config4_widths_prefill_300_tokens(dev):
+    """A 300-token prompt at config-4 widths (one 3:1 layer group) is
+    prefilled through the A8 GEMM (weights read once per 128 rows) and the
+    GEMM path's prepared-output emits; logits against the oracle within 1e-3,
+    then 4 greedy decode steps."""
+    from dataclasses import replace
+
+    from pagoda_amd.engine import QWEN35_27B, Model, argmax_first
+
+    cfg = replace(QWEN35_27B, n_layers=4, vocab=32768, max_pos=512, kv_blocks=64)
+    seed = 6
+    model = Model.synth(dev, cfg, seed)
+    oracle = ora.Qwen35(ora.Qwen35Config(n_layers=4, vocab=32768), seed)
+    prompt = np.random.default_rng(300).integers(0, cfg.vocab, 300)
+    s = model.new_session()
+    oc = oracle.new_cache()
+    got = s.forward(prompt)
+    ref = oracle.forward(prompt, oc)
+    assert rel(got, ref) < LOGIT_TOL and _elementwise_ok(got, ref)
+    for step in range(4):
+        assert argmax_first(got) == ora.argmax_first(ref), step
+        t = ora.argmax_first(ref)
+        got, ref = s.forward([t]), oracle.forward([t], oc)
+        assert rel(got, ref) < LOGIT_TOL, (step, rel(got, ref))
+    s.free()
+    model.free()

@@ -347,3 +347,25 @@ def test_shared_trunk_mixed_decode_and_verify(which, request):
             ref = oracle.forward([streams[1][k]], oc)
     for s in reqs + snap + [root]:
         s.free()
+
+
+def test_long_and_short_prefill_in_one_step(m35):
+    """A 150-token and a 7-token sequence prefilled in one ragged step (the
+    long one's GEMVs take whole 128-row GEMM blocks only through the batch),
+    both against the oracle, then decode."""
+    model, oracle = m35
+    rng = np.random.default_rng(77)
+    long_p, short_p = rng.integers(0, model.cfg.vocab, 150), rng.integers(0, model.cfg.vocab, 7)
+    a, b = model.new_session(), model.new_session()
+    _, logits = model.step_ragged([a, b], [long_p, short_p], want_logits=True)
+    oa, ob = oracle.new_cache(), oracle.new_cache()
+    ra, rb = oracle.forward(long_p, oa), oracle.forward(short_p, ob)
+    assert rel(logits[0], ra) < LOGIT_TOL and rel(logits[1], rb) < LOGIT_TOL
+    for step in range(4):
+        t = ora.argmax_first(ra)
+        assert ora.argmax_first(logits[0]) == t, step
+        g, ra = a.forward([t]), oracle.forward([t], oa)
+        assert rel(g, ra) < LOGIT_TOL, step
+        logits = [g]
+    a.free()
+    b.free()

@@ -371,3 +371,43 @@ def test_a8_stream_k_swiglu(dev, n_out, n_in):
     a, b = x64 @ dg.T, x64 @ du.T
     ref = a / (1.0 + np.exp(-a)) * b
     _class_checks(full, run(x[:7]), run(x[32:45]), run(x[3:4])[0], ref)
+
+
+@pytest.mark.parametrize("rows", [256, 300, 390, 516])
+@pytest.mark.parametrize("epi", ["store", "res", "swiglu"])
+def test_a8_prefill_gemm(dev, rows, epi):
+    """Batches of >= 256 rows take the A8 GEMM for their whole 128-row blocks
+    (weights read once per 128 rows) and the GEMV kernels for the rest (44
+    rows at 300, a 6-row partial chunk at 390, a compact 4-row chunk at 516):
+    against fp64 on the same dequantized weights, elementwise, for the store,
+    in-place residual and SwiGLU epilogues; n_out 1000 leaves a partial
+    weight tile."""
+    from pagoda_amd import Matrix
+    from pagoda_amd.matrix import act_bytes, act_prep_dev
+
+    n_out, K = 1000, 640
+    m = Matrix.synth(dev, 0, n_out, K, 61, 3, 0.02)
+    u = Matrix.synth(dev, 0, n_out, K, 62, 4, 0.02) if epi == "swiglu" else None
+    rng = np.random.default_rng(rows)
+    x = rng.normal(0, 1, (rows, K)).astype(np.float32)
+    xd = dev.upload(x)
+    act = dev.alloc(act_bytes(rows, K))
+    act_prep_dev(dev, xd, K, rows, K, act)
+    res = rng.normal(0, 1, (rows, n_out)).astype(np.float32)
+    yd = dev.upload(res)
+    x64 = x.astype(np.float64)
+    if epi == "swiglu":
+        Matrix.gemv_swiglu_act_dev(m, u, act, rows, yd, n_out)
+        g = x64 @ m.dequant().astype(np.float64).T
+        up = x64 @ u.dequant().astype(np.float64).T
+        ref = g / (1.0 + np.exp(-g)) * up
+    elif epi == "res":
+        m.gemv_act_dev(act, rows, yd, n_out, yd, n_out)
+        ref = res.astype(np.float64) + x64 @ m.dequant().astype(np.float64).T
+    else:
+        m.gemv_act_dev(act, rows, yd, n_out)
+        ref = x64 @ m.dequant().astype(np.float64).T
+    got = dev.download(yd, (rows, n_out), np.float32)
+    assert rel_err(got, ref) < GEMV_TOL, rel_err(got, ref)
+    for p in (xd, act, yd):
+        dev.free(p)
