@@ -342,12 +342,13 @@ def test_a8_stream_k_tall_matrix(dev, n_out, n_in):
     _class_checks(full, m.gemv(x[:7]), m.gemv(x[32:45]), m.gemv(x[3]), ref)
 
 
-@pytest.mark.parametrize("n_out,n_in", [(1000, 512), (2000, 5120)])
+@pytest.mark.parametrize("n_out,n_in", [(1000, 512), (2000, 5120), (4128, 64), (17408, 5120)])
 def test_a8_stream_k_swiglu(dev, n_out, n_in):
     """The fused gate/up SwiGLU GEMV takes the stream-K kernel for 5..32 rows:
     silu(x Wg^T) * (x Wu^T) against fp64 over the dequantized weights; ragged
-    last tile (n_out % 32 != 0) and blocks cut into many runs (K = 5120 with
-    few tiles)."""
+    last tile (n_out % 32 != 0), blocks cut into many runs (K = 5120),
+    one-group rows (K = 64: every block whole in one run), the config-4
+    shape. Every launch is repeated and must give the same bits."""
     from pagoda_amd import Matrix
 
     g = Matrix.synth(dev, 0, n_out, n_in, 11, 1, 0.02)
@@ -362,6 +363,9 @@ def test_a8_stream_k_swiglu(dev, n_out, n_in):
         md = dev.alloc(rows * n_out * 4)
         Matrix.gemv_swiglu_dev(g, u, xd, n_in, rows, md, n_out)
         out = dev.download(md, (rows, n_out), np.float32)
+        Matrix.gemv_swiglu_dev(g, u, xd, n_in, rows, md, n_out)
+        again = dev.download(md, (rows, n_out), np.float32)
+        np.testing.assert_array_equal(again.view(np.uint32), out.view(np.uint32))
         dev.free(xd)
         dev.free(md)
         return out
@@ -411,3 +415,4 @@ def test_a8_prefill_gemm(dev, rows, epi):
     assert rel_err(got, ref) < GEMV_TOL, rel_err(got, ref)
     for p in (xd, act, yd):
         dev.free(p)
+
