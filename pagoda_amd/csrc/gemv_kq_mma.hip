@@ -19,7 +19,11 @@
 // its 8 codes of sub-block 2 * (g % 4) and high nibbles those of the next.
 // Workgroups hold KS waves sharing one 32-row tile (KS from the shape) and
 // splitting its groups; each wave keeps PF groups of loads in flight; the
-// waves' partial sums meet in LDS in a fixed order.
+// waves' partial sums meet in LDS in a fixed order. Matrices of few tiles and
+// a long K (the 896-row down projection: 28 tiles) also split K over GS
+// workgroups per tile (grid y); their sums go to a workspace and
+// kq_part_reduce_kernel adds them in part order and applies the epilogue.
+// The split depends on the shape only, so batch rows stay bitwise equal.
 #include <type_traits>
 
 #include "common.h"
@@ -97,11 +101,79 @@ __device__ inline void stage_x(char* xs, const GemvArgs& a, int nb) {
   __syncthreads();
 }
 
+// ---- grid k split ----------------------------------------------------------
+// Workgroups per tile along K for a matrix of `tiles` tiles and U k units
+// (Q4_K: 64-groups, Q6_K: 128-halves): enough workgroups to reach ~128 when
+// the tiles alone give fewer, for K of at least min_units (below that a
+// matrix is too small to repay the second launch); 1 = no grid split.
+inline int grid_split(int tiles, int U, int min_units) {
+  if (tiles >= 128 || U < min_units) return 1;
+  int gs = 1;
+  while (gs < 8 && tiles * gs < 128) gs *= 2;
+  return gs;
+}
+// waves per workgroup under a grid split: each keeps >= 2 k units
+inline int grid_split_ks(int U, int gs) {
+  int ks = 2;
+  while (ks < 8 && 2 * ks * gs * 2 <= U) ks *= 2;
+  return ks;
+}
+
+// sums of one workgroup (lane: row n of subtile st, batch rows 16 bt + 4 q + r)
+// into the workspace [matrix][part][row][n_out]
+template <int NS, int NBT, bool DUAL>
+__device__ inline void store_part(const GemvArgs& a, int nb, int tile, const f4 (&Y)[NS][NBT]) {
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int n = tile * 32 + 16 * (st & 1) + j;
+    if (n >= a.n_out) continue;
+    const int m = (DUAL && st >= 2) ? 1 : 0;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int b = 16 * bt + 4 * q + r;
+        if (b < nb) a.y[(((size_t)m * gridDim.y + blockIdx.y) * nb + b) * a.n_out + n] = Y[st][bt][r];
+      }
+  }
+}
+
+// y = epilogue(sum over parts 0, 1, .. in order) of the workspace
+template <int EPI>
+__global__ __launch_bounds__(256) void kq_part_reduce_kernel(GemvArgs a, const float* __restrict__ ws, int gs, int nb) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, plane = (size_t)nb * a.n_out;
+  if (i >= plane) return;
+  const int b = (int)(i / a.n_out), n = (int)(i % a.n_out);
+  float v = ws[i];
+  for (int p = 1; p < gs; ++p) v += ws[p * plane + i];
+  const size_t o = (size_t)b * a.ldy + n;
+  if constexpr (EPI == EPI_STORE) a.y[o] = v;
+  if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + v;
+  if constexpr (EPI == EPI_SWIGLU) {
+    float u = ws[gs * plane + i];
+    for (int p = 1; p < gs; ++p) u += ws[(gs + p) * plane + i];
+    a.y[o] = silu_f(v) * u;
+  }
+}
+
+inline float* part_workspace(const GemvArgs& a, int nb, int gs, bool dual, hipStream_t s) {
+  return static_cast<float*>(gemv_scratch(s, (size_t)(dual ? 2 : 1) * gs * nb * a.n_out * sizeof(float), 1));
+}
+
+template <int EPI>
+void launch_part_reduce(const GemvArgs& a, const float* ws, int gs, int nb, hipStream_t s) {
+  const size_t n = (size_t)nb * a.n_out;
+  hipLaunchKernelGGL((kq_part_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, ws, gs, nb);
+}
+
 // XL (KS == 1 only): the activation rows are staged in LDS once per
 // workgroup and read from there; the register ring then carries weights only.
-template <int NBT, int KS, int PF, bool XF16, int EPI, bool XL = false>
+// PART: this workgroup's sums go to the workspace a.y, [matrix][part][row][n_out]
+template <int NBT, int KS, int PF, bool XF16, int EPI, bool XL = false, bool PART = false>
 __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kernel(GemvArgs a, int nb) {
   static_assert(!XL || KS == 1, "staged activations with whole-K waves only");
+  static_assert(!PART || KS > 1, "a grid k split keeps one tile per workgroup");
   extern __shared__ __attribute__((aligned(16))) char xs[];
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr int NS = DUAL ? 4 : 2;
@@ -219,8 +291,11 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kerne
     }
   };
 
-  const int per = (G + KS - 1) / KS;
-  const int g0 = wave * per, g1 = min(G, g0 + per);
+  // this workgroup's groups [gb, ge) (grid part blockIdx.y of gridDim.y), then this wave's
+  const int gper = PART ? (G + (int)gridDim.y - 1) / (int)gridDim.y : G;
+  const int gb = PART ? min(G, (int)blockIdx.y * gper) : 0, ge = min(G, gb + gper);
+  const int per = (ge - gb + KS - 1) / KS;
+  const int g0 = min(ge, gb + wave * per), g1 = min(ge, g0 + per);
   Q4Raw<NBT, NS, XF16> buf[PF];
 #pragma unroll
   for (int u = 0; u < PF; ++u)
@@ -251,6 +326,10 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kerne
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[w][st][bt][lane];
   }
+  if constexpr (PART) {
+    store_part<NS, NBT, DUAL>(a, nb, tile, Y);
+    return;
+  }
   // ---- epilogue: lane holds weight row n for batch rows 16bt + 4q + r ----
 #pragma unroll
   for (int st = 0; st < (DUAL ? 2 : NS); ++st) {
@@ -280,6 +359,19 @@ inline int q4k_split(const GemvArgs& a) {
   while (ks < 8 && tiles * ks < 1024 && G / (2 * ks) >= 2) ks *= 2;
   return ks;
 }
+// workgroups per tile along K (1: none); ks then re-chosen by grid_split_ks
+inline int q4k_grid_split(const GemvArgs& a) { return grid_split((a.n_out + 31) / 32, a.n_in / 64, 32); }
+
+template <int NBT, int KS, bool XF16, int EPI>
+void q4k_launch_part(const GemvArgs& a, int nb, int gs, hipStream_t s) {
+  constexpr bool DUAL = EPI == EPI_SWIGLU;
+  const int tiles = (a.n_out + 31) / 32;
+  GemvArgs p = a;
+  float* ws = part_workspace(a, nb, gs, DUAL, s);
+  p.y = ws;
+  hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI, false, true>), dim3(tiles, gs), dim3(64 * KS), 0, s, p, nb);
+  launch_part_reduce<EPI>(a, ws, gs, nb, s);
+}
 
 template <int NBT, int KS, bool XF16, int EPI>
 void q4k_launch(const GemvArgs& a, int nb, hipStream_t s) {
@@ -300,6 +392,13 @@ void q4k_launch(const GemvArgs& a, int nb, hipStream_t s) {
 
 template <int NBT, bool XF16, int EPI>
 void q4k_launch_ks(const GemvArgs& a, int nb, hipStream_t s) {
+  if (const int gs = q4k_grid_split(a); gs > 1) {
+    switch (grid_split_ks(a.n_in / 64, gs)) {
+      case 2: return q4k_launch_part<NBT, 2, XF16, EPI>(a, nb, gs, s);
+      case 4: return q4k_launch_part<NBT, 4, XF16, EPI>(a, nb, gs, s);
+      default: return q4k_launch_part<NBT, 8, XF16, EPI>(a, nb, gs, s);
+    }
+  }
   switch (q4k_split(a)) {
     case 1: return q4k_launch<NBT, 1, XF16, EPI>(a, nb, s);
     case 2: return q4k_launch<NBT, 2, XF16, EPI>(a, nb, s);
@@ -358,9 +457,10 @@ struct Q6Raw {
   XT x[8][NBT];
 };
 
-template <int NBT, int KS, bool XF16, int EPI>
+template <int NBT, int KS, bool XF16, int EPI, bool PART = false>
 __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q6k_mma_kernel(GemvArgs a, int nb) {
   static_assert(EPI != EPI_SWIGLU, "one matrix per wave");
+  static_assert(!PART || KS > 1, "a grid k split keeps one tile per workgroup");
   constexpr int NS = 2;
   __shared__ f4 red[KS > 1 ? KS - 1 : 1][NS][NBT][64];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -472,8 +572,11 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q6k_mma_kerne
   };
 
   // double buffer: the next half's loads are in flight during this one's MFMAs
-  const int per = (H + KS - 1) / KS;
-  const int u0 = min(H, wave * per), u1 = min(H, u0 + per);
+  // this workgroup's halves [hb, he) (grid part blockIdx.y of gridDim.y), then this wave's
+  const int hper = PART ? (H + (int)gridDim.y - 1) / (int)gridDim.y : H;
+  const int hb = PART ? min(H, (int)blockIdx.y * hper) : 0, he = min(H, hb + hper);
+  const int per = (he - hb + KS - 1) / KS;
+  const int u0 = min(he, hb + wave * per), u1 = min(he, u0 + per);
   Raw cur, nxt;
   if (u0 < u1) load(u0, cur);
   for (int u = u0; u < u1; ++u) {
@@ -497,6 +600,10 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q6k_mma_kerne
       for (int st = 0; st < NS; ++st)
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) Y[st][bt] += red[w][st][bt][lane];
+  }
+  if constexpr (PART) {
+    store_part<NS, NBT, false>(a, nb, tile, Y);
+    return;
   }
 #pragma unroll
   for (int st = 0; st < NS; ++st) {
@@ -677,8 +784,25 @@ void q6k_launch(const GemvArgs& a, int nb, hipStream_t s) {
     hipLaunchKernelGGL((q6k_mma_kernel<NBT, KS, XF16, EPI>), dim3(tiles), dim3(64 * KS), 0, s, a, nb);
 }
 
+template <int NBT, int KS, bool XF16, int EPI>
+void q6k_launch_part(const GemvArgs& a, int nb, int gs, hipStream_t s) {
+  const int tiles = (a.n_out + 31) / 32;
+  GemvArgs p = a;
+  float* ws = part_workspace(a, nb, gs, false, s);
+  p.y = ws;
+  hipLaunchKernelGGL((q6k_mma_kernel<NBT, KS, XF16, EPI, true>), dim3(tiles, gs), dim3(64 * KS), 0, s, p, nb);
+  launch_part_reduce<EPI>(a, ws, gs, nb, s);
+}
+
 template <int NBT, bool XF16, int EPI>
 void q6k_launch_ks(const GemvArgs& a, int nb, hipStream_t s) {
+  if (const int gs = grid_split((a.n_out + 31) / 32, a.n_in / 128, 16); gs > 1) {
+    switch (grid_split_ks(a.n_in / 128, gs)) {
+      case 2: return q6k_launch_part<NBT, 2, XF16, EPI>(a, nb, gs, s);
+      case 4: return q6k_launch_part<NBT, 4, XF16, EPI>(a, nb, gs, s);
+      default: return q6k_launch_part<NBT, 8, XF16, EPI>(a, nb, gs, s);
+    }
+  }
   switch (q6k_split(a)) {
     case 1: return q6k_launch<NBT, 1, XF16, EPI>(a, nb, s);
     case 2: return q6k_launch<NBT, 2, XF16, EPI>(a, nb, s);
