@@ -80,7 +80,7 @@ struct Q4Raw {
 
 // KS == 1: a workgroup of kTilesKS1 waves, one tile each (no k split)
 constexpr int kTilesKS1 = 4;
-// activation rows staged in LDS (XL kernels): at most this many bytes, rows
+// activation rows staged in LDS (the *_lds kernels): at most this many bytes, rows
 // padded by 16 B against bank conflicts
 constexpr int kXLdsMax = 64 * 1024;
 __host__ __device__ inline int x_lds_stride(int K, bool f16) { return K * (f16 ? 2 : 4) + 16; }
@@ -167,26 +167,20 @@ void launch_part_reduce(const GemvArgs& a, const float* ws, int gs, int nb, hipS
   hipLaunchKernelGGL((kq_part_reduce_kernel<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, ws, gs, nb);
 }
 
-// XL (KS == 1 only): the activation rows are staged in LDS once per
-// workgroup and read from there; the register ring then carries weights only.
 // PART: this workgroup's sums go to the workspace a.y, [matrix][part][row][n_out]
-template <int NBT, int KS, int PF, bool XF16, int EPI, bool XL = false, bool PART = false>
+template <int NBT, int KS, int PF, bool XF16, int EPI, bool PART = false>
 __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kernel(GemvArgs a, int nb) {
-  static_assert(!XL || KS == 1, "staged activations with whole-K waves only");
   static_assert(!PART || KS > 1, "a grid k split keeps one tile per workgroup");
-  extern __shared__ __attribute__((aligned(16))) char xs[];
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr int NS = DUAL ? 4 : 2;
   __shared__ f4 red[KS > 1 ? KS - 1 : 1][NS][NBT][64];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, q = lane >> 4;
   const int G = a.n_in >> 6, nsb = a.nsb, G4 = 4 * nsb;
-  if constexpr (XL) stage_x<NBT, XF16>(xs, a, nb);
   // wave = this wave's k range; KS == 1: every wave its own tile
   const int wave = KS == 1 ? 0 : wv;
   const int tile = KS == 1 ? blockIdx.x * kTilesKS1 + wv : blockIdx.x;
   if (tile >= (a.n_out + 31) / 32) return;
-  const int XRS = x_lds_stride(a.n_in, XF16);
 
   const uint8_t* wbase[NS];
   const uint8_t* hbase[NS];
@@ -213,25 +207,18 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kerne
       R.w[st] = *reinterpret_cast<const uint2*>(wbase[st] + (size_t)g * 1024);
       R.hdr[st] = *reinterpret_cast<const uint4*>(hbase[st] + (size_t)(g >> 2) * 512);
     }
-    if constexpr (!XL) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int bt = 0; bt < NBT; ++bt) {
-          const int k0 = 64 * g + 32 * h + 8 * q;
-          if constexpr (XF16) {
-            R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 2);
-          } else {
-            R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4);
-            R.x[h][bt][1] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4 + 16);
-          }
+      for (int bt = 0; bt < NBT; ++bt) {
+        const int k0 = 64 * g + 32 * h + 8 * q;
+        if constexpr (XF16) {
+          R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 2);
+        } else {
+          R.x[h][bt][0] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4);
+          R.x[h][bt][1] = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)k0 * 4 + 16);
         }
-    }
-  };
-  // staged activations: the same 16 (f16) or 32 (f32) bytes, from LDS
-  auto x_lds = [&](int g, int h, int bt, int i) -> uint4 {
-    const int k0 = 64 * g + 32 * h + 8 * q;
-    return *reinterpret_cast<const uint4*>(xs + (16 * bt + j) * XRS + k0 * (XF16 ? 2 : 4) + 16 * i);
+      }
   };
 
   f4 Y[NS][NBT];
@@ -249,12 +236,12 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kerne
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) {
-        const uint4 x0 = XL ? x_lds(g, h, bt, 0) : R.x[h][bt][0];
+        const uint4 x0 = R.x[h][bt][0];
         if constexpr (XF16) {
           xh[h][bt] = __builtin_bit_cast(h8, x0);
           XS[h][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[h][bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         } else {
-          const uint4 x1 = XL ? x_lds(g, h, bt, 1) : R.x[h][bt][XF16 ? 0 : 1];
+          const uint4 x1 = R.x[h][bt][XF16 ? 0 : 1];
           const float v[8] = {__builtin_bit_cast(float, x0.x), __builtin_bit_cast(float, x0.y),
                               __builtin_bit_cast(float, x0.z), __builtin_bit_cast(float, x0.w),
                               __builtin_bit_cast(float, x1.x), __builtin_bit_cast(float, x1.y),
@@ -349,9 +336,143 @@ __global__ __launch_bounds__(64 * (KS == 1 ? kTilesKS1 : KS)) void q4k_mma_kerne
   }
 }
 
-#ifndef Q4_LPF
-#define Q4_LPF 2
-#endif
+// Tall Q4_K matrices with a short K (no k split, one wave per tile, <= 16
+// rows): the staged-activation form of q4k_mma_kernel with units of two
+// 64-groups of one super-block, so each row's 16-byte header is loaded once
+// per two groups, and a PF-unit register ring whose loads past the last unit
+// re-read it (cache hits) instead of branching. Same arithmetic and group
+// order as q4k_mma_kernel with KS == 1.
+template <int NS>
+struct Q4W {
+  uint2 w[2][NS];  // 8 qs bytes per group and subtile
+  uint4 hdr[NS];   // the unit's super-block header per subtile row
+};
+
+template <int NBT, int PF, bool XF16, int EPI>
+__global__ __launch_bounds__(64 * kTilesKS1) void q4k_lds_kernel(GemvArgs a, int nb) {
+  constexpr bool DUAL = EPI == EPI_SWIGLU;
+  constexpr int NS = DUAL ? 4 : 2;
+  extern __shared__ __attribute__((aligned(16))) char xs[];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, q = lane >> 4;
+  const int G = a.n_in >> 6, nsb = a.nsb, G4 = 4 * nsb, UN = (G + 1) / 2;
+  stage_x<NBT, XF16>(xs, a, nb);
+  const int tile = blockIdx.x * kTilesKS1 + wv;
+  if (tile >= (a.n_out + 31) / 32) return;
+  const int XRS = x_lds_stride(a.n_in, XF16);
+
+  const uint8_t* wbase[NS];
+  const uint8_t* hbase[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const uint8_t* p = (DUAL && st >= 2) ? a.u0 : a.p0;
+    const uint8_t* ph = (DUAL && st >= 2) ? a.u1 : a.p1;
+    const int r = 16 * (st & 1) + j;
+    wbase[st] = p + (size_t)tile * G4 * 1024 + r * 32 + 8 * q;
+    hbase[st] = ph + (size_t)tile * nsb * 512 + r * 16;
+  }
+  using W = Q4W<NS>;
+  // unit u: groups 2u, 2u + 1 (one super-block); a missing second group re-reads the first
+  auto load = [&](int u, W& R) {
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+        R.w[h2][st] = *reinterpret_cast<const uint2*>(wbase[st] + (size_t)min(2 * u + h2, G - 1) * 1024);
+      R.hdr[st] = *reinterpret_cast<const uint4*>(hbase[st] + (size_t)(u >> 1) * 512);
+    }
+  };
+
+  f4 Y[NS][NBT];
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) Y[st][bt] = (f4){0.f, 0.f, 0.f, 0.f};
+  const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+
+  auto compute_group = [&](int g, const uint2 (&w)[NS], const uint4 (&hdr)[NS]) {
+    h8 xh[2][NBT], xl[2][NBT];
+    f4 XS[2][NBT];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const char* xp = xs + (16 * bt + j) * XRS + (64 * g + 32 * h + 8 * q) * (XF16 ? 2 : 4);
+        const uint4 x0 = *reinterpret_cast<const uint4*>(xp);
+        if constexpr (XF16) {
+          xh[h][bt] = __builtin_bit_cast(h8, x0);
+          XS[h][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[h][bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        } else {
+          const uint4 x1 = *reinterpret_cast<const uint4*>(xp + 16);
+          const float v[8] = {__builtin_bit_cast(float, x0.x), __builtin_bit_cast(float, x0.y),
+                              __builtin_bit_cast(float, x0.z), __builtin_bit_cast(float, x0.w),
+                              __builtin_bit_cast(float, x1.x), __builtin_bit_cast(float, x1.y),
+                              __builtin_bit_cast(float, x1.z), __builtin_bit_cast(float, x1.w)};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const _Float16 hv = (_Float16)v[e];
+            xh[h][bt][e] = hv;
+            xl[h][bt][e] = (_Float16)(v[e] - (float)hv);
+          }
+          f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[h][bt], ones, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          XS[h][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[h][bt], ones, t, 0, 0, 0);
+        }
+      }
+    const int js = 2 * (g & 3);
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      const float d = f16_to_f32(hdr[st].x & 0xffffu), dmin = f16_to_f32(hdr[st].x >> 16);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float sc, m;
+        q4k_sc_m(hdr[st], js + h, sc, m);
+        const float ca = d * sc;
+        const float cb = fmaf(1024.0f, ca, dmin * m);
+        const h8 bq = nib8(w[st].x, w[st].y, h);
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+          f4 P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[h][bt], bq, (f4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          if constexpr (!XF16) P = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[h][bt], bq, P, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Y[st][bt][r] = fmaf(ca, P[r], fmaf(-cb, XS[h][bt][r], Y[st][bt][r]));
+        }
+      }
+    }
+  };
+
+  W buf[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) load(min(i, UN - 1), buf[i]);
+  for (int u = 0; u < UN; u += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      if (u + i < UN) {
+        compute_group(2 * (u + i), buf[i].w[0], buf[i].hdr);
+        if (2 * (u + i) + 1 < G) compute_group(2 * (u + i) + 1, buf[i].w[1], buf[i].hdr);
+      }
+      load(min(u + i + PF, UN - 1), buf[i]);
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < (DUAL ? 2 : NS); ++st) {
+    const int n = tile * 32 + 16 * (st & 1) + j;
+    if (n >= a.n_out) continue;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int b = 16 * bt + 4 * q + r;
+        if (b >= nb) continue;
+        const size_t o = (size_t)b * a.ldy + n;
+        if constexpr (EPI == EPI_STORE) a.y[o] = Y[st][bt][r];
+        if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];
+        if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(Y[st][bt][r]) * Y[2 + st][bt][r];
+      }
+  }
+}
+
+// units in flight of q4k_lds_kernel (deeper rings measured slower)
+constexpr int kQ4UnitsInFlight = 2;
 // split of the groups: depends on the matrix shape only
 inline int q4k_split(const GemvArgs& a) {
   const int tiles = (a.n_out + 31) / 32, G = a.n_in / 64;
@@ -369,7 +490,7 @@ void q4k_launch_part(const GemvArgs& a, int nb, int gs, hipStream_t s) {
   GemvArgs p = a;
   float* ws = part_workspace(a, nb, gs, DUAL, s);
   p.y = ws;
-  hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI, false, true>), dim3(tiles, gs), dim3(64 * KS), 0, s, p, nb);
+  hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI, true>), dim3(tiles, gs), dim3(64 * KS), 0, s, p, nb);
   launch_part_reduce<EPI>(a, ws, gs, nb, s);
 }
 
@@ -378,9 +499,9 @@ void q4k_launch(const GemvArgs& a, int nb, hipStream_t s) {
   const int tiles = (a.n_out + 31) / 32;
   const size_t xlds = (size_t)16 * NBT * x_lds_stride(a.n_in, XF16);
   if constexpr (KS == 1) {
-    // staged activations pay at <= 16 rows (measured: slower at 17..32)
+    // staged activations pay at <= 16 rows (at 17..32 rows measured no faster)
     if (NBT == 1 && xlds <= kXLdsMax)
-      hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, Q4_LPF, XF16, EPI, true>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
+      hipLaunchKernelGGL((q4k_lds_kernel<NBT, kQ4UnitsInFlight, XF16, EPI>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
                          dim3(64 * kTilesKS1), xlds, s, a, nb);
     else
       hipLaunchKernelGGL((q4k_mma_kernel<NBT, KS, 2, XF16, EPI>), dim3((tiles + kTilesKS1 - 1) / kTilesKS1),
