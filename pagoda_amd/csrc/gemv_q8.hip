@@ -440,7 +440,15 @@ __global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(GemvArgs a, int rows) 
 template <int FMT, int RB, int NW, int EPI>
 void launch_q8(GemvArgs a, int nrows, hipStream_t s) {
   const size_t lds = ActLds<FMT, RB, NW>::bytes(a.n_in, EPI == EPI_SWIGLU ? 2 : 1);
-  PGD_CHECK(lds <= 64 * 1024, kErrShape, "activation rows too wide for the quantized-activation GEMV");
+  PGD_CHECK(lds <= 160 * 1024, kErrShape, "activation rows too wide for the quantized-activation GEMV");
+  if (lds > 64 * 1024) {
+    static bool set = false;  // per kernel instance: the largest LDS it may be launched with
+    if (!set) {
+      PGD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<FMT, RB, NW, EPI>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      set = true;
+    }
+  }
   const int tiles = (a.n_out + 31) / 32;
   for (int r0 = 0; r0 < nrows; r0 += RB) {
     const int rows = min(RB, nrows - r0);
@@ -462,11 +470,14 @@ void launch_waves(const GemvArgs& a, int nrows, hipStream_t s) {
   launch_q8<FMT, RB, 16, EPI>(a, nrows, s);
 }
 
+// rows per launch: decode steps take 1..8; prefills 16 at a time (weights
+// read once per 16 rows)
 template <int FMT, int EPI>
 void launch_rows(const GemvArgs& a, int nrows, hipStream_t s) {
   if (nrows == 1) return launch_waves<FMT, 1, EPI>(a, nrows, s);
   if (nrows <= 4) return launch_waves<FMT, 4, EPI>(a, nrows, s);
-  launch_waves<FMT, 8, EPI>(a, nrows, s);
+  if (nrows <= 8) return launch_waves<FMT, 8, EPI>(a, nrows, s);
+  launch_waves<FMT, 16, EPI>(a, nrows, s);
 }
 
 template <int EPI>
