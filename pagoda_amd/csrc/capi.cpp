@@ -319,7 +319,7 @@ int pgd_gdn_step_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_o
     p.ld_out = v_heads * 128;
     p.state_base = states;
     p.state_off = 0;
-    gdn_step(p, SeqMeta{row_start, row_count}, nseq, dev->stream);
+    gdn_step(p, SeqMeta{row_start, row_count}, nseq, 0, 0, dev->stream);
   });
 }
 

@@ -389,8 +389,9 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       while (s->blocks.size() < want) s->blocks.push_back(m.alloc_block());
     }
   }
-  int max_pos = 0;
+  int max_pos = 0, max_n = 0;
   size_t max_blocks = 1;
+  for (int i = 0; i < nseq; ++i) max_n = std::max(max_n, n[i]);
   for (int i = 0; i < nseq; ++i) {
     max_pos = std::max(max_pos, sess[i]->len + n[i] - 1);
     max_blocks = std::max(max_blocks, sess[i]->blocks.size());
@@ -547,7 +548,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       const int ldp = (int)w.lda;
       if (!conv_done)
         conv_step(P, ldp, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb, (size_t)L.lin_index * per_lin,
-                  sm, nseq, st);
+                  sm, nseq, max_n, st);
       GdnParams gp{};
       gp.k_heads = c.k_heads;
       gp.v_heads = c.v_heads;
@@ -569,7 +570,11 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       gp.act = a8_act_dst(act);
       gp.state_base = d_sb;
       gp.state_off = (size_t)L.lin_index * per_lin + m.conv_floats;
-      gdn_step(gp, sm, nseq, st);
+      if (max_n >= kGdnLongRows) {
+        gp.seq_of_row = d_seq;
+        gp.o_raw = static_cast<float*>(gemv::gemv_scratch(st, (size_t)rows * m.value_dim * sizeof(float), 7));
+      }
+      gdn_step(gp, sm, nseq, rows, max_n, st);
       // the residual GEMV also writes the post-mixer norm's input (act3)
       post_in = qmat_gemv_a8_res_norm(L.out, act, w.x, H, L.post_norm, eps, w.act3, st);
     } else {

@@ -30,8 +30,10 @@ struct SeqMeta {
 // Depthwise causal conv decode step + SiLU with state shift
 // (qwen3_5.rs:1800-1853, kernel k, state [channels, k-1] per sequence).
 // x/out [rows, channels]; state_base[s] + state_off is the sequence's state.
+// max_rows bounds every sequence's row count (0: one segment per sequence,
+// which is right for any row count).
 void conv_step(const float* x, int ldx, float* out, int ldo, int channels, int kernel, const float* weight,
-               float* const* state_base, size_t state_off, SeqMeta meta, int nseq, hipStream_t s);
+               float* const* state_base, size_t state_off, SeqMeta meta, int nseq, int max_rows, hipStream_t s);
 
 struct GdnParams {
   int k_heads, v_heads, k_dim, v_dim;
@@ -50,13 +52,24 @@ struct GdnParams {
   a8act::Dst act;        // the same output as prepared A8 activations (XA null: no)
   float* const* state_base;  // per sequence; state at state_base[s] + state_off, [v_heads, k_dim, v_dim]
   size_t state_off;
+  // prefill form (both null: every sequence takes the step kernel): row ->
+  // sequence, and room for the recurrence outputs before their gated norm
+  // [rows, v_heads * v_dim]
+  const int* seq_of_row;
+  float* o_raw;
 };
 
 // Gated-DeltaNet recurrence over each sequence's rows in order
 // (qwen3_5.rs:1330-1383; Metal gated_delta_step, qwen3_fuse.rs:176-279).
 // k_dim == v_dim == 128. The fp32 state of a (sequence, head) is read once
 // into registers, stepped through all its rows, and written once.
-void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, hipStream_t s);
+// Sequences of at least kGdnLongRows rows (max_rows: the step's largest row
+// count; seq_of_row and o_raw set) take the chunkwise form instead: chunks of
+// kGdnChunk tokens, each a triangular solve and small matrix products against
+// the chunk's starting state, then a row-parallel gated norm.
+constexpr int kGdnLongRows = 32;
+constexpr int kGdnChunk = 32;
+void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, int rows, int max_rows, hipStream_t s);
 
 struct AttnLayout {
   int heads, kv_heads, head_dim, rotary_dim;

@@ -72,6 +72,13 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 // causal conv step (sequential over a sequence's rows)
 // ---------------------------------------------------------------------------
+// The output of row t reads inputs t-k+1..t only (earlier rows' inputs come
+// from the state), so a sequence is cut into segments of kConvSeg rows along
+// grid z; each thread runs one channel through one segment. Segment 0 alone
+// reads the old state and alone writes the new one (the last k-1 inputs of
+// old state ++ x), so no segment reads a state another has rewritten.
+constexpr int kConvSeg = 64;
+
 __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict__ x, int ldx, float* __restrict__ out,
                                                         int ldo, int channels, int kernel,
                                                         const float* __restrict__ weight, float* const* state_base,
@@ -79,23 +86,33 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
   const int c = blockIdx.x * 256 + threadIdx.x;
   const int s = blockIdx.y;
   if (c >= channels) return;
+  const int r0 = row_start[s], n = row_count[s];
+  const int t_beg = blockIdx.z * kConvSeg;
+  if (t_beg >= n && (blockIdx.z > 0 || n > 0)) return;
+  const int t_end = gridDim.z == 1 ? n : min(n, t_beg + kConvSeg);
   const int hist = kernel - 1;
   float* st = state_base[s] + state_off + (size_t)c * hist;
   float win[8];
   float wt[8];
-  for (int k = 0; k < hist; ++k) win[k] = st[k];
+  float old[8];
+  for (int k = 0; k < hist; ++k) {
+    // window before row t_beg: inputs t_beg-hist..t_beg-1, from the state before row 0
+    const int t = t_beg - hist + k;
+    win[k] = t < 0 ? st[hist + t] : x[(size_t)(r0 + t) * ldx + c];
+  }
+  if (blockIdx.z == 0)
+    for (int k = 0; k < hist; ++k) old[k] = win[k];
   for (int k = 0; k < kernel; ++k) wt[k] = weight[(size_t)c * kernel + k];
-  const int r0 = row_start[s], n = row_count[s];
   // inputs loaded eight rows ahead (the steps are sequential; the loads are not)
   constexpr int PF = 8;
   float xr[PF];
 #pragma unroll
-  for (int k = 0; k < PF; ++k) xr[k] = k < n ? x[(size_t)(r0 + k) * ldx + c] : 0.0f;
-  for (int t = 0; t < n; ++t) {
+  for (int k = 0; k < PF; ++k) xr[k] = t_beg + k < t_end ? x[(size_t)(r0 + t_beg + k) * ldx + c] : 0.0f;
+  for (int t = t_beg; t < t_end; ++t) {
     const float xv = xr[0];
 #pragma unroll
     for (int k = 0; k + 1 < PF; ++k) xr[k] = xr[k + 1];
-    xr[PF - 1] = t + PF < n ? x[(size_t)(r0 + t + PF) * ldx + c] : 0.0f;
+    xr[PF - 1] = t + PF < t_end ? x[(size_t)(r0 + t + PF) * ldx + c] : 0.0f;
     float acc = 0.0f;
     for (int k = 0; k < hist; ++k) acc += win[k] * wt[k];
     acc += xv * wt[hist];
@@ -103,7 +120,12 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
     for (int k = 0; k + 1 < hist; ++k) win[k] = win[k + 1];
     if (hist > 0) win[hist - 1] = xv;
   }
-  for (int k = 0; k < hist; ++k) st[k] = win[k];
+  if (blockIdx.z != 0) return;
+  for (int k = 0; k < hist; ++k) {
+    // new state: inputs n-hist..n-1 of old state ++ x
+    const int t = n - hist + k;
+    st[k] = t < 0 ? old[hist + t] : x[(size_t)(r0 + t) * ldx + c];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -143,6 +165,7 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
   const float a_log = p.a_log[h], dtb = p.dt_bias[h];
   const float qscale = sqrtf((float)D);
   const int r0 = row_start[s], n = row_count[s];
+  if (p.o_raw && n >= kGdnLongRows) return;  // gdn_chunk_kernel's
   // the gate input z and the norm weight are loaded with the step's other
   // inputs, not after the reductions that need them
   const float nw = tid < D ? p.norm[tid] : 0.0f;
@@ -250,6 +273,286 @@ __global__ __launch_bounds__(256) void gdn_kernel(GdnParams p, const int* row_st
 #pragma unroll
   for (int ii = 0; ii < 16; ++ii)
     *reinterpret_cast<float4*>(st + (size_t)(16 * rg + ii) * D + 4 * cg) = make_float4(S[ii][0], S[ii][1], S[ii][2], S[ii][3]);
+}
+
+// Prefill form of the recurrence, chunkwise (the published chunked form of
+// the gated delta rule, in exact arithmetic the same recurrence). Over a
+// chunk of m tokens from state S0, with G_t the running sum of the log decay
+// g from the chunk start, gamma_t = exp(G_t), and the sequential recurrence
+// S_t = a_t S_{t-1} + k_t d_t^T, d_t = beta_t (v_t - (a_t S_{t-1})^T k_t):
+//   d_t = U_t - sum_{i<t} L_ti d_i,  U_t = beta_t (v_t - gamma_t S0^T k_t),
+//                                    L_ti = beta_t exp(G_t - G_i) (k_t . k_i)
+//   o_t = gamma_t S0^T q_t + sum_{i<=t} exp(G_t - G_i) (q_t . k_i) d_i
+//   S_m = gamma_m S0 + sum_i exp(G_m - G_i) k_i d_i^T
+// (every decay factor exp(G_t - G_i) with t >= i is at most 1). A column of S
+// (one value dimension) evolves on its own, so a head's 128 columns are split
+// over kGdnColGroups workgroups (grid x = value head * groups + group), each
+// holding its 128 x 32 slice of S in LDS and repeating the 32 x 32 token
+// products. q and k are L2 normalized per token as in the step kernel and
+// kept transposed ([k index][token]) for float4 reads in the register-blocked
+// products. The recurrence outputs go to o_raw; gdn_norm_kernel applies the
+// gated RMSNorm.
+constexpr int kGdnColGroups = 4;
+constexpr int kGdnCols = 128 / kGdnColGroups;                  // 32 columns of S per workgroup
+constexpr int kGdnCP = kGdnCols + 4, kGdnTP = kGdnChunk + 4;  // padded LDS row strides
+constexpr size_t kGdnChunkLds =
+    (size_t)(3 * 128 * kGdnTP + 2 * kGdnChunk * kGdnCP + 2 * kGdnChunk * kGdnTP + 2 * kGdnChunk) * sizeof(float);
+
+__global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnParams p, const int* row_start, const int* row_count) {
+  constexpr int D = 128, C = kGdnChunk, NCOL = kGdnCols, CP = kGdnCP, TP = kGdnTP;
+  static_assert(C == 32 && NCOL == 32 && CP == TP, "thread mappings assume 32 tokens x 32 columns");
+  extern __shared__ __attribute__((aligned(16))) float gsm[];
+  float* S = gsm;            // [D][CP]  this group's columns of the state (k index major)
+  float* KT = S + D * CP;    // [D][TP]  normalized k, transposed
+  float* QT = KT + D * TP;   // [D][TP]  normalized, scaled q, transposed
+  float* Uc = QT + D * TP;   // [C][CP]  v, then U, then exp(G_m - G_i) d_i
+  float* Zc = Uc + C * CP;   // [C][CP]  gamma_t S0^T q_t
+  float* Lm = Zc + C * CP;   // [C][TP]
+  float* Bm = Lm + C * TP;   // [C][TP]
+  float* Gs = Bm + C * TP;   // [C] running log decay
+  float* Bs = Gs + C;        // [C] beta
+  const int h = blockIdx.x / kGdnColGroups, col0 = (blockIdx.x % kGdnColGroups) * NCOL;
+  const int s = blockIdx.y, tid = threadIdx.x;
+  const int n = row_count[s];
+  if (n < kGdnLongRows) return;
+  const int r0 = row_start[s];
+  const int repeat = p.v_heads / p.k_heads, kh = h / repeat, key_dim = p.k_heads * D;
+  const int ldo = p.v_heads * D;
+  float* st = p.state_base[s] + p.state_off + (size_t)h * D * D + col0;
+  for (int i = tid; i < D * NCOL / 4; i += 256)
+    *reinterpret_cast<float4*>(S + (i >> 3) * CP + (i & 7) * 4) =
+        *reinterpret_cast<const float4*>(st + (size_t)(i >> 3) * D + (i & 7) * 4);
+  const float a_log = p.a_log[h], dtb = p.dt_bias[h];
+  const float qscale = sqrtf((float)D);
+  const int c = tid & (NCOL - 1), tq = tid >> 5;  // column phases: column c, tokens 4 tq ..
+
+  for (int t0 = 0; t0 < n; t0 += C) {
+    const int m = min(C, n - t0);
+    __syncthreads();  // the previous chunk is done with every buffer
+    // q and k of the chunk (zeros past m): 32 lanes per token, 4 elements each
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int t = (tid >> 5) + 8 * jj, e = (tid & 31) * 4;
+      float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4;
+      if (t < m) {
+        const float* cv = p.conv_out + (size_t)(r0 + t0 + t) * p.ld_conv;
+        q4 = *reinterpret_cast<const float4*>(cv + kh * D + e);
+        k4 = *reinterpret_cast<const float4*>(cv + key_dim + kh * D + e);
+      }
+      float sq = q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w;
+      float sk = k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w;
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) {
+        sq += __shfl_xor(sq, o, 64);
+        sk += __shfl_xor(sk, o, 64);
+      }
+      const float iq = 1.0f / sqrtf(sq + 1e-6f), ik = 1.0f / sqrtf(sk + 1e-6f);
+      QT[(e + 0) * TP + t] = (q4.x * iq) / qscale;
+      QT[(e + 1) * TP + t] = (q4.y * iq) / qscale;
+      QT[(e + 2) * TP + t] = (q4.z * iq) / qscale;
+      QT[(e + 3) * TP + t] = (q4.w * iq) / qscale;
+      KT[(e + 0) * TP + t] = k4.x * ik;
+      KT[(e + 1) * TP + t] = k4.y * ik;
+      KT[(e + 2) * TP + t] = k4.z * ik;
+      KT[(e + 3) * TP + t] = k4.w * ik;
+    }
+    {
+      // v of this group's columns: token tid / 8, 4 columns
+      const int t = tid >> 3, e = (tid & 7) * 4;
+      float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t < m) v4 = *reinterpret_cast<const float4*>(p.conv_out + (size_t)(r0 + t0 + t) * p.ld_conv + 2 * key_dim +
+                                                      h * D + col0 + e);
+      *reinterpret_cast<float4*>(Uc + t * CP + e) = v4;
+    }
+    if (tid < 64) {
+      // decay and beta per token, then the running sum of the log decay
+      float g = 0.f, beta = 0.f;
+      if (tid < m) {
+        const size_t row = (size_t)(r0 + t0 + tid) * p.ld_ab + h;
+        g = -expf(a_log) * softplus_f(p.a[row] + dtb);
+        beta = 1.0f / (1.0f + expf(-p.b[row]));
+      }
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) {
+        const float y = __shfl_up(g, o, 64);
+        if ((tid & 31) >= o) g += y;
+      }
+      if (tid < C) {
+        Gs[tid] = g;
+        Bs[tid] = beta;
+      }
+    }
+    __syncthreads();
+    if (tid < 128) {
+      // L (threads 0..63) and B (64..127), 4x4 blocks of tokens t x i
+      const int which = tid >> 6, b = tid & 63, tb = (b >> 3) * 4, ib = (b & 7) * 4;
+      const float* X = which ? QT : KT;
+      float acc[4][4] = {};
+#pragma unroll 4
+      for (int r = 0; r < D; ++r) {
+        const float4 x4 = *reinterpret_cast<const float4*>(X + r * TP + tb);
+        const float4 y4 = *reinterpret_cast<const float4*>(KT + r * TP + ib);
+        const float xv[4] = {x4.x, x4.y, x4.z, x4.w}, yv[4] = {y4.x, y4.y, y4.z, y4.w};
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) acc[a][bb] = fmaf(xv[a], yv[bb], acc[a][bb]);
+      }
+      float* M = which ? Bm : Lm;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int t = tb + a;
+        float v4[4];
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+          const int i = ib + bb;
+          float v = 0.f;
+          if (t < m && (which ? i <= t : i < t)) {
+            const float w = expf(Gs[t] - Gs[i]);
+            v = which ? w * acc[a][bb] : Bs[t] * (w * acc[a][bb]);
+          }
+          v4[bb] = v;
+        }
+        *reinterpret_cast<float4*>(M + t * TP + ib) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+      }
+    }
+    {
+      // W = K S0 and Z = Q S0 as 2x2 blocks (tokens tw.., columns cw..); then
+      // U = beta (v - gamma W) and gamma Z
+      const int tw = (tid >> 4) * 2, cw = (tid & 15) * 2;
+      float w[2][2] = {}, z[2][2] = {};
+#pragma unroll 8
+      for (int r = 0; r < D; ++r) {
+        const float2 k2 = *reinterpret_cast<const float2*>(KT + r * TP + tw);
+        const float2 q2 = *reinterpret_cast<const float2*>(QT + r * TP + tw);
+        const float2 s2 = *reinterpret_cast<const float2*>(S + r * CP + cw);
+        w[0][0] = fmaf(k2.x, s2.x, w[0][0]);
+        w[0][1] = fmaf(k2.x, s2.y, w[0][1]);
+        w[1][0] = fmaf(k2.y, s2.x, w[1][0]);
+        w[1][1] = fmaf(k2.y, s2.y, w[1][1]);
+        z[0][0] = fmaf(q2.x, s2.x, z[0][0]);
+        z[0][1] = fmaf(q2.x, s2.y, z[0][1]);
+        z[1][0] = fmaf(q2.y, s2.x, z[1][0]);
+        z[1][1] = fmaf(q2.y, s2.y, z[1][1]);
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int t = tw + a;
+        const float gam = expf(Gs[t]), bet = Bs[t];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+          const int cc = cw + bb;
+          Uc[t * CP + cc] = bet * (Uc[t * CP + cc] - gam * w[a][bb]);
+          Zc[t * CP + cc] = gam * z[a][bb];
+        }
+      }
+    }
+    __syncthreads();
+    // d = (I + L)^-1 U for column c, in registers (every thread of the column
+    // solves it; L is zero on and above the diagonal and past the chunk)
+    float d[C];
+#pragma unroll
+    for (int t = 0; t < C; ++t) d[t] = Uc[t * CP + c];
+#pragma unroll
+    for (int t = 1; t < C; ++t) {
+      float acc = d[t];
+#pragma unroll
+      for (int i = 0; i < t; ++i) acc = fmaf(-Lm[t * TP + i], d[i], acc);
+      d[t] = acc;
+    }
+    // outputs of tokens 4 tq .. for column c: B is zero above the diagonal
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 4 * tq + j;
+      float o = Zc[t * CP + c];
+#pragma unroll
+      for (int i4 = 0; i4 < C; i4 += 4) {
+        const float4 b4 = *reinterpret_cast<const float4*>(Bm + t * TP + i4);
+        o = fmaf(b4.x, d[i4], o);
+        o = fmaf(b4.y, d[i4 + 1], o);
+        o = fmaf(b4.z, d[i4 + 2], o);
+        o = fmaf(b4.w, d[i4 + 3], o);
+      }
+      if (t < m) p.o_raw[(size_t)(r0 + t0 + t) * ldo + h * D + col0 + c] = o;
+    }
+    const float gl = Gs[m - 1];
+#pragma unroll
+    for (int i = 0; i < C; ++i) d[i] = i < m ? expf(gl - Gs[i]) * d[i] : 0.f;
+    __syncthreads();  // every column's U is read
+    if (tq == 0) {
+#pragma unroll
+      for (int i = 0; i < C; ++i) Uc[i * CP + c] = d[i];
+    }
+    __syncthreads();
+    {
+      // S = gamma_m S0 + K^T (weighted d) as 4x4 blocks (rows rb.., columns cb..)
+      const int rb = (tid >> 3) * 4, cb = (tid & 7) * 4;
+      const float gm = expf(gl);
+      float acc[4][4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const float4 s4 = *reinterpret_cast<const float4*>(S + (rb + a) * CP + cb);
+        acc[a][0] = gm * s4.x;
+        acc[a][1] = gm * s4.y;
+        acc[a][2] = gm * s4.z;
+        acc[a][3] = gm * s4.w;
+      }
+#pragma unroll 2
+      for (int i = 0; i < C; i += 4) {
+        float kk[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const float4 k4 = *reinterpret_cast<const float4*>(KT + (rb + a) * TP + i);
+          kk[a][0] = k4.x;
+          kk[a][1] = k4.y;
+          kk[a][2] = k4.z;
+          kk[a][3] = k4.w;
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const float4 d4 = *reinterpret_cast<const float4*>(Uc + (i + ii) * CP + cb);
+          const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) acc[a][bb] = fmaf(kk[a][ii], dv[bb], acc[a][bb]);
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<float4*>(S + (rb + a) * CP + cb) = make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < D * NCOL / 4; i += 256)
+    *reinterpret_cast<float4*>(st + (size_t)(i >> 3) * D + (i & 7) * 4) =
+        *reinterpret_cast<const float4*>(S + (i >> 3) * CP + (i & 7) * 4);
+}
+
+// Gated RMSNorm of the chunkwise outputs (rows of long sequences only),
+// exactly the step kernel's tail: out and / or the prepared activations.
+__global__ __launch_bounds__(128) void gdn_norm_kernel(GdnParams p, const int* row_count) {
+  constexpr int D = 128;
+  __shared__ float part[2];
+  __shared__ float obuf[D];
+  const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  if (row_count[p.seq_of_row[row]] < kGdnLongRows) return;
+  const float o = p.o_raw[(size_t)row * p.v_heads * D + h * D + tid];
+  const float zg = p.z[(size_t)row * p.ld_z + h * D + tid];
+  const float oss = wave_sum(o * o);
+  if ((tid & 63) == 0) part[tid >> 6] = oss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((part[0] + part[1]) / (float)D + 1e-6f);
+  const float val = o * inv * p.norm[tid] * (zg / (1.0f + expf(-zg)));
+  if (p.out) p.out[(size_t)row * p.ld_out + h * D + tid] = val;
+  obuf[tid] = val;
+  __syncthreads();
+  if (p.act.XA && tid < D / 16) {
+    float v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = obuf[16 * tid + e];
+    a8act::emit_slice(p.act, row, (h * D + 16 * tid) >> 6, tid & 3, v, true);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -422,19 +725,37 @@ void rmsnorm_rows(const float* x, int ldx, const int* rows_idx, int rows, int n,
 }
 
 void conv_step(const float* x, int ldx, float* out, int ldo, int channels, int kernel, const float* weight,
-               float* const* state_base, size_t state_off, SeqMeta meta, int nseq, hipStream_t s) {
+               float* const* state_base, size_t state_off, SeqMeta meta, int nseq, int max_rows, hipStream_t s) {
   PGD_CHECK(kernel >= 1 && kernel <= 8, kErrShape, "conv kernel must be in 1..8");
   if (nseq <= 0) return;
-  hipLaunchKernelGGL(conv_step_kernel, dim3((channels + 255) / 256, nseq), dim3(256), 0, s, x, ldx, out, ldo, channels,
+  const int segs = max_rows > kConvSeg ? (max_rows + kConvSeg - 1) / kConvSeg : 1;
+  hipLaunchKernelGGL(conv_step_kernel, dim3((channels + 255) / 256, nseq, segs), dim3(256), 0, s, x, ldx, out, ldo, channels,
                      kernel, weight, state_base, state_off, meta.row_start, meta.row_count);
   PGD_HIP(hipGetLastError());
 }
 
-void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, hipStream_t s) {
+void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, int rows, int max_rows, hipStream_t s) {
   PGD_CHECK(p.k_dim == 128 && p.v_dim == 128, kErrShape, "gated delta kernel needs k_dim == v_dim == 128");
   PGD_CHECK(p.k_heads > 0 && p.v_heads % p.k_heads == 0, kErrShape, "v_heads must be a multiple of k_heads");
   if (nseq <= 0) return;
-  hipLaunchKernelGGL(gdn_kernel, dim3(p.v_heads, nseq), dim3(256), 0, s, p, meta.row_start, meta.row_count);
+  const bool chunked = p.o_raw && p.seq_of_row && max_rows >= kGdnLongRows;
+  GdnParams q = p;
+  if (!chunked) q.o_raw = nullptr;
+  hipLaunchKernelGGL(gdn_kernel, dim3(p.v_heads, nseq), dim3(256), 0, s, q, meta.row_start, meta.row_count);
+  PGD_HIP(hipGetLastError());
+  if (!chunked) return;
+  PGD_CHECK(p.ld_conv % 4 == 0, kErrShape, "chunked gated delta kernel needs 16-byte aligned conv rows");
+  constexpr size_t lds = kGdnChunkLds;
+  static bool attr = false;
+  if (!attr) {
+    PGD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gdn_chunk_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    attr = true;
+  }
+  hipLaunchKernelGGL(gdn_chunk_kernel, dim3(p.v_heads * kGdnColGroups, nseq), dim3(256), lds, s, p, meta.row_start,
+                     meta.row_count);
+  PGD_HIP(hipGetLastError());
+  hipLaunchKernelGGL(gdn_norm_kernel, dim3(p.v_heads, rows), dim3(128), 0, s, p, meta.row_count);
   PGD_HIP(hipGetLastError());
 }
 

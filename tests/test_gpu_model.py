@@ -369,3 +369,18 @@ def test_long_and_short_prefill_in_one_step(m35):
         logits = [g]
     a.free()
     b.free()
+
+
+def test_continued_long_prefill(m35):
+    """A 100-token prefill continued by a 90-token one and a 33-token one, so
+    the long-row conv segments and the chunkwise recurrence start from a
+    state that earlier steps wrote, against the oracle fed the same pieces."""
+    model, oracle = m35
+    rng = np.random.default_rng(78)
+    a = model.new_session()
+    oa = oracle.new_cache()
+    for n in (100, 90, 33):
+        toks = rng.integers(0, model.cfg.vocab, n)
+        g, r = a.forward(toks), oracle.forward(toks, oa)
+        assert rel(g, r) < LOGIT_TOL, n
+    a.free()
