@@ -147,6 +147,19 @@ int pgd_gdn_step_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_o
                      const float* b, const float* z, const float* a_log, const float* dt_bias,
                      const float* norm, float* const* states, const int* row_start, const int* row_count,
                      int nseq, float* out);
+/* pgd_gdn_step_dev for prefill: the same recurrence, where sequences of at
+ * least 32 rows take the chunkwise form (32-token chunks: a triangular solve
+ * and matrix products against each chunk's starting state, the published
+ * chunked form of the gated delta rule; equal to the per-token loop in exact
+ * arithmetic, to fp32 rounding in practice). rows: every sequence's
+ * row_start + row_count is at most rows. max_rows: the largest row_count, or
+ * any bound on it (below 32 every sequence takes the per-token kernel).
+ * Replaces the same reference loop as pgd_gdn_step_dev, which it runs one
+ * token at a time for prefill too (qwen3_5.rs:1330-1383). */
+int pgd_gdn_prefill_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_out, const float* a,
+                        const float* b, const float* z, const float* a_log, const float* dt_bias,
+                        const float* norm, float* const* states, const int* row_start, const int* row_count,
+                        int nseq, int rows, int max_rows, float* out);
 /* Paged GQA decode attention: row r attends to positions [0, pos_of_row[r]]
  * of sequence seq_of_row[r], whose pages are block_tables[seq * max_blocks
  * + p / block] in pools [pages][kv_heads][block][head_dim]. q, gate, out

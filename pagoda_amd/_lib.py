@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_matrix_gemv_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int]),
     "pgd_matrix_gemv_swiglu_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_int]),
     "pgd_gdn_step_dev": (c_int, [c_void_p, c_int, c_int] + [c_void_p] * 10 + [c_int, c_void_p]),
+    "pgd_gdn_prefill_dev": (c_int, [c_void_p, c_int, c_int] + [c_void_p] * 10 + [c_int, c_int, c_int, c_void_p]),
     "pgd_attn_decode_dev": (c_int, [c_void_p, c_int, c_int, c_int, c_int] + [c_void_p] * 7 + [c_int, c_int, c_void_p]),
     "pgd_act_bytes": (c_size_t, [c_int, c_int]),
     "pgd_act_prep_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),

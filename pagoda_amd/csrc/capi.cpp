@@ -292,13 +292,14 @@ int pgd_matrix_gemv_swiglu_dev(const pgd_matrix* gate, const pgd_matrix* up, con
   });
 }
 
-int pgd_gdn_step_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_out, const float* a, const float* b,
-                     const float* z, const float* a_log, const float* dt_bias, const float* norm, float* const* states,
-                     const int* row_start, const int* row_count, int nseq, float* out) {
+namespace {
+int gdn_call(pgd_dev* dev, int k_heads, int v_heads, const float* conv_out, const float* a, const float* b,
+             const float* z, const float* a_log, const float* dt_bias, const float* norm, float* const* states,
+             const int* row_start, const int* row_count, int nseq, int rows, int max_rows, float* out) {
   return guard([&] {
     PGD_CHECK(dev && conv_out && a && b && z && a_log && dt_bias && norm && states && row_start && row_count && out,
               kErrArg, "null argument");
-    PGD_CHECK(nseq >= 0, kErrArg, "nseq");
+    PGD_CHECK(nseq >= 0 && rows >= 0 && max_rows >= 0, kErrArg, "nseq, rows, max_rows");
     DeviceScope scope(dev);
     GdnParams p{};
     p.k_heads = k_heads;
@@ -319,8 +320,24 @@ int pgd_gdn_step_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_o
     p.ld_out = v_heads * 128;
     p.state_base = states;
     p.state_off = 0;
-    gdn_step(p, SeqMeta{row_start, row_count}, nseq, 0, 0, dev->stream);
+    gdn_step(p, SeqMeta{row_start, row_count}, nseq, rows, max_rows, dev->stream);
   });
+}
+}  // namespace
+
+int pgd_gdn_step_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_out, const float* a, const float* b,
+                     const float* z, const float* a_log, const float* dt_bias, const float* norm, float* const* states,
+                     const int* row_start, const int* row_count, int nseq, float* out) {
+  return gdn_call(dev, k_heads, v_heads, conv_out, a, b, z, a_log, dt_bias, norm, states, row_start, row_count, nseq,
+                  0, 0, out);
+}
+
+int pgd_gdn_prefill_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_out, const float* a,
+                        const float* b, const float* z, const float* a_log, const float* dt_bias, const float* norm,
+                        float* const* states, const int* row_start, const int* row_count, int nseq, int rows,
+                        int max_rows, float* out) {
+  return gdn_call(dev, k_heads, v_heads, conv_out, a, b, z, a_log, dt_bias, norm, states, row_start, row_count, nseq,
+                  rows, max_rows, out);
 }
 
 int pgd_attn_decode_dev(pgd_dev* dev, int heads, int kv_heads, int head_dim, int block, const float* q,

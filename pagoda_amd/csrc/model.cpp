@@ -570,10 +570,6 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       gp.act = a8_act_dst(act);
       gp.state_base = d_sb;
       gp.state_off = (size_t)L.lin_index * per_lin + m.conv_floats;
-      if (max_n >= kGdnLongRows) {
-        gp.seq_of_row = d_seq;
-        gp.o_raw = static_cast<float*>(gemv::gemv_scratch(st, (size_t)rows * m.value_dim * sizeof(float), 7));
-      }
       gdn_step(gp, sm, nseq, rows, max_n, st);
       // the residual GEMV also writes the post-mixer norm's input (act3)
       post_in = qmat_gemv_a8_res_norm(L.out, act, w.x, H, L.post_norm, eps, w.act3, st);

@@ -52,10 +52,8 @@ struct GdnParams {
   a8act::Dst act;        // the same output as prepared A8 activations (XA null: no)
   float* const* state_base;  // per sequence; state at state_base[s] + state_off, [v_heads, k_dim, v_dim]
   size_t state_off;
-  // prefill form (both null: every sequence takes the step kernel): row ->
-  // sequence, and room for the recurrence outputs before their gated norm
-  // [rows, v_heads * v_dim]
-  const int* seq_of_row;
+  // set by gdn_step, not by callers: the recurrence outputs of the chunkwise
+  // form before their gated norm, [rows, v_heads * v_dim] (null: step kernel only)
   float* o_raw;
 };
 
@@ -63,10 +61,12 @@ struct GdnParams {
 // (qwen3_5.rs:1330-1383; Metal gated_delta_step, qwen3_fuse.rs:176-279).
 // k_dim == v_dim == 128. The fp32 state of a (sequence, head) is read once
 // into registers, stepped through all its rows, and written once.
-// Sequences of at least kGdnLongRows rows (max_rows: the step's largest row
-// count; seq_of_row and o_raw set) take the chunkwise form instead: chunks of
-// kGdnChunk tokens, each a triangular solve and small matrix products against
-// the chunk's starting state, then a row-parallel gated norm.
+// When max_rows >= kGdnLongRows, sequences of at least kGdnLongRows rows take
+// the chunkwise form instead: chunks of kGdnChunk tokens, each a triangular
+// solve and small matrix products against the chunk's starting state, then a
+// row-parallel gated norm. rows bounds row_start + row_count of every
+// sequence (it sizes the outputs' staging); max_rows only selects whether the
+// chunkwise kernels run, so any value gives correct results.
 constexpr int kGdnLongRows = 32;
 constexpr int kGdnChunk = 32;
 void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, int rows, int max_rows, hipStream_t s);

@@ -531,12 +531,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnParams p, const int* 
 
 // Gated RMSNorm of the chunkwise outputs (rows of long sequences only),
 // exactly the step kernel's tail: out and / or the prepared activations.
-__global__ __launch_bounds__(128) void gdn_norm_kernel(GdnParams p, const int* row_count) {
+__device__ inline void gdn_norm_row(const GdnParams& p, int row, int h, int tid, float* part, float* obuf) {
   constexpr int D = 128;
-  __shared__ float part[2];
-  __shared__ float obuf[D];
-  const int h = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
-  if (row_count[p.seq_of_row[row]] < kGdnLongRows) return;
   const float o = p.o_raw[(size_t)row * p.v_heads * D + h * D + tid];
   const float zg = p.z[(size_t)row * p.ld_z + h * D + tid];
   const float oss = wave_sum(o * o);
@@ -552,6 +548,20 @@ __global__ __launch_bounds__(128) void gdn_norm_kernel(GdnParams p, const int* r
 #pragma unroll
     for (int e = 0; e < 16; ++e) v[e] = obuf[16 * tid + e];
     a8act::emit_slice(p.act, row, (h * D + 16 * tid) >> 6, tid & 3, v, true);
+  }
+}
+
+// grid (row blocks, sequence, value head); a workgroup strides over its
+// sequence's rows
+__global__ __launch_bounds__(128) void gdn_norm_kernel(GdnParams p, const int* row_start, const int* row_count) {
+  __shared__ float part[2];
+  __shared__ float obuf[128];
+  const int s = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
+  const int n = row_count[s];
+  if (n < kGdnLongRows) return;
+  for (int t = blockIdx.x; t < n; t += gridDim.x) {
+    __syncthreads();  // part and obuf of the previous row are consumed
+    gdn_norm_row(p, row_start[s] + t, h, tid, part, obuf);
   }
 }
 
@@ -738,9 +748,10 @@ void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, int rows, int max_rows
   PGD_CHECK(p.k_dim == 128 && p.v_dim == 128, kErrShape, "gated delta kernel needs k_dim == v_dim == 128");
   PGD_CHECK(p.k_heads > 0 && p.v_heads % p.k_heads == 0, kErrShape, "v_heads must be a multiple of k_heads");
   if (nseq <= 0) return;
-  const bool chunked = p.o_raw && p.seq_of_row && max_rows >= kGdnLongRows;
+  const bool chunked = rows > 0 && max_rows >= kGdnLongRows;
   GdnParams q = p;
-  if (!chunked) q.o_raw = nullptr;
+  q.o_raw = chunked ? static_cast<float*>(gemv::gemv_scratch(s, (size_t)rows * p.v_heads * 128 * sizeof(float), 7))
+                    : nullptr;
   hipLaunchKernelGGL(gdn_kernel, dim3(p.v_heads, nseq), dim3(256), 0, s, q, meta.row_start, meta.row_count);
   PGD_HIP(hipGetLastError());
   if (!chunked) return;
@@ -752,10 +763,11 @@ void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, int rows, int max_rows
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr = true;
   }
-  hipLaunchKernelGGL(gdn_chunk_kernel, dim3(p.v_heads * kGdnColGroups, nseq), dim3(256), lds, s, p, meta.row_start,
+  hipLaunchKernelGGL(gdn_chunk_kernel, dim3(p.v_heads * kGdnColGroups, nseq), dim3(256), lds, s, q, meta.row_start,
                      meta.row_count);
   PGD_HIP(hipGetLastError());
-  hipLaunchKernelGGL(gdn_norm_kernel, dim3(p.v_heads, rows), dim3(128), 0, s, p, meta.row_count);
+  hipLaunchKernelGGL(gdn_norm_kernel, dim3(std::min(max_rows, 4096), nseq, p.v_heads), dim3(128), 0, s, q,
+                     meta.row_start, meta.row_count);
   PGD_HIP(hipGetLastError());
 }
 

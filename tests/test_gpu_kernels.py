@@ -33,7 +33,7 @@ def gdn_inputs(rng, rows, kh=16, vh=32, d=128):
     return conv, a, b, z, a_log, dtb, norm
 
 
-def run_gdn(dev, counts, inputs, states, kh=16, vh=32):
+def run_gdn(dev, counts, inputs, states, kh=16, vh=32, prefill=False):
     from pagoda_amd._lib import call
     import ctypes as C
 
@@ -49,8 +49,12 @@ def run_gdn(dev, counts, inputs, states, kh=16, vh=32):
     d_rs = dev.upload(starts)
     d_rc = dev.upload(np.asarray(counts, np.int32))
     d_out = dev.alloc(rows * vh * 128 * 4)
-    call("pgd_gdn_step_dev", dev.handle, kh, vh, *[C.c_void_p(p) for p in d_in], C.c_void_p(d_ptrs),
-         C.c_void_p(d_rs), C.c_void_p(d_rc), nseq, C.c_void_p(d_out))
+    args = [dev.handle, kh, vh, *[C.c_void_p(p) for p in d_in], C.c_void_p(d_ptrs), C.c_void_p(d_rs),
+            C.c_void_p(d_rc), nseq]
+    if prefill:
+        call("pgd_gdn_prefill_dev", *args, rows, int(max(counts)), C.c_void_p(d_out))
+    else:
+        call("pgd_gdn_step_dev", *args, C.c_void_p(d_out))
     out = dev.download(d_out, (rows, vh * 128), np.float32)
     new_states = dev.download(sbuf, states.shape, np.float32)
     for p in d_in + [sbuf, d_ptrs, d_rs, d_rc, d_out]:
@@ -115,6 +119,50 @@ def test_gdn_ragged_mix(dev):
         ref = ora.gdn_step(conv[sl], a[sl], b[sl], z[sl], a_log, dtb, norm, 16, 32, 128, 128, st)
         assert rel(out[sl], ref) < TOL and rel(new_states[s], st) < TOL
         r += n
+
+
+def test_gdn_prefill_chunkwise(dev):
+    """The prefill entry point over a ragged batch whose long sequences (at
+    least 32 rows: whole chunks, a ragged last chunk, exactly one chunk) take
+    the chunkwise form and whose short ones take the per-token kernel, from
+    nonzero states, against the oracle's per-token recurrence. The chunkwise
+    sums round differently from the per-token ones, so the bar is TOL as for
+    the step kernel, on the outputs and on the final states."""
+    rng = np.random.default_rng(31)
+    counts = [300, 7, 33, 32, 31, 64, 1]
+    inputs = gdn_inputs(rng, sum(counts))
+    states = (rng.normal(0, 1, (len(counts), 32, 128, 128)) * 0.1).astype(np.float32)
+    out, new_states = run_gdn(dev, counts, inputs, states, prefill=True)
+    out_step, states_step = run_gdn(dev, counts, inputs, states)
+    conv, a, b, z, a_log, dtb, norm = inputs
+    r = 0
+    for s, n in enumerate(counts):
+        st = states[s].copy()
+        sl = slice(r, r + n)
+        ref = ora.gdn_step(conv[sl], a[sl], b[sl], z[sl], a_log, dtb, norm, 16, 32, 128, 128, st)
+        assert rel(out[sl], ref) < TOL, n
+        assert rel(new_states[s], st) < TOL, n
+        if n < 32:  # short sequences run the per-token kernel either way
+            np.testing.assert_array_equal(out[sl].view(np.uint32), out_step[sl].view(np.uint32))
+            np.testing.assert_array_equal(new_states[s].view(np.uint32), states_step[s].view(np.uint32))
+        r += n
+
+
+def test_gdn_prefill_slow_decay_long(dev):
+    """Decay close to 1 (A_log = -8, so a chunk barely forgets) over 200 rows:
+    the chunkwise products carry the whole chunk's state instead of rounding
+    away old terms."""
+    rng = np.random.default_rng(32)
+    counts = [200]
+    conv, a, b, z, a_log, dtb, norm = gdn_inputs(rng, 200)
+    a_log = np.full_like(a_log, -8.0)
+    inputs = (conv, a, b, z, a_log, dtb, norm)
+    states = (rng.normal(0, 1, (1, 32, 128, 128)) * 0.1).astype(np.float32)
+    out, new_states = run_gdn(dev, counts, inputs, states, prefill=True)
+    st = states[0].copy()
+    ref = ora.gdn_step(conv, a, b, z, a_log, dtb, norm, 16, 32, 128, 128, st)
+    assert rel(out, ref) < TOL
+    assert rel(new_states[0], st) < TOL
 
 
 @pytest.mark.parametrize("poison", [False, True])
