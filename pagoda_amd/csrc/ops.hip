@@ -100,7 +100,8 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
     const int t = t_beg - hist + k;
     win[k] = t < 0 ? st[hist + t] : x[(size_t)(r0 + t) * ldx + c];
   }
-  if (blockIdx.z == 0)
+  const bool whole = gridDim.z == 1;  // this thread runs every row: the last window is the new state
+  if (!whole)
     for (int k = 0; k < hist; ++k) old[k] = win[k];
   for (int k = 0; k < kernel; ++k) wt[k] = weight[(size_t)c * kernel + k];
   // inputs loaded eight rows ahead (the steps are sequential; the loads are not)
@@ -119,6 +120,10 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
     out[(size_t)(r0 + t) * ldo + c] = acc / (1.0f + expf(-acc));
     for (int k = 0; k + 1 < hist; ++k) win[k] = win[k + 1];
     if (hist > 0) win[hist - 1] = xv;
+  }
+  if (whole) {
+    for (int k = 0; k < hist; ++k) st[k] = win[k];
+    return;
   }
   if (blockIdx.z != 0) return;
   for (int k = 0; k < hist; ++k) {
