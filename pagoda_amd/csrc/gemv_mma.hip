@@ -761,12 +761,17 @@ __global__ __launch_bounds__(64 * T) void a8_mma_shared_kernel(GemvArgs a, const
   }
 }
 
+// Reduction workgroups are one wave, so a 32-row reduction of a 5120-wide
+// matrix spreads over 320 workgroups instead of 96 (measured 5.4 -> 5.2 us;
+// the kernel is bound by one load round trip plus launch).
+constexpr int kRedT = 64;
+
 // y[b][n] = (res[b][n] +) sum over ranges, in range order; each thread sums 4
 // consecutive outputs of one row with all KS loads issued before the adds
 template <int KS, int EPI>
-__global__ __launch_bounds__(256) void a8_reduce_kernel(GemvArgs a, int nb, const float* __restrict__ part) {
+__global__ __launch_bounds__(kRedT) void a8_reduce_kernel(GemvArgs a, int nb, const float* __restrict__ part) {
   const int n4 = a.n_out >> 2;
-  const int b = blockIdx.y, i4 = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y, i4 = blockIdx.x * kRedT + threadIdx.x;
   // deferred RMSNorm of the input (whole waves, before any lane leaves)
   const float inv = a.rss ? rss_inv(a.rss + (size_t)b * a.rss_nh, a.rss_nh, a.rss_n, a.rss_eps) : 1.0f;
   if (i4 >= n4) return;
@@ -809,9 +814,9 @@ __global__ __launch_bounds__(256) void a8_reduce_kernel(GemvArgs a, int nb, cons
 // 16-wide slice s. Slice sums run in k order: the first half's lane starts
 // them, the second continues from its partner's totals.
 template <int KS>
-__global__ __launch_bounds__(256) void a8_reduce_emit_kernel(GemvArgs a, int nb, const float* __restrict__ part) {
+__global__ __launch_bounds__(kRedT) void a8_reduce_emit_kernel(GemvArgs a, int nb, const float* __restrict__ part) {
   const int n8 = a.n_out >> 3;
-  const int b = blockIdx.y, i8 = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y, i8 = blockIdx.x * kRedT + threadIdx.x;
   const bool live = i8 < n8;  // every lane stays for the shuffles
   const int n = (live ? i8 : 0) * 8;
   const size_t plane = (size_t)nb * a.n_out, e = (size_t)b * a.n_out + n;
@@ -902,11 +907,12 @@ void launch_shared(const GemvArgs& a, const uint4* XA, const float* CA, int nb, 
                      XA, CA, nb, part);
   if (EPI == EPI_RES && a.nact.XA) {
     const int n8 = a.n_out / 8;
-    hipLaunchKernelGGL((a8_reduce_emit_kernel<KS>), dim3((n8 + 255) / 256, nb), dim3(256), 0, s, a, nb, part);
+    hipLaunchKernelGGL((a8_reduce_emit_kernel<KS>), dim3((n8 + kRedT - 1) / kRedT, nb), dim3(kRedT), 0, s, a, nb,
+                       part);
     return;
   }
   const int n4 = a.n_out / 4;
-  hipLaunchKernelGGL((a8_reduce_kernel<KS, EPI>), dim3((n4 + 255) / 256, nb), dim3(256), 0, s, a, nb, part);
+  hipLaunchKernelGGL((a8_reduce_kernel<KS, EPI>), dim3((n4 + kRedT - 1) / kRedT, nb), dim3(kRedT), 0, s, a, nb, part);
 }
 
 // one launch per chunk of up to 32 rows; the mode stages only the rows present
