@@ -615,6 +615,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "dtype_note": ("fp32 accumulation and fp32 state/KV; A8 weight codes and activations enter the matrix "
+                       "cores as f16 (activations as an f16 hi + lo pair, ~22 bits of the f32 value)"),
         "data": "synthetic (seeded random-init weights, random 19-token prompts)",
         "config": {"workload": "config4: 27B-class hybrid (64 layers, 3:1 GDN:attention), MLX affine-8, "
                                "greedy decode", "batch": args.batch, "prompt_len": 19,
