@@ -1040,6 +1040,11 @@ void launch_prepped(GemvArgs a, const A8Act& act, hipStream_t s) {
       nb = rows < 64 ? rows : 64;
       launch_pair<EPI>(a, xa, ca, nb, s);
       c += 2;
+    } else if (sk && rows > 36) {
+      // two chunks through one stream-K launch (weights streamed once)
+      nb = rows < 64 ? rows : 64;
+      run_a8_sk_chunk(a, xa, ca, nb, EPI, s);
+      c += 2;
     } else {
       nb = rows < 32 ? rows : 32;
       if (sk && nb >= 5) run_a8_sk_chunk(a, xa, ca, nb, EPI, s);
@@ -1076,6 +1081,12 @@ size_t a8_scratch_need(const GemvArgs& a, int rows, int epi) {
     if (pairs && rows > 36) {
       nb = rows < 64 ? rows : 64;
       need(1, (size_t)KS * nb * a.n_out * sizeof(float));
+    } else if (sk && rows > 36) {
+      nb = rows < 64 ? rows : 64;
+      size_t s3 = 0, s5 = 0;
+      sk_scratch_need(a, nb, epi, &s3, &s5);
+      need(3, s3);
+      need(5, s5);
     } else {
       nb = rows < 32 ? rows : 32;
       if (sk && nb >= 5) {

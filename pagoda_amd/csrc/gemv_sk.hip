@@ -75,7 +75,9 @@ __device__ inline long long run_start(long long U, int nwg, int i) { return (lon
 // run holding unit x
 __device__ inline int run_of(long long U, int nwg, long long x) { return (int)(((x + 1) * nwg - 1) / U); }
 
-// MODE 1: <= 16 rows (one batch tile), MODE 2: <= 32 rows (two)
+// MODE 1: <= 16 rows (one batch tile), MODE 2: <= 32 rows (two), MODE 4:
+// 37..64 rows as two 32-row activation chunks in one launch (four batch
+// tiles), so the weights stream once for both
 template <int MODE, bool DUAL>
 struct Geo {
   // four 16-row weight subtiles per wave: SwiGLU gate halves 0-1 and up halves
@@ -84,19 +86,22 @@ struct Geo {
   static constexpr int NS = 4;
   static constexpr int TPW = DUAL ? 1 : 2;       // tiles per wave (per matrix)
   static constexpr int TPB = kWaves * TPW;       // tiles per block
-  static constexpr int NBT = MODE == 2 ? 2 : 1;  // 16-row batch tiles
+  static constexpr int NBT = MODE;              // 16-row batch tiles
+  static constexpr int NC = MODE == 4 ? 2 : 1;   // 32-row activation chunks
+  static constexpr int ROWS = 16 * NBT;          // batch rows per launch at most
   static constexpr int NF = NS * NBT;            // f4 accumulators per lane
   static constexpr int XU4 = NBT * 256;          // u4 of operands per group ([bt][i][lane], a8_act.h)
   // constants per group in LDS: [bt][-1024 (XSP_A + XSP_B) | XS_A + XS_B][16],
   // the half-group sums added by the thread that stages them
   static constexpr int XCF = NBT * 32;
   static constexpr int SLOT = XU4 * 16 + XCF * 4;
-  static constexpr int HB = DUAL ? kWaves * 32 * 33 * 4 : 0;  // SwiGLU transpose buffers
+  static constexpr int HBR = ROWS < 32 ? 32 : ROWS;             // rows of a wave's transpose buffer
+  static constexpr int HB = DUAL ? kWaves * HBR * 33 * 4 : 0;  // SwiGLU transpose buffers
 };
 
 // Epilogue of one 32-row tile from accumulators V, subtiles s0, s0 + 1 (SwiGLU:
 // gate 0-1, up 2-3); lane: weight row n of half h, batch rows 16 bt + 4 q + rr.
-// hb: this wave's 32 x 33 float LDS buffer (SwiGLU).
+// hb: this wave's HBR x 33 float LDS buffer (SwiGLU).
 template <int MODE, int EPI>
 __device__ __attribute__((always_inline)) inline void tile_epilogue(
     const GemvArgs& a, int nb, int tile, const f4 (&V)[4][Geo<MODE, EPI == EPI_SWIGLU>::NBT], int s0, float* hb) {
@@ -121,11 +126,14 @@ __device__ __attribute__((always_inline)) inline void tile_epilogue(
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int b = lane & 31, h = lane >> 5;
-      float v[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) v[e] = b < nb ? hb[b * 33 + 16 * h + e] : 0.0f;
-      a8act::emit_slice<32>(a.oact, a.row0 + b, tile >> 1, (tile & 1) * 2 + h, v, b < nb);
+      for (int c = 0; c < (NBT + 1) / 2; ++c) {
+        const int b = 32 * c + (lane & 31), h = lane >> 5;
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = b < nb ? hb[b * 33 + 16 * h + e] : 0.0f;
+        a8act::emit_slice<32>(a.oact, a.row0 + b, tile >> 1, (tile & 1) * 2 + h, v, b < nb);
+      }
       __builtin_amdgcn_wave_barrier();
       if (!a.y) return;
     }
@@ -193,10 +201,10 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
   const long long U = k.U;
   const long long u0 = run_start(U, k.nwg, blockIdx.x), u1 = run_start(U, k.nwg, blockIdx.x + 1);
   if (u0 >= u1) return;
-  float* hb = reinterpret_cast<float*>(smem + 2 * Gm::SLOT) + wave * 32 * 33;
+  float* hb = reinterpret_cast<float*>(smem + 2 * Gm::SLOT) + wave * Gm::HBR * 33;
   // deferred RMSNorm of the input: the rows' 1/rms, shared out over the waves;
   // workgroup 0 also leaves them for the fix-up kernel
-  __shared__ float s_inv[32];
+  __shared__ float s_inv[Gm::ROWS];
   if (a.rss) {
     for (int b = wave; b < nb; b += kWaves) {
       const float v = rss_inv(a.rss + (size_t)b * a.rss_nh, a.rss_nh, a.rss_n, a.rss_eps);
@@ -212,15 +220,17 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
   struct WR {
     u4 w[NS];
     uint32_t s[NS];
-    u4 x;       // thread t: u4 t % XU4 of the group's operands
-    float c[2]; // thread t: the two half-group terms of constant t % XCF
+    u4 x[Gm::NC];  // thread t: u4 t % 512 of each chunk's operands of the group
+    float c[2];    // thread t: the two half-group terms of constant t % XCF
   };
   // lane's byte offset in a 2 KiB [k half][row][32 codes] block (subtile half 0)
   const uint32_t woff0 = (q >> 1) * 1024 + j * 32 + (q & 1) * 16;
   // constant t (bt = t / 32, w = t % 32): w < 16 -1024 XSP of row w (halves at
   // +0, +16 of the item's 64 floats), else XS of row w - 16 (halves at +32, +48)
-  const uint32_t ct = tid % Gm::XCF, cw = ct % 32;
-  const uint32_t xoff = (tid % Gm::XU4) * 16, coff = ((ct / 32) * 64 + (cw < 16 ? cw : cw + 16)) * 4, soff = j * 4;
+  // (MODE 4: constants 64.. are the second chunk's, G groups of 128 floats on)
+  const uint32_t ct = tid % Gm::XCF, cw = ct % 32, cbt = ct / 32;
+  const size_t coff = ((size_t)(cbt / 2) * G * 128 + (cbt % 2) * 64 + (cw < 16 ? cw : cw + 16)) * 4;
+  const uint32_t xoff = (tid % (Gm::XU4 / Gm::NC)) * 16, soff = j * 4;
   auto load_unit = [&](int b, int g, WR& r) {
 #pragma unroll
     for (int st = 0; st < NS; ++st) {
@@ -232,8 +242,11 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
       r.w[st] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(pc + woff0));
       r.s[st] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(ps + soff));
     }
-    // items 2g, 2g + 1 (both batch tiles) are contiguous: 512 u4 + 128 floats per group
-    r.x = *reinterpret_cast<const u4*>(reinterpret_cast<const uint8_t*>(XA + (size_t)g * 512) + xoff);
+    // items 2g, 2g + 1 (both batch tiles) are contiguous: 512 u4 + 128 floats per
+    // group; chunk c of a two-chunk launch starts c G groups on
+#pragma unroll
+    for (int c = 0; c < Gm::NC; ++c)
+      r.x[c] = *reinterpret_cast<const u4*>(reinterpret_cast<const uint8_t*>(XA + ((size_t)c * G + g) * 512) + xoff);
     const float* cp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(CA + (size_t)g * 128) + coff);
     r.c[0] = cp[0];
     r.c[1] = cp[16];
@@ -241,7 +254,9 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
   // operand ring: unit u in slot u & 1
   auto store_x = [&](int slot, const WR& r) {
     char* sb = smem + slot * Gm::SLOT;
-    if (tid < Gm::XU4) reinterpret_cast<u4*>(sb)[tid] = r.x;
+#pragma unroll
+    for (int c = 0; c < Gm::NC; ++c)
+      if (tid < Gm::XU4 / Gm::NC) reinterpret_cast<u4*>(sb)[c * 512 + tid] = r.x[c];
     if (tid < Gm::XCF) reinterpret_cast<float*>(sb + Gm::XU4 * 16)[tid] = r.c[0] + r.c[1];
   };
 
@@ -372,7 +387,7 @@ __global__ __launch_bounds__(64) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArg
     const int slot = r == r0 ? slot_r0 : 0;
     return k.part + ((((size_t)r * 2 + slot) * kWaves + wave) * NF + f) * 64 + lane;
   };
-  constexpr int RB = NF >= 8 ? 4 : 8;  // runs loaded together
+  constexpr int RB = NF >= 16 ? 2 : NF >= 8 ? 4 : 8;  // runs loaded together
   f4 V[NS][NBT];
   for (int r = r0; r <= r1; r += RB) {
     f4 P[RB][NS][NBT];
@@ -429,7 +444,8 @@ void launch_chunk_sk(const GemvArgs& a, const uint4* XA, const float* CA, int nb
   // units in flight per wave: as many as the registers hold (32 rows carry
   // twice the accumulators and operands)
   if (nb <= 16) return launch_sk<1, EPI, 4>(a, XA, CA, nb, s);
-  return launch_sk<2, EPI, 2>(a, XA, CA, nb, s);
+  if (nb <= 32) return launch_sk<2, EPI, 2>(a, XA, CA, nb, s);
+  return launch_sk<4, EPI, 2>(a, XA, CA, nb, s);
 }
 
 }  // namespace
@@ -442,23 +458,27 @@ bool a8_sk_wanted(const GemvArgs& a, int epi) {
 }
 
 void sk_scratch_need(const GemvArgs& a, int nb, int epi, size_t* slot3, size_t* slot5) {
-  static_assert(Geo<1, false>::NF == 4 && Geo<2, false>::NF == 8 && Geo<1, true>::NF == 4 && Geo<2, true>::NF == 8 &&
+  static_assert(Geo<1, false>::NF == 4 && Geo<2, false>::NF == 8 && Geo<4, false>::NF == 16 &&
+                    Geo<1, true>::NF == 4 && Geo<2, true>::NF == 8 && Geo<4, true>::NF == 16 &&
                     Geo<1, true>::TPB == kWaves && Geo<1, false>::TPB == 2 * kWaves,
                 "scratch bound follows Geo");
   const bool dual = epi == EPI_SWIGLU;
-  // launch_chunk_sk: MODE 1 up to 16 rows, MODE 2 above
-  const int TPB = kWaves * (dual ? 1 : 2), NF = 4 * (nb <= 16 ? 1 : 2);
+  // launch_chunk_sk: MODE 1 up to 16 rows, MODE 2 up to 32, MODE 4 above
+  const int TPB = kWaves * (dual ? 1 : 2), NF = 4 * (nb <= 16 ? 1 : nb <= 32 ? 2 : 4);
   const long long nblocks = ((a.n_out + 31) / 32 + TPB - 1) / TPB;
   const long long U = nblocks * (a.n_in / 64);
   const long long nwg = std::min<long long>(cu_count(), U);
   *slot3 = (size_t)nwg * 2 * kWaves * NF * 64 * sizeof(f4);
-  *slot5 = a.rss ? 32 * sizeof(float) : 0;
+  *slot5 = a.rss ? 64 * sizeof(float) : 0;
 }
 
 void run_a8_sk_chunk(const GemvArgs& a_in, const uint4* XA, const float* CA, int nb, int epi, hipStream_t s) {
-  PGD_CHECK(nb >= 5 && nb <= 32, kErrArg, "stream-K A8 GEMV takes 5..32 rows per launch");
+  // 37..64 rows: two chunks, the second of at least 5 rows (1..4-row launches
+  // are another bitwise class, taken by the split-K kernels)
+  PGD_CHECK(nb >= 5 && (nb <= 32 || (nb >= 37 && nb <= 64)), kErrArg,
+            "stream-K A8 GEMV takes 5..32 or 37..64 rows per launch");
   GemvArgs a = a_in;
-  if (a.rss) a.inv = static_cast<float*>(gemv_scratch(s, 32 * sizeof(float), 5));
+  if (a.rss) a.inv = static_cast<float*>(gemv_scratch(s, 64 * sizeof(float), 5));
   if (epi == EPI_SWIGLU) launch_chunk_sk<EPI_SWIGLU>(a, XA, CA, nb, s);
   else if (epi == EPI_RES) launch_chunk_sk<EPI_RES>(a, XA, CA, nb, s);
   else launch_chunk_sk<EPI_STORE>(a, XA, CA, nb, s);

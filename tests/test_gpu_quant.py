@@ -315,13 +315,16 @@ def test_a8_pair_launch_residual(dev, rows):
         dev.free(p)
 
 
-def _class_checks(full, sub7, sub13, single, ref):
-    """Stream-K launches (5..32 rows) compute every row alike: a row's output
-    is bitwise the same in any 5..32-row launch; 1..4-row launches use the
-    split-K kernel and agree to fp32 rounding."""
+def _class_checks(full, sub7, sub13, single, ref, sub45=None):
+    """Stream-K launches (5..32 rows, and 37..64 rows as two chunks in one
+    launch) compute every row alike: a row's output is bitwise the same in any
+    such launch; 1..4-row launches use the split-K kernel and agree to fp32
+    rounding."""
     assert rel_err(full, ref) < GEMV_TOL
     np.testing.assert_array_equal(sub7.view(np.uint32), full[:7].view(np.uint32))
     np.testing.assert_array_equal(sub13.view(np.uint32), full[32:45].view(np.uint32))
+    if sub45 is not None:
+        np.testing.assert_array_equal(sub45.view(np.uint32), full[:45].view(np.uint32))
     scale = np.abs(full[3]).max()
     assert np.abs(single.astype(np.float64) - full[3]).max() <= 1e-5 * scale
 
@@ -330,16 +333,17 @@ def _class_checks(full, sub7, sub13, single, ref):
 def test_a8_stream_k_tall_matrix(dev, n_out, n_in):
     """Matrices of >= 2048 row tiles (lm_head) take the stream-K kernel for
     5..32-row launches (two tiles per wave, partial runs added by the fix-up
-    kernel); a 45-row call is one 32-row and one 13-row launch."""
+    kernel); a 64-row call (and a 45-row one) is one launch of two 32-row
+    activation chunks."""
     from pagoda_amd import Matrix
 
     m = Matrix.synth(dev, 0, n_out, n_in, 5, 3, 0.02)
     deq = m.dequant().astype(np.float64)
     rng = np.random.default_rng(n_out)
-    x = rng.normal(0, 1, (45, n_in)).astype(np.float32)
+    x = rng.normal(0, 1, (64, n_in)).astype(np.float32)
     full = m.gemv(x)
     ref = x.astype(np.float64) @ deq.T
-    _class_checks(full, m.gemv(x[:7]), m.gemv(x[32:45]), m.gemv(x[3]), ref)
+    _class_checks(full, m.gemv(x[:7]), m.gemv(x[32:45]), m.gemv(x[3]), ref, m.gemv(x[:45]))
 
 
 @pytest.mark.parametrize("n_out,n_in", [(1000, 512), (2000, 5120), (4128, 64), (17408, 5120)])
@@ -348,14 +352,15 @@ def test_a8_stream_k_swiglu(dev, n_out, n_in):
     silu(x Wg^T) * (x Wu^T) against fp64 over the dequantized weights; ragged
     last tile (n_out % 32 != 0), blocks cut into many runs (K = 5120),
     one-group rows (K = 64: every block whole in one run), the config-4
-    shape. Every launch is repeated and must give the same bits."""
+    shape; 64 and 45 rows run as one launch of two 32-row activation chunks.
+    Every launch is repeated and must give the same bits."""
     from pagoda_amd import Matrix
 
     g = Matrix.synth(dev, 0, n_out, n_in, 11, 1, 0.02)
     u = Matrix.synth(dev, 0, n_out, n_in, 11, 2, 0.02)
     dg, du = g.dequant().astype(np.float64), u.dequant().astype(np.float64)
     rng = np.random.default_rng(n_out + n_in)
-    x = rng.normal(0, 1, (45, n_in)).astype(np.float32)
+    x = rng.normal(0, 1, (64, n_in)).astype(np.float32)
 
     def run(xs):
         rows = xs.shape[0]
@@ -374,7 +379,7 @@ def test_a8_stream_k_swiglu(dev, n_out, n_in):
     x64 = x.astype(np.float64)
     a, b = x64 @ dg.T, x64 @ du.T
     ref = a / (1.0 + np.exp(-a)) * b
-    _class_checks(full, run(x[:7]), run(x[32:45]), run(x[3:4])[0], ref)
+    _class_checks(full, run(x[:7]), run(x[32:45]), run(x[3:4])[0], ref, run(x[:45]))
 
 
 @pytest.mark.parametrize("rows", [256, 300, 390, 516])
