@@ -384,3 +384,30 @@ def test_continued_long_prefill(m35):
         g, r = a.forward(toks), oracle.forward(toks, oa)
         assert rel(g, r) < LOGIT_TOL, n
     a.free()
+
+
+def test_short_and_segmented_prefill_then_decode(m35):
+    """A 2-token sequence (shorter than the conv history, so its new conv state
+    mixes old state and inputs) prefilled in one step with a 140-token one
+    (three 64-row conv segments, the chunkwise recurrence), after a first
+    feed that left both with nonzero state; then both decode. Against the
+    oracle fed the same pieces."""
+    model, oracle = m35
+    rng = np.random.default_rng(79)
+    a, b = model.new_session(), model.new_session()
+    oa, ob = oracle.new_cache(), oracle.new_cache()
+    first = [rng.integers(0, model.cfg.vocab, 5), rng.integers(0, model.cfg.vocab, 3)]
+    model.step_ragged([a, b], first)
+    oracle.forward(first[0], oa)
+    oracle.forward(first[1], ob)
+    long_p, short_p = rng.integers(0, model.cfg.vocab, 140), rng.integers(0, model.cfg.vocab, 2)
+    _, logits = model.step_ragged([a, b], [long_p, short_p], want_logits=True)
+    ra, rb = oracle.forward(long_p, oa), oracle.forward(short_p, ob)
+    assert rel(logits[0], ra) < LOGIT_TOL and rel(logits[1], rb) < LOGIT_TOL
+    for step in range(3):
+        ta, tb = ora.argmax_first(ra), ora.argmax_first(rb)
+        _, logits = model.step_ragged([a, b], [[ta], [tb]], want_logits=True)
+        ra, rb = oracle.forward([ta], oa), oracle.forward([tb], ob)
+        assert rel(logits[0], ra) < LOGIT_TOL and rel(logits[1], rb) < LOGIT_TOL, step
+    a.free()
+    b.free()
