@@ -172,14 +172,17 @@ __global__ __launch_bounds__(64 * kGW) void a8_gemm_kernel(GemvArgs a, const uin
   const uint32_t lbase = (uint32_t)(size_t)((const __attribute__((address_space(3))) char*)smem);
   const uint32_t w_lane = lbase + woff, s_lane = lbase + kStW + j16 * 4, x_lane = lbase + kStW + kStS + lane * 16,
                  c_lane = lbase + kStW + kStS + kStX + q * 16;
+  // Loads past the last group re-read it into a stage whose group is already
+  // consumed, so every iteration issues and waits alike: no branch in the
+  // loop body, and the scheduler can interleave a group's MFMAs with its
+  // folding FMAs.
   issue(0, 0);
-  if (G > 1) issue(1, 1);
-  if (G > 1) __builtin_amdgcn_s_waitcnt(NK & 15 | (7 << 4) | (15 << 8) | ((NK >> 4) << 14));  // vmcnt(NK)
-  else __builtin_amdgcn_s_waitcnt(0);
+  issue(min(1, G - 1), 1);
+  __builtin_amdgcn_s_waitcnt(NK & 15 | (7 << 4) | (15 << 8) | ((NK >> 4) << 14));  // vmcnt(NK)
   __builtin_amdgcn_s_barrier();
   for (int g = 0; g < G; ++g) {
     const int cur = g % kStages;
-    if (g + 2 < G) issue(g + 2, (g + 2) % kStages);
+    issue(min(g + 2, G - 1), (g + 2) % kStages);
     const uint32_t so = cur * kStage;
     // codes of the 4 subtiles (stage tile t, row half h = st & 1) and their scale/bias
     uint4 W[4];
@@ -249,10 +252,10 @@ __global__ __launch_bounds__(64 * kGW) void a8_gemm_kernel(GemvArgs a, const uin
     }
     // group g + 1 landed (g + 2 may still be in flight) and every wave is
     // done with stage cur, which group g + 3 overwrites
-    if (g + 2 < G) __builtin_amdgcn_s_waitcnt(NK & 15 | (7 << 4) | (15 << 8) | ((NK >> 4) << 14));
-    else __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(NK & 15 | (7 << 4) | (15 << 8) | ((NK >> 4) << 14));
     __builtin_amdgcn_s_barrier();
   }
+  __builtin_amdgcn_s_waitcnt(0);  // the re-read loads of the last iterations
 
   // deferred RMSNorm of the input: 1/rms of each batch row (rss_inv needs the
   // whole wave), applied to the accumulators before the epilogue
