@@ -8,6 +8,8 @@ namespace pgd {
 
 namespace {
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
 // ---------------------------------------------------------------------------
 // block reductions (256 threads = 4 waves)
 // ---------------------------------------------------------------------------
@@ -336,6 +338,30 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnParams p, const int* 
   const float a_log = p.a_log[h], dtb = p.dt_bias[h];
   const float qscale = sqrtf((float)D);
   const int c = tid & (NCOL - 1), tq = tid >> 5;  // column phases: column c, tokens 4 tq ..
+  // a chunk's q, k (token (tid / 32) + 8 jj, elements 4 (tid % 32)..) and v
+  // (token tid / 8, columns 4 (tid % 8)..) in registers, loaded one chunk
+  // ahead so that no chunk waits for its inputs; zeros past the sequence
+  float4 qn[4], kn[4], vn;
+  auto load_chunk = [&](int tc) {
+    const int mc = min(C, n - tc);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int t = (tid >> 5) + 8 * jj, e = (tid & 31) * 4;
+      qn[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
+      kn[jj] = qn[jj];
+      if (t < mc) {
+        const float* cv = p.conv_out + (size_t)(r0 + tc + t) * p.ld_conv;
+        qn[jj] = *reinterpret_cast<const float4*>(cv + kh * D + e);
+        kn[jj] = *reinterpret_cast<const float4*>(cv + key_dim + kh * D + e);
+      }
+    }
+    const int t = tid >> 3, e = (tid & 7) * 4;
+    vn = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < mc)
+      vn = *reinterpret_cast<const float4*>(p.conv_out + (size_t)(r0 + tc + t) * p.ld_conv + 2 * key_dim + h * D +
+                                            col0 + e);
+  };
+  load_chunk(0);
 
   for (int t0 = 0; t0 < n; t0 += C) {
     const int m = min(C, n - t0);
@@ -344,12 +370,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnParams p, const int* 
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int t = (tid >> 5) + 8 * jj, e = (tid & 31) * 4;
-      float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4;
-      if (t < m) {
-        const float* cv = p.conv_out + (size_t)(r0 + t0 + t) * p.ld_conv;
-        q4 = *reinterpret_cast<const float4*>(cv + kh * D + e);
-        k4 = *reinterpret_cast<const float4*>(cv + key_dim + kh * D + e);
-      }
+      const float4 q4 = qn[jj], k4 = kn[jj];
       float sq = q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w;
       float sk = k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w;
 #pragma unroll
@@ -370,11 +391,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnParams p, const int* 
     {
       // v of this group's columns: token tid / 8, 4 columns
       const int t = tid >> 3, e = (tid & 7) * 4;
-      float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (t < m) v4 = *reinterpret_cast<const float4*>(p.conv_out + (size_t)(r0 + t0 + t) * p.ld_conv + 2 * key_dim +
-                                                      h * D + col0 + e);
-      *reinterpret_cast<float4*>(Uc + t * CP + e) = v4;
+      *reinterpret_cast<float4*>(Uc + t * CP + e) = vn;
     }
+    if (t0 + C < n) load_chunk(t0 + C);
     if (tid < 64) {
       // decay and beta per token, then the running sum of the log decay
       float g = 0.f, beta = 0.f;
@@ -394,68 +413,63 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnParams p, const int* 
       }
     }
     __syncthreads();
-    if (tid < 128) {
-      // L (threads 0..63) and B (64..127), 4x4 blocks of tokens t x i
-      const int which = tid >> 6, b = tid & 63, tb = (b >> 3) * 4, ib = (b & 7) * 4;
-      const float* X = which ? QT : KT;
-      float acc[4][4] = {};
-#pragma unroll 4
-      for (int r = 0; r < D; ++r) {
-        const float4 x4 = *reinterpret_cast<const float4*>(X + r * TP + tb);
-        const float4 y4 = *reinterpret_cast<const float4*>(KT + r * TP + ib);
-        const float xv[4] = {x4.x, x4.y, x4.z, x4.w}, yv[4] = {y4.x, y4.y, y4.z, y4.w};
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int bb = 0; bb < 4; ++bb) acc[a][bb] = fmaf(xv[a], yv[bb], acc[a][bb]);
-      }
-      float* M = which ? Bm : Lm;
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int t = tb + a;
-        float v4[4];
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
-          const int i = ib + bb;
-          float v = 0.f;
-          if (t < m && (which ? i <= t : i < t)) {
-            const float w = expf(Gs[t] - Gs[i]);
-            v = which ? w * acc[a][bb] : Bs[t] * (w * acc[a][bb]);
-          }
-          v4[bb] = v;
+    // fp32 MFMA tiles (v_mfma_f32_16x16x4_f32): lane l supplies A[row l % 16]
+    // [k l / 16] and B[k l / 16][col l % 16] and holds D[4 (l / 16) + r][l % 16].
+    const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lk = lane >> 4;
+    {
+      // L (t x i, i < t) and B (i <= t) from K K^T and Q K^T over the 128 k:
+      // waves 0..2 take the three nonzero 16x16 tiles of both, wave 3 writes
+      // the zero tile above the diagonal
+      if (wave < 3) {
+        const int tb = wave == 0 ? 0 : 16, ib = wave == 2 ? 16 : 0;
+        f4 aL = {0.f, 0.f, 0.f, 0.f}, aB = aL;
+#pragma unroll 8
+        for (int k0 = 0; k0 < D; k0 += 4) {
+          const float* kr = KT + (k0 + lk) * TP;
+          const float ki = kr[ib + lr];
+          aL = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[tb + lr], ki, aL, 0, 0, 0);
+          aB = __builtin_amdgcn_mfma_f32_16x16x4f32(QT[(k0 + lk) * TP + tb + lr], ki, aB, 0, 0, 0);
         }
-        *reinterpret_cast<float4*>(M + t * TP + ib) = make_float4(v4[0], v4[1], v4[2], v4[3]);
+        const int i = ib + lr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = tb + 4 * lk + r;
+          float vl = 0.f, vb = 0.f;
+          if (t < m && i <= t) {
+            const float w = expf(Gs[t] - Gs[i]);
+            vb = w * aB[r];
+            if (i < t) vl = Bs[t] * (w * aL[r]);
+          }
+          Lm[t * TP + i] = vl;
+          Bm[t * TP + i] = vb;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 4 * lk + r, i = 16 + lr;
+          Lm[t * TP + i] = 0.f;
+          Bm[t * TP + i] = 0.f;
+        }
       }
     }
     {
-      // W = K S0 and Z = Q S0 as 2x2 blocks (tokens tw.., columns cw..); then
-      // U = beta (v - gamma W) and gamma Z
-      const int tw = (tid >> 4) * 2, cw = (tid & 15) * 2;
-      float w[2][2] = {}, z[2][2] = {};
+      // W = K S0 and Z = Q S0: wave w takes tokens 16 (w / 2).., columns
+      // 16 (w % 2)..; then U = beta (v - gamma W) and gamma Z
+      const int tb = 16 * (wave >> 1), cb = 16 * (wave & 1);
+      f4 aW = {0.f, 0.f, 0.f, 0.f}, aZ = aW;
 #pragma unroll 8
-      for (int r = 0; r < D; ++r) {
-        const float2 k2 = *reinterpret_cast<const float2*>(KT + r * TP + tw);
-        const float2 q2 = *reinterpret_cast<const float2*>(QT + r * TP + tw);
-        const float2 s2 = *reinterpret_cast<const float2*>(S + r * CP + cw);
-        w[0][0] = fmaf(k2.x, s2.x, w[0][0]);
-        w[0][1] = fmaf(k2.x, s2.y, w[0][1]);
-        w[1][0] = fmaf(k2.y, s2.x, w[1][0]);
-        w[1][1] = fmaf(k2.y, s2.y, w[1][1]);
-        z[0][0] = fmaf(q2.x, s2.x, z[0][0]);
-        z[0][1] = fmaf(q2.x, s2.y, z[0][1]);
-        z[1][0] = fmaf(q2.y, s2.x, z[1][0]);
-        z[1][1] = fmaf(q2.y, s2.y, z[1][1]);
+      for (int k0 = 0; k0 < D; k0 += 4) {
+        const float sv = S[(k0 + lk) * CP + cb + lr];
+        aW = __builtin_amdgcn_mfma_f32_16x16x4f32(KT[(k0 + lk) * TP + tb + lr], sv, aW, 0, 0, 0);
+        aZ = __builtin_amdgcn_mfma_f32_16x16x4f32(QT[(k0 + lk) * TP + tb + lr], sv, aZ, 0, 0, 0);
       }
+      const int cc = cb + lr;
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const int t = tw + a;
+      for (int r = 0; r < 4; ++r) {
+        const int t = tb + 4 * lk + r;
         const float gam = expf(Gs[t]), bet = Bs[t];
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-          const int cc = cw + bb;
-          Uc[t * CP + cc] = bet * (Uc[t * CP + cc] - gam * w[a][bb]);
-          Zc[t * CP + cc] = gam * z[a][bb];
-        }
+        Uc[t * CP + cc] = bet * (Uc[t * CP + cc] - gam * aW[r]);
+        Zc[t * CP + cc] = gam * aZ[r];
       }
     }
     __syncthreads();
@@ -496,42 +510,24 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnParams p, const int* 
     }
     __syncthreads();
     {
-      // S = gamma_m S0 + K^T (weighted d) as 4x4 blocks (rows rb.., columns cb..)
-      const int rb = (tid >> 3) * 4, cb = (tid & 7) * 4;
+      // S = gamma_m S0 + K^T (weighted d): wave w takes k rows 32 w .. 32 w + 31
+      // (two 16-row tiles) by both 16-column tiles, 8 MFMA steps over the tokens
       const float gm = expf(gl);
-      float acc[4][4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float4 s4 = *reinterpret_cast<const float4*>(S + (rb + a) * CP + cb);
-        acc[a][0] = gm * s4.x;
-        acc[a][1] = gm * s4.y;
-        acc[a][2] = gm * s4.z;
-        acc[a][3] = gm * s4.w;
-      }
-#pragma unroll 2
-      for (int i = 0; i < C; i += 4) {
-        float kk[4][4];
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const float4 k4 = *reinterpret_cast<const float4*>(KT + (rb + a) * TP + i);
-          kk[a][0] = k4.x;
-          kk[a][1] = k4.y;
-          kk[a][2] = k4.z;
-          kk[a][3] = k4.w;
+        for (int ct = 0; ct < 2; ++ct) {
+          const int kb = 32 * wave + 16 * kt, cb = 16 * ct;
+          f4 acc;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = gm * S[(kb + 4 * lk + r) * CP + cb + lr];
+#pragma unroll
+          for (int i0 = 0; i0 < C; i0 += 4)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(KT[(kb + lr) * TP + i0 + lk], Uc[(i0 + lk) * CP + cb + lr], acc,
+                                                       0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) S[(kb + 4 * lk + r) * CP + cb + lr] = acc[r];
         }
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const float4 d4 = *reinterpret_cast<const float4*>(Uc + (i + ii) * CP + cb);
-          const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-          for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb) acc[a][bb] = fmaf(kk[a][ii], dv[bb], acc[a][bb]);
-        }
-      }
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-        *reinterpret_cast<float4*>(S + (rb + a) * CP + cb) = make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
     }
   }
   __syncthreads();
