@@ -81,10 +81,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 // old state ++ x), so no segment reads a state another has rewritten.
 constexpr int kConvSeg = 64;
 
+// KW: the conv kernel length (a compile-time constant, so the window lives in
+// registers rather than in per-lane scratch memory)
+template <int KW>
 __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict__ x, int ldx, float* __restrict__ out,
-                                                        int ldo, int channels, int kernel,
-                                                        const float* __restrict__ weight, float* const* state_base,
-                                                        size_t state_off, const int* row_start, const int* row_count) {
+                                                        int ldo, int channels, const float* __restrict__ weight,
+                                                        float* const* state_base, size_t state_off,
+                                                        const int* row_start, const int* row_count) {
+  constexpr int kernel = KW;
   const int c = blockIdx.x * 256 + threadIdx.x;
   const int s = blockIdx.y;
   if (c >= channels) return;
@@ -92,11 +96,12 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
   const int t_beg = blockIdx.z * kConvSeg;
   if (t_beg >= n && (blockIdx.z > 0 || n > 0)) return;
   const int t_end = gridDim.z == 1 ? n : min(n, t_beg + kConvSeg);
-  const int hist = kernel - 1;
+  constexpr int hist = kernel - 1, HA = hist > 0 ? hist : 1;
   float* st = state_base[s] + state_off + (size_t)c * hist;
-  float win[8];
-  float wt[8];
-  float old[8];
+  float win[HA];
+  float wt[kernel];
+  float old[HA];
+#pragma unroll
   for (int k = 0; k < hist; ++k) {
     // window before row t_beg: inputs t_beg-hist..t_beg-1, from the state before row 0
     const int t = t_beg - hist + k;
@@ -104,7 +109,9 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
   }
   const bool whole = gridDim.z == 1;  // this thread runs every row: the last window is the new state
   if (!whole)
+#pragma unroll
     for (int k = 0; k < hist; ++k) old[k] = win[k];
+#pragma unroll
   for (int k = 0; k < kernel; ++k) wt[k] = weight[(size_t)c * kernel + k];
   // inputs loaded eight rows ahead (the steps are sequential; the loads are not)
   constexpr int PF = 8;
@@ -117,21 +124,34 @@ __global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict_
     for (int k = 0; k + 1 < PF; ++k) xr[k] = xr[k + 1];
     xr[PF - 1] = t + PF < t_end ? x[(size_t)(r0 + t + PF) * ldx + c] : 0.0f;
     float acc = 0.0f;
+#pragma unroll
     for (int k = 0; k < hist; ++k) acc += win[k] * wt[k];
     acc += xv * wt[hist];
     out[(size_t)(r0 + t) * ldo + c] = acc / (1.0f + expf(-acc));
+#pragma unroll
     for (int k = 0; k + 1 < hist; ++k) win[k] = win[k + 1];
-    if (hist > 0) win[hist - 1] = xv;
+    if constexpr (hist > 0) win[hist - 1] = xv;
   }
   if (whole) {
+#pragma unroll
     for (int k = 0; k < hist; ++k) st[k] = win[k];
     return;
   }
   if (blockIdx.z != 0) return;
+#pragma unroll
   for (int k = 0; k < hist; ++k) {
-    // new state: inputs n-hist..n-1 of old state ++ x
+    // new state: inputs n-hist..n-1 of old state ++ x (old[] picked with
+    // compile-time indices, so it stays in registers)
     const int t = n - hist + k;
-    st[k] = t < 0 ? old[hist + t] : x[(size_t)(r0 + t) * ldx + c];
+    float v = 0.0f;
+    if (t < 0) {
+#pragma unroll
+      for (int jj = 0; jj < hist; ++jj)
+        if (jj == hist + t) v = old[jj];
+    } else {
+      v = x[(size_t)(r0 + t) * ldx + c];
+    }
+    st[k] = v;
   }
 }
 
@@ -746,8 +766,23 @@ void conv_step(const float* x, int ldx, float* out, int ldo, int channels, int k
   PGD_CHECK(kernel >= 1 && kernel <= 8, kErrShape, "conv kernel must be in 1..8");
   if (nseq <= 0) return;
   const int segs = max_rows > kConvSeg ? (max_rows + kConvSeg - 1) / kConvSeg : 1;
-  hipLaunchKernelGGL(conv_step_kernel, dim3((channels + 255) / 256, nseq, segs), dim3(256), 0, s, x, ldx, out, ldo, channels,
-                     kernel, weight, state_base, state_off, meta.row_start, meta.row_count);
+  const dim3 grid((channels + 255) / 256, nseq, segs);
+#define PGD_CONV_CASE(K)                                                                                            \
+  case K:                                                                                                          \
+    hipLaunchKernelGGL(conv_step_kernel<K>, grid, dim3(256), 0, s, x, ldx, out, ldo, channels, weight, state_base, \
+                       state_off, meta.row_start, meta.row_count);                                                 \
+    break;
+  switch (kernel) {
+    PGD_CONV_CASE(1)
+    PGD_CONV_CASE(2)
+    PGD_CONV_CASE(3)
+    PGD_CONV_CASE(4)
+    PGD_CONV_CASE(5)
+    PGD_CONV_CASE(6)
+    PGD_CONV_CASE(7)
+    PGD_CONV_CASE(8)
+  }
+#undef PGD_CONV_CASE
   PGD_HIP(hipGetLastError());
 }
 
