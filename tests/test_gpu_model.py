@@ -411,3 +411,25 @@ def test_short_and_segmented_prefill_then_decode(m35):
         assert rel(logits[0], ra) < LOGIT_TOL and rel(logits[1], rb) < LOGIT_TOL, step
     a.free()
     b.free()
+
+
+def test_forty_row_steps_take_two_chunk_launches(m35):
+    """40 sessions stepped together: a 120-row prefill (two 64- and 56-row
+    launches) and 40-row decode steps, so the fused gate/up runs as stream-K
+    launches of two 32-row activation chunks. Every session against the
+    oracle fed the same tokens, and each step's greedy ids equal the oracle's."""
+    model, oracle = m35
+    rng = np.random.default_rng(80)
+    n = 40
+    sess = [model.new_session() for _ in range(n)]
+    caches = [oracle.new_cache() for _ in range(n)]
+    feeds = [rng.integers(0, model.cfg.vocab, 3) for _ in range(n)]
+    for step in range(3):
+        _, logits = model.step_ragged(sess, feeds, want_logits=True)
+        refs = [oracle.forward(f, c) for f, c in zip(feeds, caches)]
+        for i in range(n):
+            assert rel(logits[i], refs[i]) < LOGIT_TOL, (step, i)
+        feeds = [[ora.argmax_first(r)] for r in refs]
+        assert [ora.argmax_first(l) for l in logits] == [f[0] for f in feeds], step
+    for s in sess:
+        s.free()
