@@ -152,7 +152,8 @@ int pgd_gdn_step_dev(pgd_dev* dev, int k_heads, int v_heads, const float* conv_o
  * and matrix products against each chunk's starting state, the published
  * chunked form of the gated delta rule; equal to the per-token loop in exact
  * arithmetic, to fp32 rounding in practice). rows: every sequence's
- * row_start + row_count is at most rows. max_rows: the largest row_count, or
+ * row_start + row_count is at most rows (rows past it are left unwritten,
+ * never written out of bounds). max_rows: the largest row_count, or
  * any bound on it (below 32 every sequence takes the per-token kernel).
  * Replaces the same reference loop as pgd_gdn_step_dev, which it runs one
  * token at a time for prefill too (qwen3_5.rs:1330-1383). */

@@ -55,6 +55,7 @@ struct GdnParams {
   // set by gdn_step, not by callers: the recurrence outputs of the chunkwise
   // form before their gated norm, [rows, v_heads * v_dim] (null: step kernel only)
   float* o_raw;
+  int o_rows;  // rows of o_raw (rows past it are not written or read)
 };
 
 // Gated-DeltaNet recurrence over each sequence's rows in order

@@ -518,7 +518,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_kernel(GdnParams p, const int* 
         o = fmaf(b4.z, d[i4 + 2], o);
         o = fmaf(b4.w, d[i4 + 3], o);
       }
-      if (t < m) p.o_raw[(size_t)(r0 + t0 + t) * ldo + h * D + col0 + c] = o;
+      if (t < m && r0 + t0 + t < p.o_rows) p.o_raw[(size_t)(r0 + t0 + t) * ldo + h * D + col0 + c] = o;
     }
     const float gl = Gs[m - 1];
 #pragma unroll
@@ -586,9 +586,11 @@ __global__ __launch_bounds__(128) void gdn_norm_kernel(GdnParams p, const int* r
   const int s = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
   const int n = row_count[s];
   if (n < kGdnLongRows) return;
-  for (int t = blockIdx.x; t < n; t += gridDim.x) {
+  // (rows at or past o_rows were never staged: a caller's rows bound was too small)
+  const int r0 = row_start[s], t_end = min(n, p.o_rows - r0);
+  for (int t = blockIdx.x; t < t_end; t += gridDim.x) {
     __syncthreads();  // part and obuf of the previous row are consumed
-    gdn_norm_row(p, row_start[s] + t, h, tid, part, obuf);
+    gdn_norm_row(p, r0 + t, h, tid, part, obuf);
   }
 }
 
@@ -792,6 +794,7 @@ void gdn_step(const GdnParams& p, SeqMeta meta, int nseq, int rows, int max_rows
   if (nseq <= 0) return;
   const bool chunked = rows > 0 && max_rows >= kGdnLongRows;
   GdnParams q = p;
+  q.o_rows = chunked ? rows : 0;
   q.o_raw = chunked ? static_cast<float*>(gemv::gemv_scratch(s, (size_t)rows * p.v_heads * 128 * sizeof(float), 7))
                     : nullptr;
   hipLaunchKernelGGL(gdn_kernel<kGdnRowGroups>, dim3(p.v_heads, nseq), dim3(32 * kGdnRowGroups), 0, s, q,
