@@ -387,7 +387,7 @@ __global__ __launch_bounds__(64) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArg
     const int slot = r == r0 ? slot_r0 : 0;
     return k.part + ((((size_t)r * 2 + slot) * kWaves + wave) * NF + f) * 64 + lane;
   };
-  constexpr int RB = NF >= 16 ? 2 : NF >= 8 ? 4 : 8;  // runs loaded together
+  constexpr int RB = NF >= 16 ? 2 : NF >= 8 ? 5 : 8;  // runs loaded together
   f4 V[NS][NBT];
   for (int r = r0; r <= r1; r += RB) {
     f4 P[RB][NS][NBT];
