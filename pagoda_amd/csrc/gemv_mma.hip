@@ -806,6 +806,43 @@ __global__ __launch_bounds__(kRedT) void a8_reduce_kernel(GemvArgs a, int nb, co
   a.y[o + 1] = y.y;
   a.y[o + 2] = y.z;
   a.y[o + 3] = y.w;
+  if constexpr (EPI == EPI_STORE) {
+    // causal conv of the conv channels (every row its sequence's only token),
+    // as the split-K kernels' epilogue runs it
+    if (a.cout && n < a.conv_n) {
+      const float v[4] = {y.x, y.y, y.z, y.w};
+      const int row = a.row0 + b;
+      if (a.conv_k == 4 && n + 4 <= a.conv_n) {
+        // the four channels' states and weights are loaded before any store,
+        // so the loads overlap (conv_channel's arithmetic and order)
+        float* cs = a.cbase[row] + a.coff + (size_t)n * 3;
+        const float* wt = a.cw + (size_t)n * 4;
+        float sv[12], wv[16];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) sv[i] = cs[i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) wv[i] = wt[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int k = 0; k < 3; ++k) acc += sv[3 * e + k] * wv[4 * e + k];
+          acc += v[e] * wv[4 * e + 3];
+          a.cout[(size_t)row * a.ldc + n + e] = acc / (1.0f + expf(-acc));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          cs[3 * e] = sv[3 * e + 1];
+          cs[3 * e + 1] = sv[3 * e + 2];
+          cs[3 * e + 2] = v[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < a.conv_n) conv_channel(a, row, n + e, v[e]);
+      }
+    }
+  }
 }
 
 // The residual reduction of a8_reduce_kernel that also emits the next

@@ -511,11 +511,10 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       // the input norm's deferred operands: written by the previous layer's down
       // projection, or prepared here for the first layer; one GEMV for all projections
       A8Act act = have_next_in ? next_in : a8_gnorm_prep(w.x, H, rows, H, L.in_norm, eps, w.act, st);
-      // one token per sequence, at most 4 rows: the GEMV's epilogue also runs
-      // the causal conv, row r on sequence r's state (more rows: the
-      // reduction kernel holds the outputs, and a conv there measured slower
-      // than the conv kernel)
-      conv_done = !L.full && rows == nseq && rows <= 4;
+      // one token per sequence: the GEMV's epilogue (1..4 rows, and the
+      // per-wave kernels) or its range reduction also runs the causal conv,
+      // row r on sequence r's state
+      conv_done = !L.full && rows == nseq;
       if (conv_done)
         qmat_gemv_a8_conv(L.proj, act, w.A, (int)w.lda, L.conv, d_sb, (size_t)L.lin_index * per_lin, m.conv_dim,
                           c.conv_kernel, w.D, (int)w.ldd, st);

@@ -171,8 +171,8 @@ A8Act a8_norm_prep(const float* x, int ldx, const int* rows_idx, int rows, int n
 void qmat_gemv_a8(const QMat& m, const A8Act& act, float* y, int ldy, const float* res, int ldres, hipStream_t s);
 // device scratch bytes qmat_gemv_a8 takes for `rows` rows (res: residual form)
 size_t qmat_gemv_a8_scratch(const QMat& m, int rows, bool res);
-// qmat_gemv_a8 (store) of 1..4 rows for a step where row r is the only token
-// of sequence r: outputs n < conv_n of row r also take the causal conv step of channel n
+// qmat_gemv_a8 (store) for a step where row r is the only token of sequence
+// r: outputs n < conv_n of row r also take the causal conv step of channel n
 // (the conv_step arithmetic): weights conv_w [conv_n][kernel], state at
 // state_base[r] + state_off, [conv_n][kernel - 1] (updated), SiLU output to
 // conv_out[r * ldc + n].

@@ -710,8 +710,9 @@ void qmat_gemv_a8_conv(const QMat& m, const A8Act& act, float* y, int ldy, const
   PGD_CHECK(m.fmt == FMT_A8, kErrFormat, "prepared activations feed A8 matrices");
   PGD_CHECK(conv_n <= m.n_out && kernel >= 1 && kernel <= 8 && conv_w && state_base && conv_out, kErrShape,
             "conv epilogue arguments");
-  // 1..4 rows run one launch of the split-K kernel, whose epilogue holds the outputs
-  PGD_CHECK(act.rows >= 1 && act.rows <= 4, kErrShape, "the conv epilogue is for launches of 1..4 rows");
+  // the split-K kernels' epilogue or the range reduction holds the outputs;
+  // every row must be its sequence's only token (row r on state r)
+  PGD_CHECK(act.rows >= 1, kErrShape, "the conv epilogue needs rows");
   GemvArgs a = make_args(m);
   a.y = y;
   a.ldy = ldy;
