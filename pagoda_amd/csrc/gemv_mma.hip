@@ -553,7 +553,7 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
         const size_t o = (size_t)b * a.ldy + n;
         if constexpr (EPI == EPI_STORE) {
           a.y[o] = Y[st][bt][r];
-          if (a.cout && n < a.conv_n) conv_channel(a, a.row0 + b, n, Y[st][bt][r]);
+          if (a.cout && a.conv_k != 4 && n < a.conv_n) conv_channel(a, a.row0 + b, n, Y[st][bt][r]);
         }
         if constexpr (EPI == EPI_RES) {
           const float h = a.res[(size_t)b * a.ldres + n] + Y[st][bt][r];
@@ -562,6 +562,54 @@ __global__ __launch_bounds__(64 * KP) void a8_mma_kernel(GemvArgs a, const uint4
         }
         if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(Y[st][bt][r]) * Y[NSM + st][bt][r];
       }
+  }
+  if constexpr (EPI == EPI_STORE) {
+    if (a.cout && a.conv_k == 4) {
+      // causal conv of this lane's (row, channel) pairs, conv_channel's
+      // arithmetic and order: every state and weight is loaded before any
+      // store, so the loads of all pairs overlap
+      constexpr int NR = MODE == 3 ? 1 : 4, NPR = NSM * NBT * NR;
+      float sv[NPR][3], wv[NSM][4], xv[NPR];
+      float* sp[NPR];
+      bool live[NPR];
+#pragma unroll
+      for (int st = 0; st < NSM; ++st) {
+        const int n = (blockIdx.x * MT + (st >> 1)) * 32 + 16 * (st & 1) + j;
+        const bool cn = n < a.n_out && n < a.conv_n;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wv[st][k] = cn ? a.cw[(size_t)n * 4 + k] : 0.0f;
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            const int i = (st * NBT + bt) * NR + r, b = 16 * bt + 4 * q + r;
+            live[i] = cn && b < nb;
+            xv[i] = Y[st][bt][r];
+            sp[i] = live[i] ? a.cbase[a.row0 + b] + a.coff + (size_t)n * 3 : nullptr;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) sv[i][k] = live[i] ? sp[i][k] : 0.0f;
+          }
+      }
+#pragma unroll
+      for (int st = 0; st < NSM; ++st) {
+        const int n = (blockIdx.x * MT + (st >> 1)) * 32 + 16 * (st & 1) + j;
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            const int i = (st * NBT + bt) * NR + r, b = 16 * bt + 4 * q + r;
+            if (!live[i]) continue;
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) acc += sv[i][k] * wv[st][k];
+            acc += xv[i] * wv[st][3];
+            a.cout[(size_t)(a.row0 + b) * a.ldc + n] = acc / (1.0f + expf(-acc));
+            sp[i][0] = sv[i][1];
+            sp[i][1] = sv[i][2];
+            sp[i][2] = xv[i];
+          }
+      }
+    }
   }
   if constexpr (EPI == EPI_RES && MT == 1) {
     if (emit) {
