@@ -371,10 +371,25 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
 // Cut blocks: add the runs' partial sums in run order, then the epilogue.
 // One single-wave workgroup per (block, wave of the streaming kernel), so the
 // few blocks of a matrix still spread over many compute units.
+// MODE 4 (two 32-row chunks): grid y = chunk, each workgroup the 32-row
+// fix-up of its chunk's batch tiles (half the accumulators, so five runs load
+// together), with the rows, outputs and row scales offset by 32.
 template <int MODE, int EPI>
 __global__ __launch_bounds__(64) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArgs k) {
-  using Gm = Geo<MODE, EPI == EPI_SWIGLU>;
+  using Gs = Geo<MODE, EPI == EPI_SWIGLU>;  // the streaming kernel's (partial-sum layout)
+  constexpr int CM = Gs::NC == 2 ? 2 : MODE;  // one chunk's mode
+  using Gm = Geo<CM, EPI == EPI_SWIGLU>;
   constexpr int NS = Gm::NS, NBT = Gm::NBT, NF = Gm::NF;
+  const int ch = Gs::NC == 2 ? blockIdx.y : 0;
+  if (Gs::NC == 2) {
+    if (ch == 1) {
+      a.row0 += 32;
+      if (a.y) a.y += (size_t)32 * a.ldy;
+      if (a.res) a.res += (size_t)32 * a.ldres;
+      if (a.inv) a.inv += 32;
+    }
+    nb = ch == 1 ? nb - 32 : min(nb, 32);
+  }
   __shared__ __attribute__((aligned(16))) char smem[Gm::HB > 0 ? Gm::HB / kWaves : 16];
   const int blk = blockIdx.x / kWaves, wave = blockIdx.x % kWaves, lane = threadIdx.x;
   const long long b0 = (long long)blk * k.G;
@@ -385,7 +400,7 @@ __global__ __launch_bounds__(64) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArg
   const int slot_r0 = run_start(k.U, k.nwg, r0) < b0 ? 1 : 0;
   auto at = [&](int r, int f) -> const f4* {
     const int slot = r == r0 ? slot_r0 : 0;
-    return k.part + ((((size_t)r * 2 + slot) * kWaves + wave) * NF + f) * 64 + lane;
+    return k.part + ((((size_t)r * 2 + slot) * kWaves + wave) * Gs::NF + f) * 64 + lane;
   };
   constexpr int RB = NF >= 16 ? 2 : NF >= 8 ? 5 : 8;  // runs loaded together
   f4 V[NS][NBT];
@@ -396,7 +411,7 @@ __global__ __launch_bounds__(64) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArg
 #pragma unroll
       for (int st = 0; st < NS; ++st)
 #pragma unroll
-        for (int bt = 0; bt < NBT; ++bt) P[t][st][bt] = *at(min(r + t, r1), st * NBT + bt);
+        for (int bt = 0; bt < NBT; ++bt) P[t][st][bt] = *at(min(r + t, r1), st * Gs::NBT + ch * NBT + bt);
 #pragma unroll
     for (int t = 0; t < RB; ++t) {
       if (r + t > r1) break;
@@ -407,7 +422,7 @@ __global__ __launch_bounds__(64) void a8_sk_fix_kernel(GemvArgs a, int nb, SkArg
     }
   }
   if (a.rss) scale_rows(V, a.inv, nb);
-  wave_epilogue<MODE, EPI>(a, nb, blk, wave, V, reinterpret_cast<float*>(smem));
+  wave_epilogue<CM, EPI>(a, nb, blk, wave, V, reinterpret_cast<float*>(smem));
 }
 
 // ---- host side ----
@@ -436,7 +451,7 @@ void launch_sk(const GemvArgs& a, const uint4* XA, const float* CA, int nb, hipS
   k.nwg = (int)std::min<long long>(cu_count(), k.U);
   k.part = static_cast<f4*>(gemv_scratch(s, (size_t)k.nwg * 2 * kWaves * Gm::NF * 64 * sizeof(f4), 3));
   hipLaunchKernelGGL((a8_sk_kernel<MODE, EPI, D>), dim3(k.nwg), dim3(64 * kWaves), 0, s, a, XA, CA, nb, k);
-  hipLaunchKernelGGL((a8_sk_fix_kernel<MODE, EPI>), dim3(k.nblocks * kWaves), dim3(64), 0, s, a, nb, k);
+  hipLaunchKernelGGL((a8_sk_fix_kernel<MODE, EPI>), dim3(k.nblocks * kWaves, Gm::NC), dim3(64), 0, s, a, nb, k);
 }
 
 template <int EPI>
