@@ -121,6 +121,13 @@ int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up,
  * scaled in f32. res (nullable) adds a residual as in pgd_matrix_gemv_dev. */
 int pgd_matrix_gemv_q8act_dev(const pgd_matrix* m, const float* x, int ldx, int nrows, float* y, int ldy,
                               const float* res, int ldres);
+/* Two pgd_matrix_gemv_q8act_dev calls over the same input rows in one launch
+ * (the Qwen2 attention's q/k and v projections, qwen2_gguf.rs:234-236, whose
+ * GGML types differ in Q4_K_M files): ya = a.x and yb = b.x, row stride ldy,
+ * bit-equal to the two calls. Both matrices take the same input width and one
+ * activation type (Q4_K / Q6_K: Q8_K; Q8_0 / Q5_0: Q8_0), else PGD_ERR_FORMAT. */
+int pgd_matrix_gemv_q8act_pair_dev(const pgd_matrix* a, float* ya, const pgd_matrix* b, float* yb, const float* x,
+                                   int ldx, int nrows, int ldy);
 /* No counterpart in the reference. pgd_matrix_gemv_act_dev for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc): the same kernels and results, with

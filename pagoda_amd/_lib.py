@@ -49,6 +49,7 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_act_prep_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "pgd_matrix_gemv_act_dev": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_int]),
     "pgd_matrix_gemv_q8act_dev": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p, c_int]),
+    "pgd_matrix_gemv_q8act_pair_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int]),
     "pgd_model_set_kquant_arith": (c_int, [c_void_p, c_int]),
     "pgd_matrix_gemv_act_dev_noalloc": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_int, c_void_p, c_int]),
     "pgd_noalloc_scratch_bytes": (c_size_t, []),

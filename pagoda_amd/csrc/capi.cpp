@@ -407,6 +407,17 @@ int pgd_matrix_gemv_q8act_dev(const pgd_matrix* m, const float* x, int ldx, int 
   });
 }
 
+int pgd_matrix_gemv_q8act_pair_dev(const pgd_matrix* a, float* ya, const pgd_matrix* b, float* yb, const float* x,
+                                   int ldx, int nrows, int ldy) {
+  return guard([&] {
+    PGD_CHECK(a && b && ya && yb && x && nrows > 0 && a->dev == b->dev, kErrArg, "bad argument");
+    PGD_CHECK(a->m.n_in == b->m.n_in, kErrShape, "paired matrices need one input width");
+    PGD_CHECK(qmat_q8act_pairable(a->m, b->m), kErrFormat, "paired matrices need one activation type");
+    DeviceScope scope(a->dev);
+    qmat_gemv_q8act_pair(a->m, ya, b->m, yb, x, ldx, nrows, ldy, a->dev->stream);
+  });
+}
+
 int pgd_matrix_gemv_swiglu_act_dev(const pgd_matrix* gate, const pgd_matrix* up, const void* act, int nrows,
                                    float* mid, int ldm) {
   return guard([&] {

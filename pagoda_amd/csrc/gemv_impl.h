@@ -456,6 +456,9 @@ void sk_scratch_need(const GemvArgs& a, int nb, int epi, size_t* slot3, size_t* 
 // GGML formats with candle's CPU arithmetic (activations quantized to Q8_K /
 // Q8_0, integer block dots); f32 activations
 void run_q8act(int fmt, const GemvArgs& a, int nrows, int epi, hipStream_t s);
+// two store GEMVs of one input in one launch (formats of one activation type)
+bool q8act_pair_ok(int fmt_a, int fmt_b);
+void run_q8act_pair(int fmt_a, const GemvArgs& a, int fmt_b, const GemvArgs& b, int nrows, hipStream_t s);
 // A8 on the matrix cores (f32 activations)
 void run_a8_mma(const GemvArgs& a, const A8Act& act, int epi, hipStream_t s);
 // A8 GEMM for prefill-sized batches: rows [0, rows) of a prepared activation

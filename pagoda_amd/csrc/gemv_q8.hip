@@ -26,6 +26,8 @@
 // blocks) per 32-row tile of the weight matrix; wave w takes K blocks w,
 // w + NW, ... (256-element super-blocks, or 32-weight blocks). Weights are
 // read once per launch of up to RB activation rows.
+#include <type_traits>
+
 #include "common.h"
 #include "gemv_impl.h"
 #include "quant.h"
@@ -381,15 +383,13 @@ __device__ void dots_q32(const GemvArgs& a, int tile, int rows, const ActLds<FMT
   }
 }
 
+// One 32-row weight tile of a launch: block dots over the activations
+// already quantized in L, wave partials added in wave order, epilogue.
 template <int FMT, int RB, int NW, int EPI>
-__global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(GemvArgs a, int rows) {
-  extern __shared__ __attribute__((aligned(16))) char dsm[];
+__device__ void q8_tile(const GemvArgs& a, int tile, int rows, const ActLds<FMT, RB, NW>& L) {
   constexpr int NM = EPI == EPI_SWIGLU ? 2 : 1;
   constexpr int NI = FMT == FMT_Q6K ? 2 : 1;  // output rows per lane
-  ActLds<FMT, RB, NW> L(dsm, a.n_in);
-  quantize_rows<FMT, RB, NW>(reinterpret_cast<const float*>(a.x), a.ldx, rows, a.n_in, L);
-  __syncthreads();
-  const int tile = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   float acc[NM][RB][NI];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
@@ -434,6 +434,35 @@ __global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(GemvArgs a, int rows) 
     if constexpr (EPI == EPI_STORE) a.y[o] = v[0];
     if constexpr (EPI == EPI_RES) a.y[o] = a.res[(size_t)r * a.ldres + n] + v[0];
     if constexpr (EPI == EPI_SWIGLU) a.y[o] = silu_f(v[0]) * v[NM - 1];
+  }
+}
+
+template <int FMT, int RB, int NW, int EPI>
+__global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(GemvArgs a, int rows) {
+  extern __shared__ __attribute__((aligned(16))) char dsm[];
+  ActLds<FMT, RB, NW> L(dsm, a.n_in);
+  quantize_rows<FMT, RB, NW>(reinterpret_cast<const float*>(a.x), a.ldx, rows, a.n_in, L);
+  __syncthreads();
+  q8_tile<FMT, RB, NW, EPI>(a, blockIdx.x, rows, L);
+}
+
+// Two matrices of one input (the attention's stacked q|k and v, whose formats
+// differ in Q4_K_M files) in one launch: both formats take the same
+// activation type, quantized once per workgroup; workgroups [0, split) run
+// tiles of a, the rest tiles of b. Every tile's arithmetic is that of its own
+// single-matrix launch.
+template <int FMT, int FMT2, int RB, int NW>
+__global__ __launch_bounds__(64 * NW) void q8_pair_kernel(GemvArgs a, GemvArgs b, int split, int rows) {
+  static_assert(ActLds<FMT, RB, NW>::K256 == ActLds<FMT2, RB, NW>::K256, "one activation type");
+  extern __shared__ __attribute__((aligned(16))) char dsm[];
+  ActLds<FMT, RB, NW> L(dsm, a.n_in);
+  quantize_rows<FMT, RB, NW>(reinterpret_cast<const float*>(a.x), a.ldx, rows, a.n_in, L);
+  __syncthreads();
+  if ((int)blockIdx.x < split) {
+    q8_tile<FMT, RB, NW, EPI_STORE>(a, blockIdx.x, rows, L);
+  } else {
+    const ActLds<FMT2, RB, NW> L2(dsm, a.n_in);
+    q8_tile<FMT2, RB, NW, EPI_STORE>(b, blockIdx.x - split, rows, L2);
   }
 }
 
@@ -491,7 +520,70 @@ void dispatch(int fmt, const GemvArgs& a, int nrows, hipStream_t s) {
   throw Error{kErrFormat, "quantized-activation GEMV takes Q4_K, Q6_K, Q8_0 or Q5_0 matrices"};
 }
 
+template <int FMT, int FMT2, int RB, int NW>
+void launch_pair_q8(GemvArgs a, GemvArgs b, int nrows, hipStream_t s) {
+  const size_t l1 = ActLds<FMT, RB, NW>::bytes(a.n_in, 1), l2 = ActLds<FMT2, RB, NW>::bytes(a.n_in, 1);
+  const size_t lds = l1 > l2 ? l1 : l2;
+  PGD_CHECK(lds <= 160 * 1024, kErrShape, "activation rows too wide for the quantized-activation GEMV");
+  if (lds > 64 * 1024) {
+    static bool set = false;
+    if (!set) {
+      PGD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_pair_kernel<FMT, FMT2, RB, NW>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      set = true;
+    }
+  }
+  const int ta = (a.n_out + 31) / 32, tb = (b.n_out + 31) / 32;
+  for (int r0 = 0; r0 < nrows; r0 += RB) {
+    const int rows = min(RB, nrows - r0);
+    hipLaunchKernelGGL((q8_pair_kernel<FMT, FMT2, RB, NW>), dim3(ta + tb), dim3(64 * NW), lds, s, a, b, ta, rows);
+    PGD_HIP(hipGetLastError());
+    a.x = reinterpret_cast<const float*>(a.x) + (size_t)rows * a.ldx;
+    a.y += (size_t)rows * a.ldy;
+    b.y += (size_t)rows * b.ldy;
+  }
+}
+
+// the waves and rows per launch of launch_waves / launch_rows (shared by both
+// matrices: they have the same K)
+template <int FMT, int FMT2>
+void pair_rows(const GemvArgs& a, const GemvArgs& b, int nrows, hipStream_t s) {
+  const int kb = (FMT == FMT_Q4K || FMT == FMT_Q6K) ? a.nsb : a.n_in / 128;
+  auto go = [&](auto rb) {
+    constexpr int RB = decltype(rb)::value;
+    if (kb <= 4) return launch_pair_q8<FMT, FMT2, RB, 4>(a, b, nrows, s);
+    if (kb <= 8) return launch_pair_q8<FMT, FMT2, RB, 8>(a, b, nrows, s);
+    launch_pair_q8<FMT, FMT2, RB, 16>(a, b, nrows, s);
+  };
+  if (nrows == 1) return go(std::integral_constant<int, 1>{});
+  if (nrows <= 4) return go(std::integral_constant<int, 4>{});
+  if (nrows <= 8) return go(std::integral_constant<int, 8>{});
+  go(std::integral_constant<int, 16>{});
+}
+
 }  // namespace
+
+bool q8act_pair_ok(int fmt_a, int fmt_b) {
+  auto k256 = [](int f) { return f == FMT_Q4K || f == FMT_Q6K; };
+  auto b32 = [](int f) { return f == FMT_Q8_0 || f == FMT_Q5_0; };
+  return (k256(fmt_a) && k256(fmt_b)) || (b32(fmt_a) && b32(fmt_b));
+}
+
+void run_q8act_pair(int fmt_a, const GemvArgs& a, int fmt_b, const GemvArgs& b, int nrows, hipStream_t s) {
+  PGD_CHECK(a.n_in == b.n_in, kErrShape, "paired GEMVs need one input width");
+  PGD_CHECK(q8act_pair_ok(fmt_a, fmt_b), kErrFormat, "paired GEMVs need one activation type");
+#define PGD_PAIR(F1, F2) \
+  if (fmt_a == F1 && fmt_b == F2) return pair_rows<F1, F2>(a, b, nrows, s);
+  PGD_PAIR(FMT_Q4K, FMT_Q4K)
+  PGD_PAIR(FMT_Q4K, FMT_Q6K)
+  PGD_PAIR(FMT_Q6K, FMT_Q4K)
+  PGD_PAIR(FMT_Q6K, FMT_Q6K)
+  PGD_PAIR(FMT_Q8_0, FMT_Q8_0)
+  PGD_PAIR(FMT_Q8_0, FMT_Q5_0)
+  PGD_PAIR(FMT_Q5_0, FMT_Q8_0)
+  PGD_PAIR(FMT_Q5_0, FMT_Q5_0)
+#undef PGD_PAIR
+}
 
 void run_q8act(int fmt, const GemvArgs& a, int nrows, int epi, hipStream_t s) {
   if (epi == EPI_SWIGLU) dispatch<EPI_SWIGLU>(fmt, a, nrows, s);

@@ -529,13 +529,19 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     } else {
       rmsnorm_rows(w.x, H, nullptr, rows, H, L.in_norm, eps, norm_mode, w.xn, H, st);
       // q | k | v side by side in A (q and k from one stacked launch when they share a format)
-      if (L.proj.base) {
-        gemv(L.proj, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
+      float* yv = w.A + m.q_out + m.kv_width;
+      if (L.proj.base && m.q8act && qmat_q8act_pairable(L.proj, L.v)) {
+        // stacked q|k and v in one launch (one activation quantization)
+        qmat_gemv_q8act_pair(L.proj, w.A, L.v, yv, w.xn, H, rows, (int)w.lda, st);
       } else {
-        gemv(L.q, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
-        gemv(L.k, w.xn, H, rows, w.A + m.q_out, (int)w.lda, nullptr, 0);
+        if (L.proj.base) {
+          gemv(L.proj, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
+        } else {
+          gemv(L.q, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
+          gemv(L.k, w.xn, H, rows, w.A + m.q_out, (int)w.lda, nullptr, 0);
+        }
+        gemv(L.v, w.xn, H, rows, yv, (int)w.lda, nullptr, 0);
       }
-      gemv(L.v, w.xn, H, rows, w.A + m.q_out + m.kv_width, (int)w.lda, nullptr, 0);
       q_raw = w.A;
       k_raw = w.A + m.q_out;
       v_raw = w.A + m.q_out + m.kv_width;

@@ -125,6 +125,12 @@ void qmat_gemv_q8act(const QMat& m, const float* x, int ldx, int nrows, float* y
                      hipStream_t s);
 void qmat_gemv_swiglu_q8act(const QMat& gate, const QMat& up, const float* x, int ldx, int nrows, float* mid, int ldm,
                             hipStream_t s);
+// qmat_gemv_q8act of two matrices over the same input rows in one launch
+// (ya = A.x, yb = B.x, both with row stride ldy), bit-equal to two calls;
+// qmat_q8act_pairable says whether two matrices can share a launch.
+bool qmat_q8act_pairable(const QMat& a, const QMat& b);
+void qmat_gemv_q8act_pair(const QMat& a, float* ya, const QMat& b, float* yb, const float* x, int ldx, int nrows,
+                          int ldy, hipStream_t s);
 
 // fused SwiGLU: mid[r, n] = silu(gate.x) * (up.x)
 void qmat_gemv_swiglu(const QMat& gate, const QMat& up, const float* x, int ldx, int nrows, float* mid,

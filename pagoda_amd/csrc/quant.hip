@@ -670,6 +670,23 @@ void qmat_gemv_q8act(const QMat& m, const float* x, int ldx, int nrows, float* y
   run_q8act(m.fmt, a, nrows, res ? EPI_RES : EPI_STORE, s);
 }
 
+bool qmat_q8act_pairable(const QMat& a, const QMat& b) {
+  return a.n_in == b.n_in && gemv::q8act_pair_ok(a.fmt, b.fmt);
+}
+
+void qmat_gemv_q8act_pair(const QMat& a, float* ya, const QMat& b, float* yb, const float* x, int ldx, int nrows,
+                          int ldy, hipStream_t s) {
+  PGD_CHECK(nrows >= 0 && ldx >= a.n_in && ldy >= a.n_out && ldy >= b.n_out, kErrShape, "gemv rows / strides");
+  if (nrows == 0) return;
+  GemvArgs ga = make_args(a), gb = make_args(b);
+  ga.x = gb.x = x;
+  ga.ldx = gb.ldx = ldx;
+  ga.y = ya;
+  gb.y = yb;
+  ga.ldy = gb.ldy = ldy;
+  run_q8act_pair(a.fmt, ga, b.fmt, gb, nrows, s);
+}
+
 void qmat_gemv_swiglu_q8act(const QMat& gate, const QMat& up, const float* x, int ldx, int nrows, float* mid, int ldm,
                             hipStream_t s) {
   PGD_CHECK(gate.fmt == up.fmt && gate.n_out == up.n_out && gate.n_in == up.n_in, kErrShape,

@@ -104,6 +104,12 @@ class Matrix:
         call("pgd_matrix_gemv_q8act_dev", self.handle, C.c_void_p(x_ptr), ldx, nrows, C.c_void_p(y_ptr), ldy,
              C.c_void_p(res_ptr or None), ldres)
 
+    def gemv_q8act_pair_dev(self, ya_ptr: int, other: "Matrix", yb_ptr: int, x_ptr: int, ldx: int, nrows: int,
+                            ldy: int) -> None:
+        """This matrix and `other` over the same rows in one launch (candle's CPU arithmetic)."""
+        call("pgd_matrix_gemv_q8act_pair_dev", self.handle, C.c_void_p(ya_ptr), other.handle, C.c_void_p(yb_ptr),
+             C.c_void_p(x_ptr), ldx, nrows, ldy)
+
     def gemv_act_dev(self, act_ptr: int, nrows: int, y_ptr: int, ldy: int, res_ptr: int = 0, ldres: int = 0) -> None:
         call("pgd_matrix_gemv_act_dev", self.handle, C.c_void_p(act_ptr), nrows, C.c_void_p(y_ptr), ldy,
              C.c_void_p(res_ptr or None), ldres)

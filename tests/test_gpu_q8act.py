@@ -81,6 +81,52 @@ def test_q8act_gemv_matches_oracle(dev, fmt, shape):
     m.free()
 
 
+@pytest.mark.parametrize("fa,fb", [(1, 2), (2, 1), (3, 4)])
+def test_q8act_pair_equals_two_launches(dev, fa, fb):
+    """Two matrices over one input in one launch (the attention's stacked
+    q|k and v): each output bit-equal to its own launch, at 1, 4 and 9 rows
+    (1-, 4- and 16-row launches), with a row stride wider than either."""
+    n_in, na, nb = 896, 1024, 128
+    if fa == 3:
+        na = 1000  # a partly filled last tile
+    ma, _ = make(dev, fa, na, n_in, 11 * fa)
+    mb, _ = make(dev, fb, nb, n_in, 13 * fb)
+    rng = np.random.default_rng(fa * 10 + fb)
+    x = rng.normal(0, 1, (9, n_in)).astype(np.float32)
+    xd = dev.upload(x)
+    ld = na + nb + 16
+    for rows in (1, 4, 9):
+        ys, ya, yb = dev.alloc(rows * ld * 4), dev.alloc(rows * na * 4), dev.alloc(rows * nb * 4)
+        ma.gemv_q8act_pair_dev(ys, mb, ys + na * 4, xd, n_in, rows, ld)
+        ma.gemv_q8act_dev(xd, n_in, rows, ya, na)
+        mb.gemv_q8act_dev(xd, n_in, rows, yb, nb)
+        got = dev.download(ys, (rows, ld), np.float32)
+        a = dev.download(ya, (rows, na), np.float32)
+        b = dev.download(yb, (rows, nb), np.float32)
+        np.testing.assert_array_equal(got[:, :na].view(np.uint32), a.view(np.uint32), err_msg=f"a rows={rows}")
+        np.testing.assert_array_equal(got[:, na:na + nb].view(np.uint32), b.view(np.uint32), err_msg=f"b rows={rows}")
+        for p in (ys, ya, yb):
+            dev.free(p)
+    dev.free(xd)
+    ma.free()
+    mb.free()
+
+
+def test_q8act_pair_rejects_mixed_activation_types(dev):
+    from pagoda_amd import PagodaError
+
+    ma, _ = make(dev, 1, 64, 256, 1)
+    mb, _ = make(dev, 3, 64, 256, 2)
+    xd = dev.upload(np.ones((1, 256), np.float32))
+    yd = dev.alloc(128 * 4)
+    with pytest.raises(PagodaError):
+        ma.gemv_q8act_pair_dev(yd, mb, yd + 256, xd, 256, 1, 128)
+    for p in (xd, yd):
+        dev.free(p)
+    ma.free()
+    mb.free()
+
+
 def test_q8act_rejects_a8(dev):
     from pagoda_amd import Matrix, PagodaError
 
