@@ -383,6 +383,43 @@ __device__ void dots_q32(const GemvArgs& a, int tile, int rows, const ActLds<FMT
   }
 }
 
+// Touch one dword of every 128-byte line of [base, base + bytes) across the
+// workgroup: the tile's weights are on their way into the cache while the
+// activations are quantized (the loads' values only feed `sink`).
+__device__ inline void touch(const uint8_t* base, size_t bytes, int nthreads, uint32_t& sink) {
+  for (size_t off = (size_t)threadIdx.x * 128; off < bytes; off += (size_t)nthreads * 128)
+    sink ^= *reinterpret_cast<const uint32_t*>(base + off);
+}
+
+template <int FMT>
+__device__ inline void prefetch_tile(const GemvArgs& a, bool second, int tile, int nthreads, uint32_t& sink) {
+  const uint8_t* p0 = second ? a.u0 : a.p0;
+  const uint8_t* p1 = second ? a.u1 : a.p1;
+  const uint8_t* p2 = second ? a.u2 : a.p2;
+  const uint8_t* p3 = second ? a.u3 : a.p3;
+  const size_t nsb = (size_t)a.nsb, t = (size_t)tile;
+  if constexpr (FMT == FMT_Q4K) {
+    touch(p0 + t * 4 * nsb * 1024, 4 * nsb * 1024, nthreads, sink);
+    touch(p1 + t * nsb * 512, nsb * 512, nthreads, sink);
+  } else if constexpr (FMT == FMT_Q6K) {
+    touch(p0 + t * 2 * nsb * 2048, 2 * nsb * 2048, nthreads, sink);
+    touch(p1 + t * 2 * nsb * 1024, 2 * nsb * 1024, nthreads, sink);
+    touch(p2 + t * 2 * nsb * 256, 2 * nsb * 256, nthreads, sink);
+    touch(p3 + t * nsb * 64, nsb * 64, nthreads, sink);
+  } else {
+    // row-major planes: the tile's rows
+    const size_t r0 = t * 32, nr = (size_t)min(32, a.n_out - tile * 32), nb = (size_t)(a.n_in / 32);
+    if constexpr (FMT == FMT_Q8_0) {
+      touch(p0 + r0 * a.n_in, nr * a.n_in, nthreads, sink);
+      touch(p1 + r0 * nb * 2, nr * nb * 2, nthreads, sink);
+    } else {
+      touch(p0 + r0 * (a.n_in / 2), nr * (a.n_in / 2), nthreads, sink);
+      touch(p1 + r0 * nb * 4, nr * nb * 4, nthreads, sink);
+      touch(p2 + r0 * nb * 2, nr * nb * 2, nthreads, sink);
+    }
+  }
+}
+
 // One 32-row weight tile of a launch: block dots over the activations
 // already quantized in L, wave partials added in wave order, epilogue.
 template <int FMT, int RB, int NW, int EPI>
@@ -437,13 +474,27 @@ __device__ void q8_tile(const GemvArgs& a, int tile, int rows, const ActLds<FMT,
   }
 }
 
+// the prefetch loads' values are never used: a store no launch can reach keeps them
+__device__ inline void keep(const GemvArgs& a, int rows, uint32_t sink) {
+  if (rows < 0 && sink == 0x9e3779b9u) a.y[0] = 0.0f;
+}
+
 template <int FMT, int RB, int NW, int EPI>
 __global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(GemvArgs a, int rows) {
   extern __shared__ __attribute__((aligned(16))) char dsm[];
+  // long rows (a wave walks several K blocks): the tile's later blocks are in
+  // the cache by the time the wave reaches them (measured: the 4864-wide down
+  // projection 13.2 -> 11.0 us for Q6_K; tiles of one block per wave lost)
+  uint32_t sink = 0;
+  if constexpr (NW == 16) {
+    prefetch_tile<FMT>(a, false, blockIdx.x, 64 * NW, sink);
+    if constexpr (EPI == EPI_SWIGLU) prefetch_tile<FMT>(a, true, blockIdx.x, 64 * NW, sink);
+  }
   ActLds<FMT, RB, NW> L(dsm, a.n_in);
   quantize_rows<FMT, RB, NW>(reinterpret_cast<const float*>(a.x), a.ldx, rows, a.n_in, L);
   __syncthreads();
   q8_tile<FMT, RB, NW, EPI>(a, blockIdx.x, rows, L);
+  keep(a, rows, sink);
 }
 
 // Two matrices of one input (the attention's stacked q|k and v, whose formats
@@ -455,15 +506,22 @@ template <int FMT, int FMT2, int RB, int NW>
 __global__ __launch_bounds__(64 * NW) void q8_pair_kernel(GemvArgs a, GemvArgs b, int split, int rows) {
   static_assert(ActLds<FMT, RB, NW>::K256 == ActLds<FMT2, RB, NW>::K256, "one activation type");
   extern __shared__ __attribute__((aligned(16))) char dsm[];
+  const bool first = (int)blockIdx.x < split;
+  uint32_t sink = 0;
+  if constexpr (NW == 16) {
+    if (first) prefetch_tile<FMT>(a, false, blockIdx.x, 64 * NW, sink);
+    else prefetch_tile<FMT2>(b, false, blockIdx.x - split, 64 * NW, sink);
+  }
   ActLds<FMT, RB, NW> L(dsm, a.n_in);
   quantize_rows<FMT, RB, NW>(reinterpret_cast<const float*>(a.x), a.ldx, rows, a.n_in, L);
   __syncthreads();
-  if ((int)blockIdx.x < split) {
+  if (first) {
     q8_tile<FMT, RB, NW, EPI_STORE>(a, blockIdx.x, rows, L);
   } else {
     const ActLds<FMT2, RB, NW> L2(dsm, a.n_in);
     q8_tile<FMT2, RB, NW, EPI_STORE>(b, blockIdx.x - split, rows, L2);
   }
+  keep(a, rows, sink);
 }
 
 template <int FMT, int RB, int NW, int EPI>
