@@ -232,6 +232,17 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
   const size_t coff = ((size_t)(cbt / 2) * G * 128 + (cbt % 2) * 64 + (cw < 16 ? cw : cw + 16)) * 4;
   const uint32_t xoff = (tid % (Gm::XU4 / Gm::NC)) * 16, soff = j * 4;
   auto load_unit = [&](int b, int g, WR& r) {
+    // the operands first: they are published one unit before use, and the
+    // loads retire in issue order, so waiting for them leaves the unit's
+    // weights in flight
+    // items 2g, 2g + 1 (both batch tiles) are contiguous: 512 u4 + 128 floats per
+    // group; chunk c of a two-chunk launch starts c G groups on
+#pragma unroll
+    for (int c = 0; c < Gm::NC; ++c)
+      r.x[c] = *reinterpret_cast<const u4*>(reinterpret_cast<const uint8_t*>(XA + ((size_t)c * G + g) * 512) + xoff);
+    const float* cp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(CA + (size_t)g * 128) + coff);
+    r.c[0] = cp[0];
+    r.c[1] = cp[16];
 #pragma unroll
     for (int st = 0; st < NS; ++st) {
       // missing tiles re-read the last one
@@ -242,14 +253,6 @@ __global__ __launch_bounds__(64 * kWaves) void a8_sk_kernel(GemvArgs a, const ui
       r.w[st] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(pc + woff0));
       r.s[st] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(ps + soff));
     }
-    // items 2g, 2g + 1 (both batch tiles) are contiguous: 512 u4 + 128 floats per
-    // group; chunk c of a two-chunk launch starts c G groups on
-#pragma unroll
-    for (int c = 0; c < Gm::NC; ++c)
-      r.x[c] = *reinterpret_cast<const u4*>(reinterpret_cast<const uint8_t*>(XA + ((size_t)c * G + g) * 512) + xoff);
-    const float* cp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(CA + (size_t)g * 128) + coff);
-    r.c[0] = cp[0];
-    r.c[1] = cp[16];
   };
   // operand ring: unit u in slot u & 1
   auto store_x = [&](int slot, const WR& r) {
