@@ -387,7 +387,7 @@ __device__ void dots_q32(const GemvArgs& a, int tile, int rows, const ActLds<FMT
 // workgroup: the tile's weights are on their way into the cache while the
 // activations are quantized (the loads' values only feed `sink`).
 __device__ inline void touch(const uint8_t* base, size_t bytes, int nthreads, uint32_t& sink) {
-  for (size_t off = (size_t)threadIdx.x * 128; off < bytes; off += (size_t)nthreads * 128)
+  for (size_t off = (size_t)threadIdx.x * 128; off + 4 <= bytes; off += (size_t)nthreads * 128)
     sink ^= *reinterpret_cast<const uint32_t*>(base + off);
 }
 
