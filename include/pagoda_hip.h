@@ -289,6 +289,37 @@ int pgd_set_kv_wire_f16(int on);
  * (the trait's default None, lib.rs:224). */
 int pgd_session_fork_prefix(const pgd_session* s, int n, pgd_session** out);
 
+/* ---- engine-addressable KV pages ------------------------------------------
+ * The engine's PagedKvCache hands out physical BlockIds with reference counts
+ * and copy-on-write, "exactly what a tensor-backed implementation would swap
+ * in" (pagoda/src/kv_cache.rs:1-8, alloc/inc_ref/dec_ref/ref_count 65-105),
+ * and its RadixCache maps each cached token to a KvSlot = (BlockId, offset)
+ * (pagoda/src/radix_cache.rs:17-18). A page id here names one page of
+ * kv_block positions in every full-attention layer's K and V pools; position
+ * p of a session lives in slot p % kv_block of its page p / kv_block.
+ * Sessions and the engine hold references alike; a page returns to the pool
+ * when its count reaches zero, and a session copies a shared, partly filled
+ * page before its first write into it. */
+/* PagedKvCache::num_blocks / block_size / num_free_blocks (kv_cache.rs:48-56);
+ * each output nullable. */
+int pgd_model_kv_pool(const pgd_model* m, int* n_pages, int* page_tokens, int* n_free);
+/* The page ids holding positions [0, len) of s, in position order. *n gets
+ * the count (ids = NULL queries it); cap below it is PGD_ERR_ARG. */
+int pgd_session_pages(const pgd_session* s, int32_t* ids, int cap, int* n);
+/* PagedKvCache::inc_ref / dec_ref (kv_cache.rs:90-105) on n held pages (a free
+ * page or an id outside the pool is an error and changes nothing). */
+int pgd_page_retain(pgd_model* m, const int32_t* ids, int n);
+int pgd_page_release(pgd_model* m, const int32_t* ids, int n);
+/* PagedKvCache::ref_count (kv_cache.rs:74). */
+int pgd_page_refcount(const pgd_model* m, int32_t id, int* count);
+/* A new session of length n_pos whose KV is the held pages ids[0..n_pages)
+ * (n_pages = ceil(n_pos / kv_block), distinct): the radix cache's matched
+ * slots become the session's cache without a copy; the session takes its own
+ * reference on each page. No cached logits (as a graft, lib.rs:603-616).
+ * PGD_ERR_STATE for the hybrid model, whose recurrent state is not a
+ * function of KV pages (cache_prefix default None, lib.rs:224). */
+int pgd_session_from_pages(pgd_model* m, const int32_t* ids, int n_pages, int n_pos, pgd_session** out);
+
 #ifdef __cplusplus
 }
 #endif

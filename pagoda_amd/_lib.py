@@ -65,6 +65,12 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_session_fork": (c_int, [c_void_p, P(c_void_p)]),
     "pgd_session_fork_prefix": (c_int, [c_void_p, c_int, P(c_void_p)]),
     "pgd_set_kv_wire_f16": (c_int, [c_int]),
+    "pgd_model_kv_pool": (c_int, [c_void_p, P(c_int), P(c_int), P(c_int)]),
+    "pgd_session_pages": (c_int, [c_void_p, c_void_p, c_int, P(c_int)]),
+    "pgd_page_retain": (c_int, [c_void_p, c_void_p, c_int]),
+    "pgd_page_release": (c_int, [c_void_p, c_void_p, c_int]),
+    "pgd_page_refcount": (c_int, [c_void_p, C.c_int32, P(c_int)]),
+    "pgd_session_from_pages": (c_int, [c_void_p, c_void_p, c_int, c_int, P(c_void_p)]),
     "pgd_session_free": (c_int, [c_void_p]),
     "pgd_session_len": (c_int, [c_void_p, P(c_int)]),
     "pgd_forward": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),

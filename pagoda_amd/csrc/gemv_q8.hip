@@ -557,14 +557,25 @@ void launch_waves(const GemvArgs& a, int nrows, hipStream_t s) {
   launch_q8<FMT, RB, 16, EPI>(a, nrows, s);
 }
 
+// LDS of one launch of RB rows: the quantized rows, or the wave partials of
+// the widest (16-wave) workgroup, whichever is larger
+template <int FMT, int RB>
+size_t lds_need(int n_in, int nm) {
+  return ActLds<FMT, RB, 16>::bytes(n_in, nm);
+}
+
 // rows per launch: decode steps take 1..8; prefills 16 at a time (weights
-// read once per 16 rows)
+// read once per 16 rows). Wide rows whose RB quantized rows do not fit the
+// 160 KiB of LDS take fewer rows per launch (the per-row arithmetic does not
+// depend on RB, so the results are the same).
 template <int FMT, int EPI>
 void launch_rows(const GemvArgs& a, int nrows, hipStream_t s) {
-  if (nrows == 1) return launch_waves<FMT, 1, EPI>(a, nrows, s);
-  if (nrows <= 4) return launch_waves<FMT, 4, EPI>(a, nrows, s);
-  if (nrows <= 8) return launch_waves<FMT, 8, EPI>(a, nrows, s);
-  launch_waves<FMT, 16, EPI>(a, nrows, s);
+  const int nm = EPI == EPI_SWIGLU ? 2 : 1;
+  const size_t cap = 160 * 1024;
+  if (nrows > 8 && lds_need<FMT, 16>(a.n_in, nm) <= cap) return launch_waves<FMT, 16, EPI>(a, nrows, s);
+  if (nrows > 4 && lds_need<FMT, 8>(a.n_in, nm) <= cap) return launch_waves<FMT, 8, EPI>(a, nrows, s);
+  if (nrows > 1 && lds_need<FMT, 4>(a.n_in, nm) <= cap) return launch_waves<FMT, 4, EPI>(a, nrows, s);
+  launch_waves<FMT, 1, EPI>(a, nrows, s);
 }
 
 template <int EPI>
@@ -613,10 +624,15 @@ void pair_rows(const GemvArgs& a, const GemvArgs& b, int nrows, hipStream_t s) {
     if (kb <= 8) return launch_pair_q8<FMT, FMT2, RB, 8>(a, b, nrows, s);
     launch_pair_q8<FMT, FMT2, RB, 16>(a, b, nrows, s);
   };
-  if (nrows == 1) return go(std::integral_constant<int, 1>{});
-  if (nrows <= 4) return go(std::integral_constant<int, 4>{});
-  if (nrows <= 8) return go(std::integral_constant<int, 8>{});
-  go(std::integral_constant<int, 16>{});
+  const size_t cap = 160 * 1024;
+  auto fits = [&](auto rb) {
+    constexpr int RB = decltype(rb)::value;
+    return lds_need<FMT, RB>(a.n_in, 1) <= cap && lds_need<FMT2, RB>(a.n_in, 1) <= cap;
+  };
+  if (nrows > 8 && fits(std::integral_constant<int, 16>{})) return go(std::integral_constant<int, 16>{});
+  if (nrows > 4 && fits(std::integral_constant<int, 8>{})) return go(std::integral_constant<int, 8>{});
+  if (nrows > 1 && fits(std::integral_constant<int, 4>{})) return go(std::integral_constant<int, 4>{});
+  go(std::integral_constant<int, 1>{});
 }
 
 }  // namespace

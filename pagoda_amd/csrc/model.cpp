@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstring>
 #include <string>
+#include <unordered_map>
 #include <unordered_set>
 
 #include "common.h"
@@ -353,10 +354,13 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   // state half-advanced, so the sessions are marked unusable instead of
   // silently continuing from it (a batched step commits all or nothing,
   // pagoda-hf/src/llama.rs:750-778).
+  // Armed just before the first kernel that writes session state, so that a
+  // capacity or allocation error before it (page pool, rope tables,
+  // workspace, metadata buffers) leaves every session usable.
   struct PoisonOnThrow {
     Session* const* s;
     int n;
-    bool armed = true;
+    bool armed = false;
     ~PoisonOnThrow() {
       if (armed)
         for (int i = 0; i < n; ++i) s[i]->poisoned = true;
@@ -373,17 +377,22 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     for (int i = 0; i < nseq; ++i) {
       const Session* s = sess[i];
       size_t want = (size_t)(s->len + n[i] + c.kv_block - 1) / c.kv_block;
-      need += want - s->blocks.size();
-      if (s->len % c.kv_block && m.refcount[s->blocks.back()] > 1) need += 1;
+      // a step that failed after this allocation may have left pages past len
+      if (want > s->blocks.size()) need += want - s->blocks.size();
+      // the partly filled page holding position len, when another holder shares it
+      if (s->len % c.kv_block && m.refcount[s->blocks[s->len / c.kv_block]] > 1) need += 1;
     }
     PGD_CHECK(need <= m.free_blocks.size(), kErrAlloc, "KV page pool exhausted");
     for (int i = 0; i < nseq; ++i) {
       Session* s = sess[i];
-      if (s->len % c.kv_block && m.refcount[s->blocks.back()] > 1) {
-        int nb = m.alloc_block();
-        m.copy_block(nb, s->blocks.back());
-        m.release_block(s->blocks.back());
-        s->blocks.back() = nb;
+      if (s->len % c.kv_block) {
+        int& tail = s->blocks[s->len / c.kv_block];
+        if (m.refcount[tail] > 1) {
+          int nb = m.alloc_block();
+          m.copy_block(nb, tail);
+          m.release_block(tail);
+          tail = nb;
+        }
       }
       size_t want = (size_t)(s->len + n[i] + c.kv_block - 1) / c.kv_block;
       while (s->blocks.size() < want) s->blocks.push_back(m.alloc_block());
@@ -494,6 +503,21 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
   const int H = c.hidden;
   const int norm_mode = c.arch == PGD_ARCH_QWEN35 ? 0 : m.q8act ? 2 : 1;
   const float eps = c.arch == PGD_ARCH_QWEN35 ? 1e-6f : c.eps;
+  // step outputs: ids, max values, non-finite counts
+  size_t out_bytes = (size_t)lrows * 12;
+  if (m.out_dev.bytes < out_bytes) {
+    PGD_HIP(hipStreamSynchronize(st));
+    m.out_dev = DevBuf(out_bytes * 2);
+  }
+  if (m.out_host_cap < out_bytes) {
+    PGD_HIP(hipStreamSynchronize(st));
+    if (m.out_host) PGD_HIP(hipHostFree(m.out_host));
+    m.out_host = nullptr;
+    m.out_host_cap = 0;
+    PGD_HIP(hipHostMalloc(&m.out_host, out_bytes * 2));
+    m.out_host_cap = out_bytes * 2;
+  }
+  poison.armed = true;
   qmat_embed(m.embed, d_tok, rows, w.x, H, st);
   const size_t per_lin = m.conv_floats + m.state_floats;
   const bool hybrid = c.arch == PGD_ARCH_QWEN35;
@@ -634,13 +658,6 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     rmsnorm_rows(w.x, H, d_lr, lrows, H, m.final_norm, eps, norm_mode, w.xn, H, st);
     gemv(m.head, w.xn, H, lrows, w.logits, c.vocab, nullptr, 0);
   }
-  size_t out_bytes = (size_t)lrows * 12;
-  if (m.out_dev.bytes < out_bytes) m.out_dev = DevBuf(out_bytes * 2);
-  if (m.out_host_cap < out_bytes) {
-    if (m.out_host) PGD_HIP(hipHostFree(m.out_host));
-    PGD_HIP(hipHostMalloc(&m.out_host, out_bytes * 2));
-    m.out_host_cap = out_bytes * 2;
-  }
   uint32_t* d_ids = m.out_dev.as<uint32_t>();
   float* d_vals = (float*)(d_ids + lrows);
   int* d_nf = (int*)(d_vals + lrows);
@@ -757,8 +774,11 @@ int pgd_session_fork(const pgd_session* ps, pgd_session** out) {
     held->s.model = &m;
     m.live_sessions++;
     held->s.len = s.len;
-    held->s.blocks = s.blocks;
-    for (int b : s.blocks) m.refcount[b]++;
+    // only the pages holding positions [0, len): a failed step may have left
+    // pages past them, which stay the parent's own
+    const size_t used = ((size_t)s.len + m.cfg.kv_block - 1) / m.cfg.kv_block;
+    held->s.blocks.assign(s.blocks.begin(), s.blocks.begin() + std::min(used, s.blocks.size()));
+    for (int b : held->s.blocks) m.refcount[b]++;
     held->s.last_logits = s.last_logits;
     held->s.has_logits = s.has_logits;
     if (m.rec_floats) {
@@ -797,6 +817,120 @@ int pgd_session_fork_prefix(const pgd_session* ps, int n, pgd_session** out) {
     // its slots at or past n are never read before they are rewritten
     const size_t keep = ((size_t)n + m.cfg.kv_block - 1) / m.cfg.kv_block;
     held->s.blocks.assign(s.blocks.begin(), s.blocks.begin() + keep);
+    for (int b : held->s.blocks) m.refcount[b]++;
+    *out = held;
+  });
+  if (rc && held) delete held;
+  return rc;
+}
+
+// ---- engine-addressable KV pages ----
+// The engine's paged cache hands out physical block ids with reference counts
+// and copy-on-write (pagoda/src/kv_cache.rs:1-8, 65-125); its radix cache maps
+// each cached token to a (block, offset) slot (pagoda/src/radix_cache.rs:17-18).
+// These entry points expose this backend's KV pages under the same scheme: a
+// page id names the same page in every full-attention layer's K and V pools.
+
+int pgd_model_kv_pool(const pgd_model* pm, int* n_pages, int* page_tokens, int* n_free) {
+  return guard([&] {
+    PGD_CHECK(pm, kErrArg, "null argument");
+    const Model& m = pm->m;
+    if (n_pages) *n_pages = (int)m.refcount.size();
+    if (page_tokens) *page_tokens = m.cfg.kv_block;
+    if (n_free) *n_free = (int)m.free_blocks.size();
+  });
+}
+
+int pgd_session_pages(const pgd_session* ps, int32_t* ids, int cap, int* n) {
+  return guard([&] {
+    PGD_CHECK(ps && n, kErrArg, "null argument");
+    const Session& s = ps->s;
+    PGD_CHECK(!s.poisoned, kErrState, "session state is undefined after a failed step");
+    const Model& m = *s.model;
+    PGD_CHECK(m.n_full > 0, kErrState, "model has no KV pages");
+    // a failed step may have allocated pages past len: only the ones holding
+    // positions [0, len) are the session's KV
+    const int used = (s.len + m.cfg.kv_block - 1) / m.cfg.kv_block;
+    *n = used;
+    if (!ids) return;
+    PGD_CHECK(cap >= used, kErrArg, "page id buffer holds " + std::to_string(cap) + " of " + std::to_string(used));
+    for (int i = 0; i < used; ++i) ids[i] = s.blocks[i];
+  });
+}
+
+namespace {
+void check_held_pages(const Model& m, const int32_t* ids, int n) {
+  PGD_CHECK(n >= 0 && (n == 0 || ids), kErrArg, "bad page list");
+  for (int i = 0; i < n; ++i) {
+    PGD_CHECK(ids[i] >= 0 && ids[i] < (int)m.refcount.size(), kErrArg,
+              "page id " + std::to_string(ids[i]) + " outside the pool");
+    PGD_CHECK(m.refcount[ids[i]] > 0, kErrState, "page " + std::to_string(ids[i]) + " is free");
+  }
+}
+}  // namespace
+
+int pgd_page_retain(pgd_model* pm, const int32_t* ids, int n) {
+  return guard([&] {
+    PGD_CHECK(pm, kErrArg, "null argument");
+    Model& m = pm->m;
+    check_held_pages(m, ids, n);
+    for (int i = 0; i < n; ++i) m.refcount[ids[i]]++;
+  });
+}
+
+int pgd_page_release(pgd_model* pm, const int32_t* ids, int n) {
+  return guard([&] {
+    PGD_CHECK(pm, kErrArg, "null argument");
+    Model& m = pm->m;
+    check_held_pages(m, ids, n);
+    // a page listed twice must hold two references
+    std::unordered_map<int, int> count;
+    for (int i = 0; i < n; ++i) count[ids[i]]++;
+    for (auto& kv : count)
+      PGD_CHECK(m.refcount[kv.first] >= kv.second, kErrState,
+                "page " + std::to_string(kv.first) + " released more often than held");
+    for (int i = 0; i < n; ++i) m.release_block(ids[i]);
+  });
+}
+
+int pgd_page_refcount(const pgd_model* pm, int32_t id, int* count) {
+  return guard([&] {
+    PGD_CHECK(pm && count, kErrArg, "null argument");
+    const Model& m = pm->m;
+    PGD_CHECK(id >= 0 && id < (int)m.refcount.size(), kErrArg, "page id outside the pool");
+    *count = m.refcount[id];
+  });
+}
+
+int pgd_session_from_pages(pgd_model* pm, const int32_t* ids, int n_pages, int n_pos, pgd_session** out) {
+  pgd_session* held = nullptr;
+  int rc = guard([&] {
+    PGD_CHECK(pm && out, kErrArg, "null argument");
+    Model& m = pm->m;
+    // a recurrent (GDN) state is not a function of KV pages: a hybrid session
+    // cannot be rebuilt from them (CandleCausalLM::cache_prefix default None,
+    // pagoda-hf/src/lib.rs:224)
+    PGD_CHECK(m.rec_floats == 0, kErrState, "a recurrent-state model cannot build a session from KV pages");
+    PGD_CHECK(m.n_full > 0, kErrState, "model has no KV pages");
+    PGD_CHECK(n_pos >= 0 && n_pos <= m.cfg.max_pos, kErrArg, "length outside 0..max_pos");
+    const int need = (n_pos + m.cfg.kv_block - 1) / m.cfg.kv_block;
+    PGD_CHECK(n_pages == need, kErrArg,
+              std::to_string(n_pos) + " positions take " + std::to_string(need) + " pages, not " +
+                  std::to_string(n_pages));
+    check_held_pages(m, ids, n_pages);
+    {
+      std::unordered_set<int> seen;
+      for (int i = 0; i < n_pages; ++i)
+        PGD_CHECK(seen.insert(ids[i]).second, kErrArg, "page " + std::to_string(ids[i]) + " listed twice");
+    }
+    held = new pgd_session();
+    held->s.model = &m;
+    m.live_sessions++;
+    held->s.len = n_pos;
+    held->s.blocks.assign(ids, ids + n_pages);
+    // the session takes its own reference on every page; a page another
+    // holder keeps (refcount > 1) is copied before the session's first write
+    // into it (the step's copy-on-write of a shared tail)
     for (int b : held->s.blocks) m.refcount[b]++;
     *out = held;
   });

@@ -145,6 +145,41 @@ class Model:
         call("pgd_session_import", self.handle, _p(buf), C.c_size_t(buf.size), C.byref(h))
         return Session(self, h)
 
+    # ---- engine-addressable KV pages (pagoda/src/kv_cache.rs, radix_cache.rs) ----
+    def kv_pool(self) -> dict:
+        """PagedKvCache::num_blocks / block_size / num_free_blocks
+        (pagoda/src/kv_cache.rs:48-56) of the device page pool."""
+        n, b, f = C.c_int(), C.c_int(), C.c_int()
+        call("pgd_model_kv_pool", self.handle, C.byref(n), C.byref(b), C.byref(f))
+        return {"pages": n.value, "page_tokens": b.value, "free": f.value}
+
+    def page_retain(self, ids) -> None:
+        """PagedKvCache::inc_ref (kv_cache.rs:90) for each page id."""
+        a = np.ascontiguousarray(ids, np.int32)
+        call("pgd_page_retain", self.handle, _p(a) if a.size else None, int(a.size))
+
+    def page_release(self, ids) -> None:
+        """PagedKvCache::dec_ref (kv_cache.rs:95) for each page id."""
+        a = np.ascontiguousarray(ids, np.int32)
+        call("pgd_page_release", self.handle, _p(a) if a.size else None, int(a.size))
+
+    def page_refcount(self, page: int) -> int:
+        """PagedKvCache::ref_count (kv_cache.rs:74)."""
+        n = C.c_int()
+        call("pgd_page_refcount", self.handle, C.c_int32(int(page)), C.byref(n))
+        return n.value
+
+    def session_from_pages(self, ids, n_pos: int) -> "Session":
+        """A session whose first n_pos positions are the KV held in `ids`
+        (ceil(n_pos / page_tokens) pages, in position order): the radix
+        cache's matched (BlockId, offset) slots (radix_cache.rs:17-18) made
+        into a live cache without copying. Qwen2 only."""
+        a = np.ascontiguousarray(ids, np.int32)
+        h = C.c_void_p()
+        call("pgd_session_from_pages", self.handle, _p(a) if a.size else None, int(a.size), int(n_pos),
+             C.byref(h))
+        return Session(self, h)
+
     def step_ragged(self, sessions, feeds, all_rows: bool = False, want_logits: bool = False):
         """One batched forward: session i feeds feeds[i] (>= 1 tokens).
         Returns (ids, logits|None); ids per session (last position) or per fed
@@ -211,6 +246,15 @@ class Session:
         h = C.c_void_p()
         call("pgd_session_fork_prefix", self.handle, int(n), C.byref(h))
         return Session(self.model, h)
+
+    def pages(self) -> np.ndarray:
+        """Page ids holding positions [0, context_len) in order; position p
+        lives in slot p % page_tokens of pages[p // page_tokens]."""
+        n = C.c_int()
+        call("pgd_session_pages", self.handle, None, 0, C.byref(n))
+        ids = np.zeros(n.value, np.int32)
+        call("pgd_session_pages", self.handle, _p(ids) if ids.size else None, int(ids.size), C.byref(n))
+        return ids
 
     def export_kv(self) -> bytes:
         n = C.c_size_t()

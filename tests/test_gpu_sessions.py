@@ -243,3 +243,135 @@ def test_one_nonfinite_logit_faults_the_row(dev, tmp_path):
     finally:
         model.free()
         clean.free()
+
+
+# ------------------------------------------------- engine-addressable KV pages
+def _bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("k", [16, 21, 37])
+def test_session_from_pages_equals_fork_prefix(dev, k):
+    """The radix-cache flow of pagoda/src/radix_cache.rs over device pages: a
+    finished request's pages are retained by the engine (inc_ref), its session
+    is freed, and a later request whose prompt shares the first k tokens is
+    built from those page ids without a copy. It decodes bit for bit like a
+    prefix graft of the original, the original's KV is never disturbed by the
+    new session's writes (copy-on-write of the shared partial page), and
+    every page goes back to the pool once every holder let go."""
+    from pagoda_amd.engine import Model
+
+    cfg = small2(kv_blocks=64)
+    model = Model.synth(dev, cfg, 5)
+    try:
+        pool = model.kv_pool()
+        assert pool == {"pages": 64, "page_tokens": 16, "free": 64}
+        toks = np.random.default_rng(9).integers(0, cfg.vocab, 40)
+        s = model.new_session()
+        s.forward(toks)
+        pages = s.pages()
+        assert pages.size == 3 and len(set(pages.tolist())) == 3
+        assert all(model.page_refcount(p) == 1 for p in pages)
+        g = s.fork_prefix(k)
+        before = s.export_kv()
+        # engine side: the radix cache takes its references on the pages that
+        # hold the first k positions (ceil(k / 16))
+        held = pages[: (k + 15) // 16]
+        model.page_retain(held)
+        assert all(model.page_refcount(p) == 3 for p in held)  # s, g, engine
+        t = model.session_from_pages(held, k)
+        assert t.context_len() == k
+        np.testing.assert_array_equal(t.pages(), held)
+        cont = [11, 12, 13, 14, 15, 16, 17, 18, 19]
+        np.testing.assert_array_equal(_bits(t.forward(cont)), _bits(g.forward(cont)))
+        for tok in (3, 7, 1):
+            np.testing.assert_array_equal(_bits(t.forward([tok])), _bits(g.forward([tok])))
+        assert s.export_kv() == before
+        # the engine's pages still hold the original KV: a second session
+        # built from them later decodes like the first one did
+        u = model.session_from_pages(held, k)
+        t2 = s.fork_prefix(k)
+        np.testing.assert_array_equal(_bits(u.forward(cont)), _bits(t2.forward(cont)))
+        for x in (s, g, t, u, t2):
+            x.free()
+        assert all(model.page_refcount(p) == 1 for p in held)  # the engine's own
+        model.page_release(held)
+        assert all(model.page_refcount(p) == 0 for p in pages)
+        assert model.kv_pool()["free"] == 64
+    finally:
+        model.free()
+
+
+def test_session_from_pages_errors(dev):
+    from pagoda_amd import PagodaError
+    from pagoda_amd.engine import Model
+
+    model = Model.synth(dev, small2(kv_blocks=32), 5)
+    try:
+        s = model.new_session()
+        s.forward(np.arange(20))
+        p = s.pages()
+        free_page = next(i for i in range(32) if model.page_refcount(i) == 0)
+        bad = [
+            (p, 33),                      # 33 positions need 3 pages
+            (p[:1], 20),                  # 20 positions need 2
+            ([p[0], p[0]], 20),           # a page listed twice
+            ([p[0], free_page], 20),      # a free page
+            ([p[0], 99], 20),             # outside the pool
+        ]
+        for ids, n in bad:
+            with pytest.raises(PagodaError):
+                model.session_from_pages(ids, n)
+        with pytest.raises(PagodaError):
+            model.page_retain([free_page])
+        with pytest.raises(PagodaError):
+            model.page_release([p[0], p[0]])  # held once
+        assert model.page_refcount(p[0]) == 1
+        e = model.session_from_pages([], 0)
+        assert e.context_len() == 0 and e.pages().size == 0
+        e.free()
+        s.free()
+    finally:
+        model.free()
+    hy = Model.synth(dev, small35(n_layers=4), 11)
+    try:
+        h = hy.new_session()
+        h.forward([1, 2, 3])
+        hp = h.pages()
+        with pytest.raises(PagodaError) as ei:
+            hy.session_from_pages(hp, 3)
+        assert ei.value.code == -5
+        h.free()
+    finally:
+        hy.free()
+
+
+def test_pool_exhaustion_leaves_sessions_usable(dev):
+    """A step that cannot get KV pages fails with PGD_ERR_ALLOC before any
+    state is written: no session advances or is poisoned, and both continue
+    exactly like twins that never saw the failed step (atomic batched step,
+    pagoda-hf/src/llama.rs:750-778)."""
+    from pagoda_amd import PagodaError
+    from pagoda_amd.engine import Model
+
+    model = Model.synth(dev, small2(kv_blocks=6), 5)
+    try:
+        rng = np.random.default_rng(12)
+        a_t, b_t = rng.integers(0, 1024, 30), rng.integers(0, 1024, 40)
+        a, b = model.new_session(), model.new_session()
+        a.forward(a_t)
+        b.forward(b_t)  # 2 + 3 pages of 6
+        ta, tb = a.fork(), b.fork()  # share the pages: no new ones
+        with pytest.raises(PagodaError) as ei:
+            model.step_ragged([a, b], [rng.integers(0, 1024, 20), [5]])  # a needs 2 more, 1 free
+        assert ei.value.code == -6
+        assert (a.context_len(), b.context_len()) == (30, 40)
+        # the failed step took no pages for good either: a twin-for-twin
+        # continuation needs and finds them
+        for x, y in ((a, ta), (b, tb)):
+            np.testing.assert_array_equal(_bits(x.forward([9])), _bits(y.forward([9])))
+            x.free()
+            y.free()
+        assert model.kv_pool()["free"] == 6
+    finally:
+        model.free()
