@@ -88,6 +88,23 @@ def gpu_bench(args):
     for s in sessions:
         s.free()
 
+    # ---- the same batch decode with each step replayed from a HIP graph ----
+    model.set_graphs(True)
+    sessions = [model.new_session() for _ in range(batch)]
+    ids, _ = model.step_ragged(sessions, prompts)
+    for _ in range(args.warmup):
+        ids, _ = model.step_ragged(sessions, [[int(t)] for t in ids])
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ids, _ = model.step_ragged(sessions, [[int(t)] for t in ids])
+    dev.sync()
+    tok_s_graph = batch * args.steps / (time.perf_counter() - t0)
+    log(f"batch {batch} graphed: {tok_s_graph:.1f} tok/s")
+    for s in sessions:
+        s.free()
+    model.set_graphs(False)
+
     # ---- batch 1 decode ----
     s = model.new_session()
     s.forward(prompts[0])
@@ -103,15 +120,37 @@ def gpu_bench(args):
     b1_tok_s = n1 / wall1
     log(f"batch 1: {wall1 * 1e3 / n1:.2f} ms/token, {b1_tok_s:.1f} tok/s")
     s.free()
+    b1_graph = graphed_batch1(model, dev, prompts[0], args.warmup, n1)
+    log(f"batch 1 graphed: {b1_graph:.1f} tok/s")
     c5 = None if args.no_config5 else config5(model, cfg)
     model.free()
     c1 = config1(dev)
     return {
         "tok_s": tok_s, "ms_per_step": ms_per_step, "batch1_tok_s": b1_tok_s, "step_ms_pct": pct, "config5": c5,
+        "tok_s_graph": tok_s_graph, "batch1_tok_s_graph": b1_graph,
         "config1": c1,
         "weight_gb": info["weight_bytes"] / 1e9, "algo_gb_per_step": info["algo_bytes_per_token"] / 1e9,
         "roofline": roof,
     }
+
+
+def graphed_batch1(model, dev, prompt, warmup, n):
+    """Batch-1 greedy decode with every step replayed from a HIP graph
+    (pgd_model_set_graphs); returns tok/s over n timed steps."""
+    model.set_graphs(True)
+    s = model.new_session()
+    s.forward(prompt)
+    tok = 1
+    for _ in range(warmup + 2):
+        tok, _ = s.forward_greedy(tok)
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        tok, _ = s.forward_greedy(tok)
+    rate = n / (time.perf_counter() - t0)
+    s.free()
+    model.set_graphs(False)
+    return rate
 
 
 def config1(dev):
@@ -167,11 +206,29 @@ def config1(dev):
         fed += 1
     warm_ms = (time.perf_counter() - t0) * 1e3
     w.free()
+    # the cold stream again with every decode step replayed from a HIP graph
+    model.set_graphs(True)
+    g = model.new_session()
+    ids, _ = model.step_ragged([g], [prompt])
+    tok = int(ids[0])
+    gcold = [tok]
+    for _ in range(31):
+        tok, _ = g.forward_greedy(tok)
+        gcold.append(tok)
+    for _ in range(8):
+        tok, _ = g.forward_greedy(tok)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        tok, _ = g.forward_greedy(tok)
+    gdec_s = time.perf_counter() - t0
+    g.free()
     model.free()
     out = {"prompt": 81, "gen": 32, "prefill_ms": round(prefill_ms, 3), "gen_tok_s": round(31 / gen_s, 1),
-           "decode_tok_s": round(n / dec_s, 1), "warm_fed_tokens": fed, "warm_ms": round(warm_ms, 2),
+           "decode_tok_s": round(n / dec_s, 1), "decode_tok_s_graph": round(n / gdec_s, 1),
+           "graph_ids_equal_eager": gcold == cold, "warm_fed_tokens": fed, "warm_ms": round(warm_ms, 2),
            "warm_equals_cold": warm == cold}
-    log(f"config 1: prefill {prefill_ms:.2f} ms, decode {out['decode_tok_s']} tok/s, warm fed {fed}, "
+    log(f"config 1: prefill {prefill_ms:.2f} ms, decode {out['decode_tok_s']} tok/s "
+        f"(graphed {out['decode_tok_s_graph']}, ids equal: {gcold == cold}), warm fed {fed}, "
         f"warm == cold: {warm == cold}")
     return out
 
@@ -635,6 +692,9 @@ def main():
                                "greedy decode", "batch": args.batch, "prompt_len": 19,
                    "weight_gb": round(g["weight_gb"], 3), "algo_weight_gb_per_step": round(g["algo_gb_per_step"], 3)},
         "batch1_tok_s": round(g["batch1_tok_s"], 2),
+        "graphs": {"value": round(g["tok_s_graph"], 2), "batch1_tok_s": round(g["batch1_tok_s_graph"], 2),
+                   "note": "the same decode steps replayed from HIP graphs (pgd_model_set_graphs), one per "
+                           "launch signature; results bitwise equal to eager launches"},
         "step_ms_percentiles": g["step_ms_pct"],
         "config5": g["config5"],
         "config1": g["config1"],

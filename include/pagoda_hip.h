@@ -231,6 +231,16 @@ int pgd_model_config_get(const pgd_model* m, pgd_model_config* cfg);
  * (PGD_ARITH_DEQUANT_F32). A8 (hybrid model) matrices are unaffected. */
 enum { PGD_ARITH_DEQUANT_F32 = 0, PGD_ARITH_CPU_Q8 = 1 };
 int pgd_model_set_kquant_arith(pgd_model* m, int mode);
+/* No reference counterpart (the reference's Metal path encodes every kernel
+ * of a token into one command buffer, qwen3_fuse.rs). on != 0: each step's
+ * launches (embedding to argmax) are captured once per launch signature
+ * (batch shape, buffers, attention plan layout) into a HIP graph and replayed
+ * on later steps with the same signature; per-step data (tokens, positions,
+ * page tables) is uploaded before the replay. Results are bitwise those of
+ * the eager launches. The first step of a signature runs eagerly, the second
+ * is captured. graph_stats: graphs held, replays so far. */
+int pgd_model_set_graphs(pgd_model* m, int on);
+int pgd_model_graph_stats(const pgd_model* m, int* graphs, long long* launches);
 int pgd_model_free(pgd_model* m);
 /* weight bytes on the device, algorithmic weight bytes per decode step, KV pages free */
 int pgd_model_info(const pgd_model* m, size_t* weight_bytes, double* algo_bytes_per_token, int* kv_free);

@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_checkpoint_config": (c_int, [c_char_p, c_int, c_int, c_void_p]),
     "pgd_model_config_get": (c_int, [c_void_p, c_void_p]),
     "pgd_model_free": (c_int, [c_void_p]),
+    "pgd_model_set_graphs": (c_int, [c_void_p, c_int]),
+    "pgd_model_graph_stats": (c_int, [c_void_p, P(c_int), P(C.c_longlong)]),
     "pgd_model_info": (c_int, [c_void_p, P(c_size_t), P(c_double), P(c_int)]),
     "pgd_session_new": (c_int, [c_void_p, P(c_void_p)]),
     "pgd_session_fork": (c_int, [c_void_p, P(c_void_p)]),

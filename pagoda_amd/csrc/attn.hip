@@ -445,11 +445,14 @@ void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, con
     out[field] = (int)out.size();
     out.insert(out.end(), v.begin(), v.end());
   };
+  // the page list last: a decode step's other sections keep their offsets
+  // while its rows' contexts grow within a chunk (stable launch arguments for
+  // a captured step)
   put(2, items);
-  put(3, pages);
   put(4, item_rows);
   put(5, row_slot_off);
   put(6, row_slots);
+  put(3, pages);
 }
 
 AttnPlan attn_plan_view(const int* host, const int* dev) {

@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
@@ -56,7 +57,13 @@ void validate_config(const pgd_model_config& c, bool synthetic) {
 }
 
 // ---------------------------------------------------------------------------
+void Model::drop_graphs() {
+  for (auto& g : graphs) (void)hipGraphExecDestroy(g.second.exec);
+  graphs.clear();
+}
+
 Model::~Model() {
+  drop_graphs();
   if (dev) {
     DeviceScope scope(dev);
     (void)hipStreamSynchronize(dev->stream);
@@ -328,6 +335,52 @@ Ws carve_ws(Model& m, int rows, int lrows) {
 
 }  // namespace
 
+// Replays the captured graph of a step whose launches are keyed by `key`;
+// the first step with a key runs eagerly (it sizes every scratch buffer),
+// the second is captured and replayed. A capture that fails (a buffer grew
+// during it) is dropped and the step runs eagerly: nothing executes while a
+// stream is being captured.
+void run_graphed(Model& m, const std::vector<long long>& key, const std::function<void()>& forward) {
+  hipStream_t st = m.dev->stream;
+  const uint64_t epoch = gemv::scratch_epoch();
+  auto it = m.graphs.find(key);
+  if (it != m.graphs.end() && it->second.epoch == epoch) {
+    PGD_HIP(hipGraphLaunch(it->second.exec, st));
+    m.graph_launches++;
+    return;
+  }
+  if (it != m.graphs.end()) {
+    (void)hipGraphExecDestroy(it->second.exec);
+    m.graphs.erase(it);
+  }
+  if (!m.graph_seen.insert(key).second || m.graph_seen.size() > 4096) {
+    if (m.graph_seen.size() > 4096) m.graph_seen.clear();
+    if (m.graphs.size() >= 64) m.drop_graphs();
+    hipGraph_t g = nullptr;
+    PGD_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    bool ok = true;
+    try {
+      forward();
+    } catch (...) {
+      ok = false;
+    }
+    hipError_t e = hipStreamEndCapture(st, &g);
+    ok = ok && e == hipSuccess && g && gemv::scratch_epoch() == epoch;
+    hipGraphExec_t ex = nullptr;
+    if (ok) ok = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) == hipSuccess;
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipGetLastError();  // a failed capture's error is not this step's
+    if (ok) {
+      m.graphs[key] = {ex, epoch};
+      PGD_HIP(hipGraphLaunch(ex, st));
+      m.graph_launches++;
+      return;
+    }
+    if (ex) (void)hipGraphExecDestroy(ex);
+  }
+  forward();
+}
+
 void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, int nseq, StepOut& out) {
   const pgd_model_config& c = m.cfg;
   hipStream_t st = m.dev->stream;
@@ -405,6 +458,9 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     max_pos = std::max(max_pos, sess[i]->len + n[i] - 1);
     max_blocks = std::max(max_blocks, sess[i]->blocks.size());
   }
+  // block-table stride rounded up to 16 pages: it is a launch argument, and a
+  // captured step stays valid while contexts grow by up to 256 positions
+  max_blocks = align_up(max_blocks, 16);
   m.ensure_rope(max_pos);
   const int rd = c.rotary_dim;
   // ---- attention plan (same for every full-attention layer) ----
@@ -517,151 +573,168 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
     PGD_HIP(hipHostMalloc(&m.out_host, out_bytes * 2));
     m.out_host_cap = out_bytes * 2;
   }
-  poison.armed = true;
-  qmat_embed(m.embed, d_tok, rows, w.x, H, st);
-  const size_t per_lin = m.conv_floats + m.state_floats;
-  const bool hybrid = c.arch == PGD_ARCH_QWEN35;
-  // the next input norm's deferred input, when the last residual GEMV wrote it
-  A8Act next_in;
-  bool have_next_in = false;
-  for (size_t li = 0; li < m.layers.size(); ++li) {
-    auto& L = m.layers[li];
-    A8Act post_in;  // the post-mixer norm's deferred input
-    bool conv_done = false;  // the projection GEMV ran the causal conv
-    // ---- projections of the normed input ----
-    const float *q_raw = nullptr, *k_raw = nullptr, *v_raw = nullptr;
-    int ld_q = 0, ld_kv = 0;
-    if (hybrid) {
-      // the input norm's deferred operands: written by the previous layer's down
-      // projection, or prepared here for the first layer; one GEMV for all projections
-      A8Act act = have_next_in ? next_in : a8_gnorm_prep(w.x, H, rows, H, L.in_norm, eps, w.act, st);
-      // one token per sequence: the GEMV's epilogue (1..4 rows, and the
-      // per-wave kernels) or its range reduction also runs the causal conv,
-      // row r on sequence r's state
-      conv_done = !L.full && rows == nseq;
-      if (conv_done)
-        qmat_gemv_a8_conv(L.proj, act, w.A, (int)w.lda, L.conv, d_sb, (size_t)L.lin_index * per_lin, m.conv_dim,
-                          c.conv_kernel, w.D, (int)w.ldd, st);
-      else
-        qmat_gemv_a8(L.proj, act, w.A, (int)w.lda, nullptr, 0, st);
-      if (L.full) {
+  uint32_t* d_ids = m.out_dev.as<uint32_t>();
+  float* d_vals = (float*)(d_ids + lrows);
+  int* d_nf = (int*)(d_vals + lrows);
+  // every launch of the forward, from the embedding rows to the argmax; the
+  // same launches with the same arguments whenever graph_key() is the same
+  auto forward = [&]() {
+    qmat_embed(m.embed, d_tok, rows, w.x, H, st);
+    const size_t per_lin = m.conv_floats + m.state_floats;
+    const bool hybrid = c.arch == PGD_ARCH_QWEN35;
+    // the next input norm's deferred input, when the last residual GEMV wrote it
+    A8Act next_in;
+    bool have_next_in = false;
+    for (size_t li = 0; li < m.layers.size(); ++li) {
+      auto& L = m.layers[li];
+      A8Act post_in;  // the post-mixer norm's deferred input
+      bool conv_done = false;  // the projection GEMV ran the causal conv
+      // ---- projections of the normed input ----
+      const float *q_raw = nullptr, *k_raw = nullptr, *v_raw = nullptr;
+      int ld_q = 0, ld_kv = 0;
+      if (hybrid) {
+        // the input norm's deferred operands: written by the previous layer's down
+        // projection, or prepared here for the first layer; one GEMV for all projections
+        A8Act act = have_next_in ? next_in : a8_gnorm_prep(w.x, H, rows, H, L.in_norm, eps, w.act, st);
+        // one token per sequence: the GEMV's epilogue (1..4 rows, and the
+        // per-wave kernels) or its range reduction also runs the causal conv,
+        // row r on sequence r's state
+        conv_done = !L.full && rows == nseq;
+        if (conv_done)
+          qmat_gemv_a8_conv(L.proj, act, w.A, (int)w.lda, L.conv, d_sb, (size_t)L.lin_index * per_lin, m.conv_dim,
+                            c.conv_kernel, w.D, (int)w.ldd, st);
+        else
+          qmat_gemv_a8(L.proj, act, w.A, (int)w.lda, nullptr, 0, st);
+        if (L.full) {
+          q_raw = w.A;
+          k_raw = w.A + m.q_out;
+          v_raw = w.A + m.q_out + m.kv_width;
+          ld_q = ld_kv = (int)w.lda;
+        }
+      } else {
+        rmsnorm_rows(w.x, H, nullptr, rows, H, L.in_norm, eps, norm_mode, w.xn, H, st);
+        // q | k | v side by side in A (q and k from one stacked launch when they share a format)
+        float* yv = w.A + m.q_out + m.kv_width;
+        if (L.proj.base && m.q8act && qmat_q8act_pairable(L.proj, L.v)) {
+          // stacked q|k and v in one launch (one activation quantization)
+          qmat_gemv_q8act_pair(L.proj, w.A, L.v, yv, w.xn, H, rows, (int)w.lda, st);
+        } else {
+          if (L.proj.base) {
+            gemv(L.proj, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
+          } else {
+            gemv(L.q, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
+            gemv(L.k, w.xn, H, rows, w.A + m.q_out, (int)w.lda, nullptr, 0);
+          }
+          gemv(L.v, w.xn, H, rows, yv, (int)w.lda, nullptr, 0);
+        }
         q_raw = w.A;
         k_raw = w.A + m.q_out;
         v_raw = w.A + m.q_out + m.kv_width;
         ld_q = ld_kv = (int)w.lda;
       }
-    } else {
-      rmsnorm_rows(w.x, H, nullptr, rows, H, L.in_norm, eps, norm_mode, w.xn, H, st);
-      // q | k | v side by side in A (q and k from one stacked launch when they share a format)
-      float* yv = w.A + m.q_out + m.kv_width;
-      if (L.proj.base && m.q8act && qmat_q8act_pairable(L.proj, L.v)) {
-        // stacked q|k and v in one launch (one activation quantization)
-        qmat_gemv_q8act_pair(L.proj, w.A, L.v, yv, w.xn, H, rows, (int)w.lda, st);
+      if (!L.full) {
+        // stacked rows: [qkv (conv_dim) | z (value_dim) | b (v_heads) | a (v_heads)]
+        const float* P = w.A;
+        const int ldp = (int)w.lda;
+        if (!conv_done)
+          conv_step(P, ldp, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb, (size_t)L.lin_index * per_lin,
+                    sm, nseq, max_n, st);
+        GdnParams gp{};
+        gp.k_heads = c.k_heads;
+        gp.v_heads = c.v_heads;
+        gp.k_dim = c.k_dim;
+        gp.v_dim = c.v_dim;
+        gp.conv_out = w.D;
+        gp.ld_conv = (int)w.ldd;
+        gp.z = P + m.conv_dim;
+        gp.ld_z = ldp;
+        gp.b = P + m.conv_dim + m.value_dim;
+        gp.a = P + m.conv_dim + m.value_dim + c.v_heads;
+        gp.ld_ab = ldp;
+        gp.a_log = L.a_log;
+        gp.dt_bias = L.dt_bias;
+        gp.norm = L.gnorm;
+        // the gated norm writes the out projection's operands itself
+        const A8Act act = a8_act_view(w.act, rows, m.value_dim);
+        gp.out = nullptr;
+        gp.act = a8_act_dst(act);
+        gp.state_base = d_sb;
+        gp.state_off = (size_t)L.lin_index * per_lin + m.conv_floats;
+        gdn_step(gp, sm, nseq, rows, max_n, st);
+        // the residual GEMV also writes the post-mixer norm's input (act3)
+        post_in = qmat_gemv_a8_res_norm(L.out, act, w.x, H, L.post_norm, eps, w.act3, st);
       } else {
-        if (L.proj.base) {
-          gemv(L.proj, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
+        AttnLayout al{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.kv_block, L.k_pool, L.v_pool};
+        QkvPrep qp{};
+        qp.variant = hybrid ? 0 : 1;
+        qp.q_raw = q_raw;
+        qp.ld_q = ld_q;
+        qp.k_raw = k_raw;
+        qp.v_raw = v_raw;
+        qp.ld_kv = ld_kv;
+        qp.q_norm = L.q_norm;
+        qp.k_norm = L.k_norm;
+        qp.q_bias = L.qb;
+        qp.k_bias = L.kb;
+        qp.v_bias = L.vb;
+        qp.q = w.D;
+        qp.gate = w.F;
+        qkv_prep(qp, al, rm, rows, st);
+        if (hybrid) {
+          // attention writes the o projection's operands itself
+          const A8Act act = a8_act_view(w.act, rows, c.heads * c.head_dim);
+          const a8act::Dst dst = a8_act_dst(act);
+          attn_decode(w.D, w.F, nullptr, al, rm, ap, rows, st, &dst);
+          post_in = qmat_gemv_a8_res_norm(L.o, act, w.x, H, L.post_norm, eps, w.act3, st);
         } else {
-          gemv(L.q, w.xn, H, rows, w.A, (int)w.lda, nullptr, 0);
-          gemv(L.k, w.xn, H, rows, w.A + m.q_out, (int)w.lda, nullptr, 0);
+          attn_decode(w.D, nullptr, w.E, al, rm, ap, rows, st);
+          gemv(L.o, w.E, c.heads * c.head_dim, rows, w.x, H, w.x, H);
         }
-        gemv(L.v, w.xn, H, rows, yv, (int)w.lda, nullptr, 0);
       }
-      q_raw = w.A;
-      k_raw = w.A + m.q_out;
-      v_raw = w.A + m.q_out + m.kv_width;
-      ld_q = ld_kv = (int)w.lda;
-    }
-    if (!L.full) {
-      // stacked rows: [qkv (conv_dim) | z (value_dim) | b (v_heads) | a (v_heads)]
-      const float* P = w.A;
-      const int ldp = (int)w.lda;
-      if (!conv_done)
-        conv_step(P, ldp, w.D, (int)w.ldd, m.conv_dim, c.conv_kernel, L.conv, d_sb, (size_t)L.lin_index * per_lin,
-                  sm, nseq, max_n, st);
-      GdnParams gp{};
-      gp.k_heads = c.k_heads;
-      gp.v_heads = c.v_heads;
-      gp.k_dim = c.k_dim;
-      gp.v_dim = c.v_dim;
-      gp.conv_out = w.D;
-      gp.ld_conv = (int)w.ldd;
-      gp.z = P + m.conv_dim;
-      gp.ld_z = ldp;
-      gp.b = P + m.conv_dim + m.value_dim;
-      gp.a = P + m.conv_dim + m.value_dim + c.v_heads;
-      gp.ld_ab = ldp;
-      gp.a_log = L.a_log;
-      gp.dt_bias = L.dt_bias;
-      gp.norm = L.gnorm;
-      // the gated norm writes the out projection's operands itself
-      const A8Act act = a8_act_view(w.act, rows, m.value_dim);
-      gp.out = nullptr;
-      gp.act = a8_act_dst(act);
-      gp.state_base = d_sb;
-      gp.state_off = (size_t)L.lin_index * per_lin + m.conv_floats;
-      gdn_step(gp, sm, nseq, rows, max_n, st);
-      // the residual GEMV also writes the post-mixer norm's input (act3)
-      post_in = qmat_gemv_a8_res_norm(L.out, act, w.x, H, L.post_norm, eps, w.act3, st);
-    } else {
-      AttnLayout al{c.heads, c.kv_heads, c.head_dim, c.rotary_dim, c.kv_block, L.k_pool, L.v_pool};
-      QkvPrep qp{};
-      qp.variant = hybrid ? 0 : 1;
-      qp.q_raw = q_raw;
-      qp.ld_q = ld_q;
-      qp.k_raw = k_raw;
-      qp.v_raw = v_raw;
-      qp.ld_kv = ld_kv;
-      qp.q_norm = L.q_norm;
-      qp.k_norm = L.k_norm;
-      qp.q_bias = L.qb;
-      qp.k_bias = L.kb;
-      qp.v_bias = L.vb;
-      qp.q = w.D;
-      qp.gate = w.F;
-      qkv_prep(qp, al, rm, rows, st);
+      // ---- SwiGLU MLP ----
       if (hybrid) {
-        // attention writes the o projection's operands itself
-        const A8Act act = a8_act_view(w.act, rows, c.heads * c.head_dim);
-        const a8act::Dst dst = a8_act_dst(act);
-        attn_decode(w.D, w.F, nullptr, al, rm, ap, rows, st, &dst);
-        post_in = qmat_gemv_a8_res_norm(L.o, act, w.x, H, L.post_norm, eps, w.act3, st);
+        const A8Act act = post_in;
+        // the SwiGLU epilogue writes the down projection's operands itself
+        const A8Act mid = a8_act_view(w.act2, rows, c.intermediate);
+        qmat_gemv_a8_swiglu(L.gate, L.up, act, nullptr, 0, st, &mid);
+        // the residual GEMV also writes the next layer's input norm (act)
+        if (li + 1 < m.layers.size()) {
+          next_in = qmat_gemv_a8_res_norm(L.down, mid, w.x, H, m.layers[li + 1].in_norm, eps, w.act, st);
+          have_next_in = true;
+        } else {
+          qmat_gemv_a8(L.down, mid, w.x, H, w.x, H, st);
+        }
       } else {
-        attn_decode(w.D, nullptr, w.E, al, rm, ap, rows, st);
-        gemv(L.o, w.E, c.heads * c.head_dim, rows, w.x, H, w.x, H);
+        rmsnorm_rows(w.x, H, nullptr, rows, H, L.post_norm, eps, norm_mode, w.xn, H, st);
+        if (m.q8act) qmat_gemv_swiglu_q8act(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
+        else qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
+        gemv(L.down, w.G, c.intermediate, rows, w.x, H, w.x, H);
       }
     }
-    // ---- SwiGLU MLP ----
+    // ---- head ----
     if (hybrid) {
-      const A8Act act = post_in;
-      // the SwiGLU epilogue writes the down projection's operands itself
-      const A8Act mid = a8_act_view(w.act2, rows, c.intermediate);
-      qmat_gemv_a8_swiglu(L.gate, L.up, act, nullptr, 0, st, &mid);
-      // the residual GEMV also writes the next layer's input norm (act)
-      if (li + 1 < m.layers.size()) {
-        next_in = qmat_gemv_a8_res_norm(L.down, mid, w.x, H, m.layers[li + 1].in_norm, eps, w.act, st);
-        have_next_in = true;
-      } else {
-        qmat_gemv_a8(L.down, mid, w.x, H, w.x, H, st);
-      }
+      A8Act act = a8_norm_prep(w.x, H, d_lr, lrows, H, m.final_norm, eps, nullptr, 0, w.act, st);
+      qmat_gemv_a8(m.head, act, w.logits, c.vocab, nullptr, 0, st);
     } else {
-      rmsnorm_rows(w.x, H, nullptr, rows, H, L.post_norm, eps, norm_mode, w.xn, H, st);
-      if (m.q8act) qmat_gemv_swiglu_q8act(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
-      else qmat_gemv_swiglu(L.gate, L.up, w.xn, H, rows, w.G, c.intermediate, st);
-      gemv(L.down, w.G, c.intermediate, rows, w.x, H, w.x, H);
+      rmsnorm_rows(w.x, H, d_lr, lrows, H, m.final_norm, eps, norm_mode, w.xn, H, st);
+      gemv(m.head, w.xn, H, lrows, w.logits, c.vocab, nullptr, 0);
     }
-  }
-  // ---- head ----
-  if (hybrid) {
-    A8Act act = a8_norm_prep(w.x, H, d_lr, lrows, H, m.final_norm, eps, nullptr, 0, w.act, st);
-    qmat_gemv_a8(m.head, act, w.logits, c.vocab, nullptr, 0, st);
+    argmax_rows(w.logits, c.vocab, lrows, c.vocab, out.last_max, d_ids, d_vals, d_nf, st);
+  };
+  poison.armed = true;
+  if (m.use_graphs) {
+    // Everything a launch argument depends on besides the model: shapes,
+    // workspace / metadata / output buffers, the attention plan's header and
+    // section offsets (its page list comes last, so it may grow), and the
+    // scratch buffers' allocation epoch.
+    std::vector<long long> key = {rows, nseq, lrows, out.all_rows, out.last_max, max_n, (long long)max_blocks,
+                                  (long long)(uintptr_t)m.ws.p, (long long)m.ws.bytes,
+                                  (long long)(uintptr_t)m.meta_dev.p, (long long)(uintptr_t)m.out_dev.p, m.q8act};
+    for (int i = 0; i < 8; ++i) key.push_back(plan[i]);
+    run_graphed(m, key, forward);
   } else {
-    rmsnorm_rows(w.x, H, d_lr, lrows, H, m.final_norm, eps, norm_mode, w.xn, H, st);
-    gemv(m.head, w.xn, H, lrows, w.logits, c.vocab, nullptr, 0);
+    forward();
   }
-  uint32_t* d_ids = m.out_dev.as<uint32_t>();
-  float* d_vals = (float*)(d_ids + lrows);
-  int* d_nf = (int*)(d_vals + lrows);
-  argmax_rows(w.logits, c.vocab, lrows, c.vocab, out.last_max, d_ids, d_vals, d_nf, st);
   PGD_HIP(hipMemcpyAsync(m.out_host, m.out_dev.p, out_bytes, hipMemcpyDeviceToHost, st));
   if (out.logits)
     PGD_HIP(hipMemcpyAsync(out.logits, w.logits, (size_t)lrows * c.vocab * 4, hipMemcpyDeviceToHost, st));
@@ -710,6 +783,28 @@ int pgd_model_set_kquant_arith(pgd_model* pm, int mode) {
     PGD_CHECK(pm, kErrArg, "null model");
     PGD_CHECK(mode == PGD_ARITH_DEQUANT_F32 || mode == PGD_ARITH_CPU_Q8, kErrArg, "unknown arithmetic mode");
     pm->m.q8act = mode == PGD_ARITH_CPU_Q8 ? 1 : 0;
+  });
+}
+
+int pgd_model_set_graphs(pgd_model* pm, int on) {
+  return guard([&] {
+    PGD_CHECK(pm, kErrArg, "null argument");
+    Model& m = pm->m;
+    DeviceScope scope(m.dev);
+    PGD_HIP(hipStreamSynchronize(m.dev->stream));
+    m.use_graphs = on != 0;
+    if (!m.use_graphs) {
+      m.drop_graphs();
+      m.graph_seen.clear();
+    }
+  });
+}
+
+int pgd_model_graph_stats(const pgd_model* pm, int* graphs, long long* launches) {
+  return guard([&] {
+    PGD_CHECK(pm, kErrArg, "null argument");
+    if (graphs) *graphs = (int)pm->m.graphs.size();
+    if (launches) *launches = pm->m.graph_launches;
   });
 }
 

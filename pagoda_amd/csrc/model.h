@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <map>
+#include <set>
 #include <utility>
 #include <vector>
 
@@ -82,6 +84,17 @@ struct Model {
   // arithmetic of the GGML-format (Qwen2) matrices: 1 = candle's CPU quantized
   // matmul (activations quantized to Q8_K / Q8_0), 0 = f32 dequant-then-dot
   int q8act = 0;
+  // captured decode steps (pgd_model_set_graphs): one executable graph per
+  // launch signature, the signatures seen once, replays so far
+  struct Graph {
+    hipGraphExec_t exec;
+    uint64_t epoch;
+  };
+  bool use_graphs = false;
+  std::map<std::vector<long long>, Graph> graphs;
+  std::set<std::vector<long long>> graph_seen;
+  long long graph_launches = 0;
+  void drop_graphs();
 
   ~Model();
   void ensure_rope(int pos);

@@ -221,6 +221,9 @@ struct ScratchArena {
 };
 // install (nullptr: back to allocating); returns the previous arena
 ScratchArena* set_scratch_arena(ScratchArena* a);
+// Counts the (re)allocations of the stream scratch buffers: launch arguments
+// recorded before a change may point at freed memory.
+uint64_t scratch_epoch();
 }  // namespace gemv
 
 }  // namespace pgd

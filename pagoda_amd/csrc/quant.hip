@@ -1,5 +1,6 @@
 // quant.hip — quantized matrix storage: allocation, upload, dequant,
 // embedding rows, the GEMV front end and the seeded synthetic generator.
+#include <atomic>
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -423,6 +424,12 @@ ScratchArena* set_scratch_arena(ScratchArena* a) {
   return old;
 }
 
+namespace {
+std::atomic<uint64_t> g_scratch_epoch{0};
+}
+
+uint64_t scratch_epoch() { return g_scratch_epoch.load(std::memory_order_relaxed); }
+
 void* gemv_scratch(hipStream_t s, size_t bytes, int slot) {
   if (ScratchArena* ar = t_arena) {
     PGD_CHECK(slot >= 0 && slot < 8, kErrArg, "scratch slot");
@@ -448,6 +455,7 @@ void* gemv_scratch(hipStream_t s, size_t bytes, int slot) {
       e.second = 0;
     }
     size_t want = std::max(bytes, (size_t)4 << 20);
+    g_scratch_epoch.fetch_add(1, std::memory_order_relaxed);
     hipError_t err = hipMalloc(&e.first, want);
     if (err != hipSuccess) throw Error{kErrAlloc, std::string("hipMalloc gemv scratch: ") + hipGetErrorString(err)};
     e.second = want;

@@ -119,6 +119,17 @@ class Model:
         ARITH_DEQUANT_F32 for the GGML-format matrices."""
         call("pgd_model_set_kquant_arith", self.handle, int(mode))
 
+    def set_graphs(self, on: bool) -> None:
+        """Capture each step's launches into a HIP graph per launch signature
+        and replay it on later steps of that signature (bitwise the same
+        results as eager launches)."""
+        call("pgd_model_set_graphs", self.handle, int(bool(on)))
+
+    def graph_stats(self) -> dict:
+        g, n = C.c_int(), C.c_longlong()
+        call("pgd_model_graph_stats", self.handle, C.byref(g), C.byref(n))
+        return {"graphs": g.value, "replays": n.value}
+
     def info(self) -> dict:
         wb, ab, kf = C.c_size_t(), C.c_double(), C.c_int()
         call("pgd_model_info", self.handle, C.byref(wb), C.byref(ab), C.byref(kf))

@@ -137,3 +137,25 @@ def test_q8act_rejects_a8(dev):
         m.gemv_q8act_dev(xd, 256, 1, yd, 64)
     dev.free(xd)
     dev.free(yd)
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("n_in", [8960, 18944])
+def test_q8act_wide_rows_16(dev, fmt, n_in):
+    """Down projections of the larger Qwen2 sizes (intermediate 8960: 1.5B,
+    18944: 7B): 16 quantized rows of these widths do not fit the LDS at once,
+    so the launch takes fewer rows at a time with the same per-row arithmetic."""
+    n_out = 256
+    m, blk = make(dev, fmt, n_out, n_in, 7 * fmt + n_in % 89)
+    x = np.random.default_rng(n_in).normal(0, 1, (16, n_in)).astype(np.float32)
+    xd = dev.upload(x)
+    yd = dev.alloc(16 * n_out * 4)
+    m.gemv_q8act_dev(xd, n_in, 16, yd, n_out)
+    y = dev.download(yd, (16, n_out), np.float32)
+    assert close(y, oracle_rows(fmt, blk, n_out, n_in, x))
+    y1 = dev.alloc(n_out * 4)
+    m.gemv_q8act_dev(xd, n_in, 1, y1, n_out)
+    np.testing.assert_array_equal(dev.download(y1, (1, n_out), np.float32)[0].view(np.uint32), y[0].view(np.uint32))
+    for p in (xd, yd, y1):
+        dev.free(p)
+    m.free()

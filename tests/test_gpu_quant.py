@@ -421,3 +421,38 @@ def test_a8_prefill_gemm(dev, rows, epi):
     for p in (xd, act, yd):
         dev.free(p)
 
+
+
+@pytest.mark.parametrize("n_out,n_in,rows,dual", [(17408, 5120, 32, True), (17408, 5120, 64, True),
+                                                   (17408, 5120, 9, True), (151936, 5120, 32, False)])
+def test_a8_stream_k_repeatable(dev, n_out, n_in, rows, dual):
+    """Stream-K launches leave the cut blocks' partial sums in scratch for the
+    fix-up launch: 12 launches back to back over the same operands must all
+    give the same bits (a piece read before it was stored, or one left over
+    from the previous launch, shows up as a launch that differs)."""
+    from pagoda_amd import Matrix
+    from pagoda_amd.matrix import act_bytes, act_prep_dev
+
+    print(f"stream-K repeat {n_out}x{n_in} rows {rows} dual {dual}", flush=True)
+    g = Matrix.synth(dev, 0, n_out, n_in, 21, 1, 0.02)
+    u = Matrix.synth(dev, 0, n_out, n_in, 21, 2, 0.02) if dual else None
+    x = np.random.default_rng(rows).normal(0, 1, (rows, n_in)).astype(np.float32)
+    xd = dev.upload(x)
+    act = dev.alloc(act_bytes(rows, n_in))
+    act_prep_dev(dev, xd, n_in, rows, n_in, act)
+    outs = []
+    yd = dev.alloc(rows * n_out * 4)
+    for _ in range(12):
+        if dual:
+            Matrix.gemv_swiglu_act_dev(g, u, act, rows, yd, n_out)
+        else:
+            g.gemv_act_dev(act, rows, yd, n_out)
+        outs.append(dev.download(yd, (rows, n_out), np.float32))
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    assert np.isfinite(outs[0]).all()
+    for p in (xd, act, yd):
+        dev.free(p)
+    g.free()
+    if u is not None:
+        u.free()
