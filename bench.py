@@ -359,8 +359,15 @@ def roofline(dev, cfg, batch):
         t = json.loads(tfile.read_text())
         if str(batch) in t.get("hbm_bytes_per_launch", {}):
             traffic = t["hbm_bytes_per_launch"][str(batch)]
+    copy = copy_peak(dev)
+    mfma = None
+    mfile = ROOT / "profiles" / "mfma_busy.json"
+    if mfile.exists():
+        mfma = json.loads(mfile.read_text())
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+            "copy_peak": copy["gbs"], "frac_of_copy": achieved / copy["gbs"], "copy_note": copy["note"],
+            "mfma_busy": mfma,
             "kernel": (f"fused gate/up SwiGLU A8 GEMV 5120->2x17408, {batch} rows: a8_sk_kernel<2,2,2> (stream-K) "
                        f"+ a8_sk_fix_kernel<2,2> (cut blocks); 1 row: a8_mma_kernel<3,4,1,4,1,2>"),
             "algo_bytes_per_launch": algo, "avg_launch_us": avg_ms * 1e3,
@@ -370,6 +377,34 @@ def roofline(dev, cfg, batch):
 
 KQ_SHAPES = [(896, 4864), (4864, 896), (896, 1152), (896, 151936)]  # K x N
 KQ_ROWS = [1, 4, 8, 16, 32, 64]
+
+
+def copy_peak(dev):
+    """The on-box streaming rate: a plain device-to-device copy of 1 GiB (4x
+    the last-level cache) queued on the library's stream, timed with HIP
+    events over 10 copies; bytes read + bytes written per second."""
+    from pagoda_amd import Event
+    from pagoda_amd._lib import call
+    import ctypes as C
+
+    n = 1 << 30
+    a, b = dev.alloc(n), dev.alloc(n)
+
+    def cp():
+        call("pgd_device_copy_dev", dev.handle, C.c_void_p(b), C.c_void_p(a), C.c_size_t(n))
+
+    for _ in range(3):
+        cp()
+    e0 = Event(dev).record()
+    for _ in range(10):
+        cp()
+    e1 = Event(dev).record()
+    gbs = 2 * n * 10 / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    dev.free(a)
+    dev.free(b)
+    log(f"device copy 1 GiB: {gbs:.0f} GB/s (read + write)")
+    return {"gbs": gbs, "note": "device-to-device copy of 1 GiB (hipMemcpyAsync on the library stream), "
+                                "(read + write bytes) / time over 10 copies"}
 
 
 def kernel_sweeps():
@@ -509,9 +544,12 @@ def a8_sweep(rows_list, only=None):
             t_us = e0.elapsed_ms(e1) / L * 1e3
             algo = per + rows * K * 4 + rows * N * 4
             gbs = algo / (t_us * 1e-6) / 1e9
-            log(f"{name:9s} N={N:6d} K={K:5d} rows={rows:2d}: {t_us:8.1f} us {gbs:7.0f} GB/s {100 * gbs / HBM_PEAK_GBS:5.1f}%")
+            flops = 2.0 * rows * N * K * (2 if epi == 2 else 1)
+            tfs = flops / (t_us * 1e-6) / 1e12
+            log(f"{name:9s} N={N:6d} K={K:5d} rows={rows:2d}: {t_us:8.1f} us {gbs:7.0f} GB/s {100 * gbs / HBM_PEAK_GBS:5.1f}%"
+                f"  {tfs:6.1f} TFLOP/s useful")
             out.append({"matrix": name, "N": N, "K": K, "rows": rows, "us": round(t_us, 2), "algo_bytes": algo,
-                        "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+                        "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "useful_tflops": round(tfs, 1)})
             for p in (x, act, y, res):
                 dev.free(p)
         for m in ms + (us or []):
@@ -585,6 +623,14 @@ def cpu_baseline(args):
     from oracle import pyoracle as ora
 
     cores = ora.lib().ora_num_threads()
+    cpu_model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     c = ora.Qwen35Config(n_layers=4, vocab=4096)
     t0 = time.time()
     m = ora.Qwen35(c, 2026)
@@ -595,7 +641,7 @@ def cpu_baseline(args):
     n = 0
     t0 = time.perf_counter()
     tok = 1
-    while n < 3 or (time.perf_counter() - t0 < 10.0 and n < 20):
+    while n < 3 or (time.perf_counter() - t0 < 12.0 and n < 200):
         logits = m.forward([tok], cache)
         tok = int(np.argmax(logits))
         n += 1
@@ -609,7 +655,8 @@ def cpu_baseline(args):
     rate = small / per_tok4  # algorithmic weight bytes per second
     model_bytes = 16 * group + V * H * 8.5 / 8
     tok_s = rate / model_bytes
-    return {"value": tok_s, "unit": "tok/s", "cores": cores, "kind": "port",
+    return {"value": tok_s, "unit": "tok/s", "cores": cores, "kind": "port", "cpu_model": cpu_model,
+            "host_cpus": os.cpu_count(),
             "sample": f"oracle.c decode, batch 1, one full-width 4-layer group (3 GDN + 1 attention, vocab 4096), "
                       f"{n} tokens in {per_tok4 * n:.1f}s; weight-bytes rate {rate / 1e9:.2f} GB/s extrapolated "
                       f"to 64 layers + 151936-row lm_head"}

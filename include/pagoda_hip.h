@@ -56,6 +56,11 @@ int pgd_device_free(pgd_dev* dev, void* ptr);
 /* kind: 0 host->device, 1 device->host, 2 device->device (synchronous) */
 int pgd_device_memcpy(pgd_dev* dev, void* dst, const void* src, size_t bytes, int kind);
 
+/* Device-to-device copy queued on the handle's stream, not waited for (no
+ * reference counterpart: the on-box streaming rate the roofline report
+ * quotes beside the HBM specification). */
+int pgd_device_copy_dev(pgd_dev* dev, void* dst, const void* src, size_t bytes);
+
 /* ---- timing: HIP events recorded on the device handle's stream --------- */
 typedef struct pgd_event pgd_event;
 int pgd_event_new(pgd_dev* dev, pgd_event** out);

@@ -26,6 +26,7 @@ SIGNATURES: dict[str, tuple] = {
     "pgd_device_malloc": (c_int, [c_void_p, c_size_t, P(c_void_p)]),
     "pgd_device_free": (c_int, [c_void_p, c_void_p]),
     "pgd_device_memcpy": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int]),
+    "pgd_device_copy_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t]),
     "pgd_event_new": (c_int, [c_void_p, P(c_void_p)]),
     "pgd_event_record": (c_int, [c_void_p]),
     "pgd_event_elapsed_ms": (c_int, [c_void_p, c_void_p, P(c_float)]),

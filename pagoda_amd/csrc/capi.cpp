@@ -119,6 +119,14 @@ int pgd_device_memcpy(pgd_dev* dev, void* dst, const void* src, size_t bytes, in
   });
 }
 
+int pgd_device_copy_dev(pgd_dev* dev, void* dst, const void* src, size_t bytes) {
+  return guard([&] {
+    PGD_CHECK(dev && (bytes == 0 || (dst && src)), kErrArg, "null argument");
+    DeviceScope scope(dev);
+    if (bytes) PGD_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev->stream));
+  });
+}
+
 int pgd_event_new(pgd_dev* dev, pgd_event** out) {
   return guard([&] {
     PGD_CHECK(dev && out, kErrArg, "null argument");

@@ -254,3 +254,116 @@ def test_config4_widths_prefill_300_tokens(dev):
         assert rel(got, ref) < LOGIT_TOL, (step, rel(got, ref))
     s.free()
     model.free()
+
+
+def _c5_passes(model, trunk, suffixes, gen, want_logits=False):
+    """Config-5 pattern: every request forks one
+    prefilled trunk (KV pages shared copy-on-write), its suffix is prefilled
+    in one ragged step, then pass A decodes one token per request per step;
+    pass B restarts from the same post-suffix states and packs 1-token decode
+    rows (even requests) with 4-token known-token verify chunks (odd
+    requests, replaying pass A's tokens) into one ragged batch per step.
+    Returns pass A's streams (and logits per step) and the number of verified
+    ids that differ from pass A's."""
+    root = model.new_session()
+    root.forward(trunk)
+    reqs = [root.fork() for _ in suffixes]
+    first, lg = model.step_ragged(reqs, suffixes, want_logits=want_logits)
+    logits = [lg]
+    snap = [r.fork() for r in reqs]
+    streams = [[int(t)] for t in first]
+    for _ in range(gen - 1):
+        ids, lg = model.step_ragged(reqs, [[s[-1]] for s in streams], want_logits=want_logits)
+        logits.append(lg)
+        for s, t in zip(streams, ids):
+            s.append(int(t))
+    n = len(suffixes)
+    pos = [1] * n
+    mismatches = 0
+    while any(p < gen for p in pos):
+        sess, feeds, owners = [], [], []
+        for i in range(n):
+            if pos[i] >= gen:
+                continue
+            k = 1 if i % 2 == 0 else min(4, gen - pos[i])
+            feeds.append(streams[i][pos[i] - 1:pos[i] - 1 + k])
+            sess.append(snap[i])
+            owners.append((i, k))
+        ids, _ = model.step_ragged(sess, feeds, all_rows=True)
+        at = 0
+        for i, k in owners:
+            mismatches += sum(int(t) != s for t, s in zip(ids[at:at + k], streams[i][pos[i]:pos[i] + k]))
+            pos[i] += k
+            at += k
+    for s in reqs + snap + [root]:
+        s.free()
+    return streams, logits, mismatches
+
+
+def test_config5_widths_shared_trunk_mixed_verify(dev, capsys):
+    """Config 5 at config-4 widths on one 3:1 layer group (reduced vocab): a
+    300-token trunk (two 256-position attention chunks, so every row's
+    attention merges chunks) shared by 64 forks with distinct 50-token
+    suffixes; 64-row decode steps (two-chunk launches) and mixed decode /
+    verify batches. Every verified id equals the decoded stream, and two
+    requests' logits at every step are within 1e-3 of the oracle fed the same
+    tokens, with the oracle's greedy ids."""
+    import time
+    from dataclasses import replace
+
+    from pagoda_amd.engine import QWEN35_27B, Model
+
+    cfg = replace(QWEN35_27B, n_layers=4, vocab=8192, max_pos=512, kv_blocks=2048)
+    seed = 55
+    t0 = time.time()
+    model = Model.synth(dev, cfg, seed)
+    rng = np.random.default_rng(300)
+    trunk = rng.integers(0, cfg.vocab, 300)
+    suffixes = [rng.integers(0, cfg.vocab, 50) for _ in range(64)]
+    gen = 8
+    streams, logits, mism = _c5_passes(model, trunk, suffixes, gen, want_logits=True)
+    with capsys.disabled():
+        print(f"\n[config5 widths] gpu passes done ({time.time() - t0:.1f} s), verify mismatches {mism}", flush=True)
+    assert mism == 0
+    oracle = ora.Qwen35(ora.Qwen35Config(n_layers=4, vocab=cfg.vocab), seed)
+    oc = oracle.new_cache()
+    oracle.forward(trunk, oc)
+    for i in (0, 37):
+        c = oc.clone()
+        ref = oracle.forward(suffixes[i], c)
+        for k in range(gen):
+            got = logits[k][i]
+            assert rel(got, ref) < LOGIT_TOL, (i, k, rel(got, ref))
+            assert ora.argmax_first(ref) == streams[i][k], (i, k, margin(ref))
+            if k + 1 < gen:
+                ref = oracle.forward([streams[i][k]], c)
+    with capsys.disabled():
+        print(f"[config5 widths] oracle checks done ({time.time() - t0:.1f} s)", flush=True)
+    model.free()
+
+
+def test_config5_full_size_verify_is_exact(dev, capsys):
+    """Config 5 at full size (64 layers, vocab 151936): 64 requests share one
+    3968-token trunk, add 50-token suffixes and decode; every token a 4-token
+    verify chunk yields in the mixed pass equals the decode pass's token
+    (the size-independent property the continuous-batching engine relies on
+    when it accepts verified tokens)."""
+    import time
+    from dataclasses import replace
+
+    from pagoda_amd.engine import QWEN35_27B, Model
+
+    trunk_len, sfx, gen = 3968, 50, 9
+    cfg = replace(QWEN35_27B, max_pos=4096 + 64,
+                  kv_blocks=(trunk_len // 16 + 2) + 2 * 64 * ((sfx + gen + 4) // 16 + 2) + 16)
+    t0 = time.time()
+    model = Model.synth(dev, cfg, 2026)
+    rng = np.random.default_rng(5)
+    trunk = rng.integers(0, cfg.vocab, trunk_len)
+    suffixes = [rng.integers(0, cfg.vocab, sfx) for _ in range(64)]
+    streams, _, mism = _c5_passes(model, trunk, suffixes, gen)
+    with capsys.disabled():
+        print(f"\n[config5 full size] {time.time() - t0:.1f} s, verify mismatches {mism}", flush=True)
+    assert mism == 0
+    assert all(len(s) == gen for s in streams)
+    model.free()

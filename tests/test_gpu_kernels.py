@@ -77,7 +77,7 @@ def test_gdn_decode_step_config3(dev, B):
         assert rel(new_states[s], st) < TOL, s
 
 
-@pytest.mark.parametrize("B", [1, 8])
+@pytest.mark.parametrize("B", [1, 8, 32, 64])
 def test_gdn_4token_chunk_matches_sequential(dev, B):
     """4-token verify chunk == the CPU sequential recurrence, and == four
     single-token GPU steps bitwise (the state round trip through memory is
