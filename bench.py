@@ -37,6 +37,9 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+# the graph-replayed passes (off with --no-graphs: rocprofv3's kernel tracer
+# crashes the host process inside hipGraphLaunch)
+USE_GRAPHS = True
 
 
 def log(*a):
@@ -89,21 +92,23 @@ def gpu_bench(args):
         s.free()
 
     # ---- the same batch decode with each step replayed from a HIP graph ----
-    model.set_graphs(True)
-    sessions = [model.new_session() for _ in range(batch)]
-    ids, _ = model.step_ragged(sessions, prompts)
-    for _ in range(args.warmup):
-        ids, _ = model.step_ragged(sessions, [[int(t)] for t in ids])
-    dev.sync()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        ids, _ = model.step_ragged(sessions, [[int(t)] for t in ids])
-    dev.sync()
-    tok_s_graph = batch * args.steps / (time.perf_counter() - t0)
-    log(f"batch {batch} graphed: {tok_s_graph:.1f} tok/s")
-    for s in sessions:
-        s.free()
-    model.set_graphs(False)
+    tok_s_graph = None
+    if USE_GRAPHS:
+        model.set_graphs(True)
+        sessions = [model.new_session() for _ in range(batch)]
+        ids, _ = model.step_ragged(sessions, prompts)
+        for _ in range(args.warmup):
+            ids, _ = model.step_ragged(sessions, [[int(t)] for t in ids])
+        dev.sync()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            ids, _ = model.step_ragged(sessions, [[int(t)] for t in ids])
+        dev.sync()
+        tok_s_graph = batch * args.steps / (time.perf_counter() - t0)
+        log(f"batch {batch} graphed: {tok_s_graph:.1f} tok/s")
+        for s in sessions:
+            s.free()
+        model.set_graphs(False)
 
     # ---- batch 1 decode ----
     s = model.new_session()
@@ -120,8 +125,10 @@ def gpu_bench(args):
     b1_tok_s = n1 / wall1
     log(f"batch 1: {wall1 * 1e3 / n1:.2f} ms/token, {b1_tok_s:.1f} tok/s")
     s.free()
-    b1_graph = graphed_batch1(model, dev, prompts[0], args.warmup, n1)
-    log(f"batch 1 graphed: {b1_graph:.1f} tok/s")
+    b1_graph = None
+    if USE_GRAPHS:
+        b1_graph = graphed_batch1(model, dev, prompts[0], args.warmup, n1)
+        log(f"batch 1 graphed: {b1_graph:.1f} tok/s")
     c5 = None if args.no_config5 else config5(model, cfg)
     model.free()
     c1 = config1(dev)
@@ -207,28 +214,48 @@ def config1(dev):
     warm_ms = (time.perf_counter() - t0) * 1e3
     w.free()
     # the cold stream again with every decode step replayed from a HIP graph
-    model.set_graphs(True)
-    g = model.new_session()
-    ids, _ = model.step_ragged([g], [prompt])
-    tok = int(ids[0])
-    gcold = [tok]
-    for _ in range(31):
-        tok, _ = g.forward_greedy(tok)
-        gcold.append(tok)
+    gdec, gequal = None, None
+    if USE_GRAPHS:
+        model.set_graphs(True)
+        g = model.new_session()
+        ids, _ = model.step_ragged([g], [prompt])
+        tok = int(ids[0])
+        gcold = [tok]
+        for _ in range(31):
+            tok, _ = g.forward_greedy(tok)
+            gcold.append(tok)
+        for _ in range(8):
+            tok, _ = g.forward_greedy(tok)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            tok, _ = g.forward_greedy(tok)
+        gdec = round(n / (time.perf_counter() - t0), 1)
+        gequal = gcold == cold
+        g.free()
+        model.set_graphs(False)
+    # the other arithmetic of GGML matrices: f32 dequant-then-dot (the
+    # Metal-like one, matrix-core GEMVs and the paged attention kernel)
+    from pagoda_amd.engine import ARITH_DEQUANT_F32
+
+    model.set_kquant_arith(ARITH_DEQUANT_F32)
+    f = model.new_session()
+    model.step_ragged([f], [prompt])
+    tok = 1
     for _ in range(8):
-        tok, _ = g.forward_greedy(tok)
+        tok, _ = f.forward_greedy(tok)
     t0 = time.perf_counter()
     for _ in range(n):
-        tok, _ = g.forward_greedy(tok)
-    gdec_s = time.perf_counter() - t0
-    g.free()
+        tok, _ = f.forward_greedy(tok)
+    fdec = round(n / (time.perf_counter() - t0), 1)
+    f.free()
     model.free()
     out = {"prompt": 81, "gen": 32, "prefill_ms": round(prefill_ms, 3), "gen_tok_s": round(31 / gen_s, 1),
-           "decode_tok_s": round(n / dec_s, 1), "decode_tok_s_graph": round(n / gdec_s, 1),
-           "graph_ids_equal_eager": gcold == cold, "warm_fed_tokens": fed, "warm_ms": round(warm_ms, 2),
+           "arith": "cpu_q8 (candle's CPU quantized matmul, bit-equal to the CPU restatement)",
+           "decode_tok_s": round(n / dec_s, 1), "decode_tok_s_graph": gdec, "decode_tok_s_dequant_f32": fdec,
+           "graph_ids_equal_eager": gequal, "warm_fed_tokens": fed, "warm_ms": round(warm_ms, 2),
            "warm_equals_cold": warm == cold}
     log(f"config 1: prefill {prefill_ms:.2f} ms, decode {out['decode_tok_s']} tok/s "
-        f"(graphed {out['decode_tok_s_graph']}, ids equal: {gcold == cold}), warm fed {fed}, "
+        f"(graphed {gdec}, ids equal: {gequal}; dequant_f32 arithmetic {fdec}), warm fed {fed}, "
         f"warm == cold: {warm == cold}")
     return out
 
@@ -669,6 +696,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graphs", action="store_true", help="skip the graph-replayed passes (for kernel traces)")
     ap.add_argument("--roofline-only", action="store_true")
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--no-config5", action="store_true")
@@ -684,6 +712,8 @@ def main():
     ap.add_argument("--kernel-sweeps", action="store_true",
                     help="config 2 (Q4_K/Q6_K GEMV sweep) and config 3 (GDN step) kernel timings")
     args = ap.parse_args()
+    global USE_GRAPHS
+    USE_GRAPHS = not args.no_graphs
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
@@ -739,7 +769,8 @@ def main():
                                "greedy decode", "batch": args.batch, "prompt_len": 19,
                    "weight_gb": round(g["weight_gb"], 3), "algo_weight_gb_per_step": round(g["algo_gb_per_step"], 3)},
         "batch1_tok_s": round(g["batch1_tok_s"], 2),
-        "graphs": {"value": round(g["tok_s_graph"], 2), "batch1_tok_s": round(g["batch1_tok_s_graph"], 2),
+        "graphs": None if g["tok_s_graph"] is None else {
+                   "value": round(g["tok_s_graph"], 2), "batch1_tok_s": round(g["batch1_tok_s_graph"], 2),
                    "note": "the same decode steps replayed from HIP graphs (pgd_model_set_graphs), one per "
                            "launch signature; results bitwise equal to eager launches"},
         "step_ms_percentiles": g["step_ms_pct"],

@@ -140,8 +140,10 @@ int pgd_matrix_gemv_q8act_pair_dev(const pgd_matrix* a, float* ya, const pgd_mat
  * pgd_noalloc_scratch_bytes() (40 MiB) device array per GPU, held until the
  * process ends; calls no hipMalloc / hipFree. A launch needing more scratch
  * (37..64-row launches of matrices over ~41000 rows) is PGD_ERR_SHAPE before anything
- * runs. Every call on one GPU shares that array: calls that overlap on one GPU
- * (other threads, other device handles' streams) race. */
+ * runs. Every call on one GPU shares that array: a call queued on another
+ * device handle's stream than the previous call's first waits (on the GPU,
+ * through an event) for that call to finish; calls are serialized on the
+ * host. The array keeps the last call's contents. */
 size_t pgd_noalloc_scratch_bytes(void);
 int pgd_matrix_gemv_act_dev_noalloc(const pgd_matrix* m, const void* act, int nrows, float* y, int ldy,
                                     const float* res, int ldres);

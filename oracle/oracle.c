@@ -476,12 +476,22 @@ void ora_rms_zero(float* x, const float* w, int n) {
   for (int i = 0; i < n; ++i) x[i] = x[i] * inv * w[i];
 }
 
-static float silu(float x) { return x / (1.0f + expf(-x)); }       /* qwen3_5.rs:1758 */
-static float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); } /* qwen3_5.rs:1762 */
+/* e^x for the f32 paths: the double-precision exponential rounded once to
+ * f32, i.e. the correctly rounded f32 value (the reference calls the
+ * platform's f32 exp, Rust f32::exp -> libm expf, which every libm returns
+ * within one ulp of it; glibc's and macOS's expf differ from it by one ulp on
+ * a small fraction of inputs). The GPU path evaluates it the same way. */
+static float ora_expf(float x) { return (float)exp((double)x); }
+void ora_exp_rows(const float* x, int n, float* y) {
+  for (int i = 0; i < n; ++i) y[i] = ora_expf(x[i]);
+}
+
+static float silu(float x) { return x / (1.0f + ora_expf(-x)); }       /* qwen3_5.rs:1758 */
+static float sigmoidf_(float x) { return 1.0f / (1.0f + ora_expf(-x)); } /* qwen3_5.rs:1762 */
 static float softplus(float x) {                                     /* qwen3_5.rs:1766-1774 */
   if (x > 20.0f) return x;
-  if (x < -20.0f) return expf(x);
-  return logf(1.0f + expf(x));
+  if (x < -20.0f) return ora_expf(x);
+  return logf(1.0f + ora_expf(x));
 }
 
 /* pagoda-hf/src/qwen3_5.rs:1747-1756 (rms_gated). */
@@ -595,8 +605,8 @@ void ora_gdn_step(const float* conv_out, const float* a, const float* b, const f
     float scale = sqrtf((float)k_dim);
     for (int i = 0; i < v_heads * k_dim; ++i) qh[i] /= scale;
     for (int h = 0; h < v_heads; ++h) {
-      float g = -expf(a_log[h]) * softplus(a[t * v_heads + h] + dt_bias[h]);
-      float decay = expf(g);
+      float g = -ora_expf(a_log[h]) * softplus(a[t * v_heads + h] + dt_bias[h]);
+      float decay = ora_expf(g);
       float beta = sigmoidf_(b[t * v_heads + h]);
       const float* qv = qh + (size_t)h * k_dim;
       const float* kv = kh + (size_t)h * k_dim;
@@ -648,7 +658,7 @@ void ora_attn_decode(const float* q, const float* k_cache, const float* v_cache,
     }
     float sum = 0.0f;
     for (int p = 0; p < len; ++p) {
-      scores[p] = expf(scores[p] - max_s);
+      scores[p] = ora_expf(scores[p] - max_s);
       sum += scores[p];
     }
     float* oh = out + (size_t)h * hd;

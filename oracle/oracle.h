@@ -145,6 +145,8 @@ void ora_qwen2_set_kquant_mode(ora_qwen2* m, int mode);
 /* greedy tie rule of the engine sampler: first max over finite values
  * (pagoda/src/sampler.rs:59-69). */
 uint32_t ora_argmax_first(const float* x, int n);
+/* y[i] = e^x[i] as the f32 paths evaluate it: the double exponential rounded once. */
+void ora_exp_rows(const float* x, int n, float* y);
 
 int ora_num_threads(void);
 

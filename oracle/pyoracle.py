@@ -96,6 +96,7 @@ def lib():
         _lib.ora_q8_0_quantize_act.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
         _lib.ora_q8_0_vec_dot.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
         _lib.ora_num_threads.restype = C.c_int
+        _lib.ora_exp_rows.argtypes = [C.c_void_p, C.c_int, C.c_void_p]
         _lib.ora_rope_cos_sin.argtypes = [C.c_int, C.c_int, C.c_float, C.c_void_p, C.c_void_p]
     return _lib
 
@@ -196,6 +197,14 @@ def q8k_quantize(x: np.ndarray) -> np.ndarray:
     out = np.zeros(kq_blocks(x.size) * 292, np.uint8)
     lib().ora_q8k_quantize(_p(x), x.size, _p(out))
     return out.view(Q8K_DTYPE)
+
+
+def exp_f32(x: np.ndarray) -> np.ndarray:
+    """e^x as the oracle's f32 paths evaluate it (double exponential rounded once)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().ora_exp_rows(_p(x), int(x.size), _p(y))
+    return y
 
 
 def kq_vec_dot_q8k(fmt: int, blocks: np.ndarray, n_out: int, n_in: int, q8k: np.ndarray) -> np.ndarray:

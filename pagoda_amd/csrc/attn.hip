@@ -468,6 +468,102 @@ AttnPlan attn_plan_view(const int* host, const int* dev) {
   return p;
 }
 
+// Attention in the CPU path's exact operation order, one 256-thread
+// workgroup per (row, head): score_p = (sum_i q_i k_pi, i in order) / sqrt(hd)
+// (one thread per position); the max; e_p = exp(score_p - max);
+// sum = e_0 + e_1 + ... in position order; w_p = e_p / sum;
+// out_i = sum_p w_p v_pi in position order, one thread per dimension over V
+// rows staged in LDS a chunk at a time (FullAttn::forward / Qwen2 attend:
+// pagoda-hf/src/qwen3_5.rs:1433-1475, qwen2_gguf.rs:252-266). Bit-equal to
+// that order; used by the Qwen2 arithmetic that reproduces the reference CPU
+// path (candle's quantized matmul). Scores live in LDS: the context is at
+// most kExactMax positions.
+constexpr int kExactMax = 32256;
+constexpr int kExactThreads = 256;
+constexpr int kExactChunkFloats = 8192;  // V rows staged per round: 32 KiB
+__global__ __launch_bounds__(kExactThreads) void attn_exact_kernel(const float* __restrict__ q,
+                                                                   float* __restrict__ out, AttnLayout L, RowMeta m) {
+  extern __shared__ float sc[];  // [len] scores, then weights | V chunk [kExactChunkFloats / hd][hd]
+  __shared__ float qs[256];
+  __shared__ float red[kExactThreads / 64];
+  __shared__ float s_sum;
+  const int r = blockIdx.y, h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int hd = L.head_dim, kvh = h / (L.heads / L.kv_heads);
+  const int seq = m.seq_of_row[r], len = m.pos_of_row[r] + 1;
+  const int* bt = m.block_tables + (size_t)seq * m.max_blocks;
+  float* vs = sc + m.max_blocks * L.block;
+  const float* qh = q + ((size_t)r * L.heads + h) * hd;
+  for (int i = tid; i < hd; i += kExactThreads) qs[i] = qh[i];
+  __syncthreads();
+  const float scale = sqrtf((float)hd);
+  float mx = -INFINITY;
+  for (int p = tid; p < len; p += kExactThreads) {
+    const float* kr = L.k_pool + (((size_t)bt[p / L.block] * L.kv_heads + kvh) * L.block + (p % L.block)) * hd;
+    float dot = 0.0f;
+    for (int i = 0; i < hd; i += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kr + i);
+      dot += qs[i] * k4.x;
+      dot += qs[i + 1] * k4.y;
+      dot += qs[i + 2] * k4.z;
+      dot += qs[i + 3] * k4.w;
+    }
+    const float s = dot / scale;
+    sc[p] = s;
+    mx = fmaxf(mx, s);
+  }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red[wv] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < kExactThreads / 64; ++w) mx = fmaxf(mx, red[w]);
+  for (int p = tid; p < len; p += kExactThreads) sc[p] = exp_cr(sc[p] - mx);
+  __syncthreads();
+  if (tid == 0) {
+    float sum = 0.0f;
+    for (int p = 0; p < len; ++p) sum += sc[p];
+    s_sum = sum;
+  }
+  __syncthreads();
+  const float sum = s_sum;
+  for (int p = tid; p < len; p += kExactThreads) sc[p] = sc[p] / sum;
+  float acc = 0.0f;
+  const int chunk = kExactChunkFloats / hd;
+  for (int p0 = 0; p0 < len; p0 += chunk) {
+    const int n = min(chunk, len - p0);
+    __syncthreads();  // the weights are written / the previous chunk is consumed
+    for (int e = tid * 4; e < n * hd; e += kExactThreads * 4) {
+      const int p = p0 + e / hd, i = e % hd;
+      const float* vr = L.v_pool + (((size_t)bt[p / L.block] * L.kv_heads + kvh) * L.block + (p % L.block)) * hd;
+      *reinterpret_cast<float4*>(vs + e) = *reinterpret_cast<const float4*>(vr + i);
+    }
+    __syncthreads();
+    if (tid < hd)
+      for (int t = 0; t < n; ++t) acc += sc[p0 + t] * vs[t * hd + tid];
+  }
+  if (tid < hd) out[((size_t)r * L.heads + h) * hd + tid] = acc;
+}
+
+void attn_exact(const float* q, float* out, const AttnLayout& L, const RowMeta& m, int rows, int max_len,
+                hipStream_t s) {
+  PGD_CHECK(L.kv_heads > 0 && L.heads % L.kv_heads == 0, kErrShape, "heads must be a multiple of kv_heads");
+  PGD_CHECK(L.head_dim % 4 == 0 && L.head_dim <= 256, kErrShape, "exact-order attention: head_dim <= 256");
+  PGD_CHECK(max_len <= kExactMax && max_len == m.max_blocks * L.block, kErrShape,
+            "exact-order attention holds at most " + std::to_string(kExactMax) + " positions");
+  if (rows <= 0) return;
+  const size_t lds = ((size_t)max_len + kExactChunkFloats) * sizeof(float);
+  if (lds > 64 * 1024) {
+    static bool set = false;
+    if (!set) {
+      PGD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_exact_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)((kExactMax + kExactChunkFloats) * sizeof(float))));
+      set = true;
+    }
+  }
+  hipLaunchKernelGGL(attn_exact_kernel, dim3(L.heads, rows), dim3(kExactThreads), lds, s, q, out, L, m);
+  PGD_HIP(hipGetLastError());
+}
+
 void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m,
                  const AttnPlan& plan, int rows, hipStream_t s, const a8act::Dst* act) {
   PGD_CHECK(L.kv_heads > 0 && L.heads % L.kv_heads == 0, kErrShape, "heads must be a multiple of kv_heads");

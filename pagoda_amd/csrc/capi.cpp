@@ -452,21 +452,30 @@ constexpr size_t kScratchBytes = (size_t)40 << 20;
 // hipGetSymbolAddress on each device
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
+// One GPU's copy of scratch and its last user: calls queued on different
+// streams are ordered through `done`, an event recorded after each call, so
+// a call on another stream never overwrites partial sums still being read.
+struct ScratchSlot {
+  uint8_t* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+};
 std::mutex g_scratch_mu;
-std::map<int, uint8_t*> g_scratch_ptr;  // device ordinal -> that GPU's copy of scratch
+std::map<int, ScratchSlot> g_scratch;  // device ordinal -> that GPU's slot
 
-// the current device's copy of scratch, looked up once per device
-uint8_t* scratch_on_current_device() {
+// the current device's slot, set up once per device
+ScratchSlot& scratch_on_current_device() {
   int dev = 0;
   PGD_HIP(hipGetDevice(&dev));
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  auto it = g_scratch_ptr.find(dev);
-  if (it != g_scratch_ptr.end()) return it->second;
+  auto it = g_scratch.find(dev);
+  if (it != g_scratch.end()) return it->second;
   void* p = nullptr;
   hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   PGD_CHECK(e == hipSuccess && p, kErrState, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
-  g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
-  return static_cast<uint8_t*>(p);
+  ScratchSlot sl;
+  sl.ptr = static_cast<uint8_t*>(p);
+  PGD_HIP(hipEventCreateWithFlags(&sl.done, hipEventDisableTiming));
+  return g_scratch[dev] = sl;
 }
 
 struct ArenaScope {
@@ -497,9 +506,16 @@ int pgd_matrix_gemv_act_dev_noalloc(const pgd_matrix* m, const void* act, int nr
                   " matrix need " + std::to_string(need) + " bytes of scratch, above the fixed " +
                   std::to_string(kScratchBytes >> 20) + " MiB");
     DeviceScope scope(m->dev);
-    ArenaScope arena(scratch_on_current_device(), kScratchBytes);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ScratchSlot& sl = scratch_on_current_device();
+    hipStream_t st = m->dev->stream;
+    // the previous call was queued on another stream: wait for it on the GPU
+    if (sl.last && sl.last != st) PGD_HIP(hipStreamWaitEvent(st, sl.done, 0));
+    ArenaScope arena(sl.ptr, kScratchBytes);
     A8Act a = a8_act_view(const_cast<void*>(act), nrows, m->m.n_in);
-    qmat_gemv_a8(m->m, a, y, ldy, res, ldres, m->dev->stream);
+    qmat_gemv_a8(m->m, a, y, ldy, res, ldres, st);
+    PGD_HIP(hipEventRecord(sl.done, st));
+    sl.last = st;
   });
 }
 

@@ -127,7 +127,12 @@ __device__ inline float group_sum(float v, int width) {
   return v;
 }
 
-__device__ inline float silu_f(float x) { return x / (1.0f + expf(-x)); }
-__device__ inline float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+// e^x correctly rounded to f32: the double-precision exponential (error well
+// below one double ulp) rounded once, so the result is the f32 nearest to
+// e^x except when e^x lies within ~2^-29 f32 ulp of a rounding midpoint. The
+// CPU restatement evaluates it the same way, so both sides agree bit for bit.
+__device__ inline float exp_cr(float x) { return (float)exp((double)x); }
+__device__ inline float silu_f(float x) { return x / (1.0f + exp_cr(-x)); }
+__device__ inline float sigmoid_f(float x) { return 1.0f / (1.0f + exp_cr(-x)); }
 
 }  // namespace pgd

@@ -18,11 +18,18 @@
 //   Q4_K: d_w d_x sum_j sc_j dot_j - dmin_w d_x sum_j m_j bsum_j
 //   Q6_K: d_w d_x sum_j sc_j (dot_j(q) - 32 bsum_j)       (q = 6-bit code)
 //   Q8_0: sumi d_w d_x;  Q5_0: (dot(q) - 16 sum(x_q)) d_w d_x   (q = 5-bit code)
-// The f32 terms are added per wave over its blocks, then over the waves
-// in wave order: a fixed order for a given shape, whatever the row count, so
-// batched rows are bitwise equal to single-row launches.
+// The float arithmetic is GGML's scalar one, term for term and in its order,
+// so every output is bit-equal to the CPU restatement: the integer products
+// of a 256-block are kept in eight residue classes (element index mod 8,
+// GGML's aux32[8] lanes), each scaled by d = d_w d_x and added into its own
+// running sum block after block, the Q4_K min terms into a ninth, and the
+// eight sums are added at the end; 32-blocks add (sumi d_w) d_x block after
+// block. Waves compute their blocks' terms in parallel (exact integers, one
+// rounding per product) and leave them in LDS; one lane per output then adds
+// them in block order. The per-row arithmetic does not depend on the number
+// of rows, so batched rows are bitwise equal to single-row launches.
 //
-// Work split: one workgroup of NW waves (4, 8 or 16, from the number of K
+// Work split: one workgroup of NW waves (4 or 8, from the number of K
 // blocks) per 32-row tile of the weight matrix; wave w takes K blocks w,
 // w + NW, ... (256-element super-blocks, or 32-weight blocks). Weights are
 // read once per launch of up to RB activation rows.
@@ -44,30 +51,37 @@ __device__ inline int dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// activations in LDS: q [RB][Kp] i8 | d [RB][nb] f32 | sums [RB][nb][SUMS] i32
+// activations in LDS: q [RB][Kp] i8 | d [RB][nb] f32 | sums [RB][nb][SUMS] i32,
+// then the block terms [NM][RB][nb][32 outputs][NT] f32 (NT: 9 for Q4_K, the
+// eight residue classes and the min term; 8 for Q6_K; 1 for 32-blocks)
 template <int FMT, int RB, int NW>
 struct ActLds {
   static constexpr bool K256 = FMT == FMT_Q4K || FMT == FMT_Q6K;
   static constexpr int BLK = K256 ? 256 : 32;
   static constexpr int SUMS = K256 ? 16 : 1;
+  static constexpr int NT = FMT == FMT_Q4K ? 9 : FMT == FMT_Q6K ? 8 : 1;
   int Kp, nb;
   int8_t* q;
   float* d;
   int* s;
-  float* red;  // [NM][NW][RB][32] wave partials, over the activations once the dots are done
+  float* t;
+  __host__ __device__ static size_t act_bytes(int nbh) {
+    return ((((size_t)RB * nbh * BLK + 15) & ~(size_t)15) + (size_t)RB * nbh * 4 + (size_t)RB * nbh * SUMS * 4 + 15) &
+           ~(size_t)15;
+  }
   __device__ ActLds(char* base, int n_in) {
     nb = (n_in + BLK - 1) / BLK;
     Kp = nb * BLK;
     q = reinterpret_cast<int8_t*>(base);
     d = reinterpret_cast<float*>(base + (((size_t)RB * Kp + 15) & ~(size_t)15));
     s = reinterpret_cast<int*>(d + RB * nb);
-    red = reinterpret_cast<float*>(base);
+    t = reinterpret_cast<float*>(base + act_bytes(nb));
   }
+  // term slot of matrix m, row r, block b, tile output n
+  __device__ float* term(int m, int r, int b, int n) const { return t + ((((size_t)m * RB + r) * nb + b) * 32 + n) * NT; }
   static size_t bytes(int n_in, int nm) {
-    const int nbh = (n_in + BLK - 1) / BLK, Kph = nbh * BLK;
-    const size_t act = (((size_t)RB * Kph + 15) & ~(size_t)15) + (size_t)RB * nbh * 4 + (size_t)RB * nbh * SUMS * 4;
-    const size_t red = (size_t)nm * NW * RB * 32 * 4;
-    return act > red ? act : red;
+    const int nbh = (n_in + BLK - 1) / BLK;
+    return act_bytes(nbh) + (size_t)nm * RB * nbh * 32 * NT * 4;
   }
 };
 
@@ -177,14 +191,16 @@ __device__ void quantize_rows(const float* __restrict__ x, int ldx, int rows, in
   }
 }
 
-// ---- per-format block dots of one wave over its blocks ----------------------
-// acc[m][r][i]: matrix m (0, or 1 = SwiGLU up), activation row r, the lane's
-// i-th output row of the tile (see each format's row map).
+// ---- per-format block terms of one wave over its blocks -------------------
 
-// Q4_K: lane l = output row l >> 1, half h = l & 1 of each 32-byte run.
+// byte b of a dword, alone in its byte lane (for products of one element)
+__device__ inline uint32_t byte_lane(uint32_t v, int b) { return v & (0xFFu << (8 * b)); }
+
+// Q4_K: lane l = output row l >> 1, half h = l & 1 of each 32-byte run. The
+// lane's bytes 16 h + 4 i + k of a run hold elements of residue 4 (i & 1) + k
+// (mod 8) in both nibbles.
 template <int RB, int NW, int NM>
-__device__ void dots_q4k(const GemvArgs& a, int tile, int rows, const ActLds<FMT_Q4K, RB, NW>& L,
-                         float (&acc)[NM][RB][1]) {
+__device__ void dots_q4k(const GemvArgs& a, int tile, int rows, const ActLds<FMT_Q4K, RB, NW>& L) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int jr = lane >> 1, h = lane & 1, row = tile * 32 + jr;
   for (int sb = w; sb < a.nsb; sb += NW) {
@@ -214,11 +230,11 @@ __device__ void dots_q4k(const GemvArgs& a, int tile, int rows, const ActLds<FMT
         }
       }
       const float dw = f16_to_f32(hdr.x & 0xffffu), dmin = f16_to_f32(hdr.x >> 16);
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        if (r >= rows) break;
+      for (int r = 0; r < rows; ++r) {
         const int8_t* xq = L.q + (size_t)r * L.Kp + sb * 256;
-        int isum = 0;
+        int aux[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) aux[l] = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           if (j >= nj) break;
@@ -226,32 +242,42 @@ __device__ void dots_q4k(const GemvArgs& a, int tile, int rows, const ActLds<FMT
           const uint4 xh = *reinterpret_cast<const uint4*>(xq + 64 * j + 32 + 16 * h);
           const uint32_t qw[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
           const uint32_t lw[4] = {xl.x, xl.y, xl.z, xl.w}, hw[4] = {xh.x, xh.y, xh.z, xh.w};
-          int dl = 0, dh = 0;
+          int tl[8], th[8];
+#pragma unroll
+          for (int l = 0; l < 8; ++l) tl[l] = th[l] = 0;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            dl = dot4(qw[i] & 0x0F0F0F0Fu, lw[i], dl);
-            dh = dot4((qw[i] >> 4) & 0x0F0F0F0Fu, hw[i], dh);
+            const uint32_t lo = qw[i] & 0x0F0F0F0Fu, hi = (qw[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              tl[4 * (i & 1) + k] = dot4(byte_lane(lo, k), lw[i], tl[4 * (i & 1) + k]);
+              th[4 * (i & 1) + k] = dot4(byte_lane(hi, k), hw[i], th[4 * (i & 1) + k]);
+            }
           }
-          isum += sc[2 * j] * dl + sc[2 * j + 1] * dh;
+#pragma unroll
+          for (int l = 0; l < 8; ++l) aux[l] += sc[2 * j] * tl[l] + sc[2 * j + 1] * th[l];
         }
-        isum += __shfl_xor(isum, 1, 64);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) aux[l] += __shfl_xor(aux[l], 1, 64);
         const int* bs = L.s + (r * L.nb + sb) * 16;
         int msum = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) msum += mn[k] * (bs[2 * k] + bs[2 * k + 1]);
+        for (int k = 0; k < 16; ++k) msum += bs[k] * mn[k / 2];
         const float d8 = L.d[r * L.nb + sb];
-        acc[m][r][0] += (dw * d8) * (float)isum;
-        acc[m][r][0] -= (dmin * d8) * (float)msum;
+        const float d = dw * d8, dm = dmin * d8;
+        float* t = L.term(m, r, sb, jr);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t[4 * h + c] = d * (float)aux[4 * h + c];
+        if (h == 0) t[8] = dm * (float)msum;
       }
     }
   }
 }
 
 // Q6_K: lane l = dword k = l >> 4 of row 16 hh + (l & 15), for row halves hh
-// 0 and 1 (acc index hh).
+// 0 and 1. The lane's elements all have residue 4 (k & 1) + c, c = 0..3.
 template <int RB, int NW, int NM>
-__device__ void dots_q6k(const GemvArgs& a, int tile, int rows, const ActLds<FMT_Q6K, RB, NW>& L,
-                         float (&acc)[NM][RB][2]) {
+__device__ void dots_q6k(const GemvArgs& a, int tile, int rows, const ActLds<FMT_Q6K, RB, NW>& L) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int k = lane >> 4, jr = lane & 15;
   for (int sb = w; sb < a.nsb; sb += NW) {
@@ -265,50 +291,52 @@ __device__ void dots_q6k(const GemvArgs& a, int tile, int rows, const ActLds<FMT
       for (int hh = 0; hh < 2; ++hh) {
         const int row = tile * 32 + 16 * hh + jr;
         const float dw = f16_to_f32(reinterpret_cast<const uint16_t*>(p3)[q6k_d_off(row, sb, a.nsb)]);
-        int iw[RB];
-#pragma unroll
-        for (int r = 0; r < RB; ++r) iw[r] = 0;
+        // codes - 32 (signed bytes) of elements 4k + 16 mm + (0..3) of half u,
+        // mm = 0..7, and the sub-block scales
+        uint32_t v[2][8];
+        int sc[2][8];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          if (sb * 256 + 128 * u >= a.n_in) break;
-          const uint4 ql = *reinterpret_cast<const uint4*>(p0 + q6k_ql_off(row, 64 * (2 * sb + u) + 4 * k, a.nsb));
-          const u2v qh = *reinterpret_cast<const u2v*>(p1 + q6k_qh_off(row, 32 * (2 * sb + u) + 4 * k, a.nsb));
-          const u2v scw = *reinterpret_cast<const u2v*>(p2 + q6k_sc_off(row, 16 * sb + 8 * u, a.nsb));
-          // codes of elements 4k + 16 m + (0..3) of this half, m = 0..7
+          const bool live = sb * 256 + 128 * u < a.n_in;
+          const uint4 ql = live ? *reinterpret_cast<const uint4*>(p0 + q6k_ql_off(row, 64 * (2 * sb + u) + 4 * k, a.nsb))
+                                : make_uint4(0, 0, 0, 0);
+          const u2v qh = live ? *reinterpret_cast<const u2v*>(p1 + q6k_qh_off(row, 32 * (2 * sb + u) + 4 * k, a.nsb))
+                              : (u2v){0u, 0u};
+          const u2v scw = live ? *reinterpret_cast<const u2v*>(p2 + q6k_sc_off(row, 16 * sb + 8 * u, a.nsb))
+                               : (u2v){0u, 0u};
           const uint32_t qlw[4] = {ql.x, ql.y, ql.z, ql.w};
-          uint32_t v[8];
 #pragma unroll
           for (int mm = 0; mm < 8; ++mm) {
             const uint32_t lo = (qlw[mm & 3] >> (mm >= 4 ? 4 : 0)) & 0x0F0F0F0Fu;
             const uint32_t hq = (mm & 1) ? qh.y : qh.x;
             const uint32_t hb = (hq >> (2 * (mm >> 1))) & 0x03030303u;
-            v[mm] = lo | (hb << 4);
-          }
-          int sc[8];
-#pragma unroll
-          for (int mm = 0; mm < 8; ++mm) sc[mm] = (int)(int8_t)(((mm < 4 ? scw.x : scw.y) >> (8 * (mm & 3))) & 255u);
-#pragma unroll
-          for (int r = 0; r < RB; ++r) {
-            if (r >= rows) break;
-            const int8_t* xq = L.q + (size_t)r * L.Kp + sb * 256 + 128 * u + 4 * k;
-            int part = 0;
-#pragma unroll
-            for (int mm = 0; mm < 8; ++mm)
-              part += sc[mm] * dot4(v[mm], *reinterpret_cast<const uint32_t*>(xq + 16 * mm), 0);
-            // the four dword lanes of a row, then the -32 offset of the codes
-            part += __shfl_xor(part, 16, 64);
-            part += __shfl_xor(part, 32, 64);
-            const int* bs = L.s + (r * L.nb + sb) * 16 + 8 * u;
-            int corr = 0;
-#pragma unroll
-            for (int mm = 0; mm < 8; ++mm) corr += sc[mm] * bs[mm];
-            iw[r] += part - 32 * corr;
+            v[u][mm] = (((lo | (hb << 4)) | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+            sc[u][mm] = (int)(int8_t)(((mm < 4 ? scw.x : scw.y) >> (8 * (mm & 3))) & 255u);
           }
         }
+        const int nu = sb * 256 + 128 < a.n_in ? 2 : 1;
+        for (int r = 0; r < rows; ++r) {
+          int iw[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
-          if (r >= rows) break;
-          acc[m][r][hh] += (dw * L.d[r * L.nb + sb]) * (float)iw[r];
+          for (int u = 0; u < 2; ++u) {
+            if (u >= nu) break;
+            const int8_t* xq = L.q + (size_t)r * L.Kp + sb * 256 + 128 * u + 4 * k;
+#pragma unroll
+            for (int mm = 0; mm < 8; ++mm) {
+              const uint32_t xw = *reinterpret_cast<const uint32_t*>(xq + 16 * mm);
+#pragma unroll
+              for (int c = 0; c < 4; ++c) iw[c] += sc[u][mm] * dot4(byte_lane(v[u][mm], c), xw, 0);
+            }
+          }
+          // dword lanes k and k ^ 2 hold the same residues
+#pragma unroll
+          for (int c = 0; c < 4; ++c) iw[c] += __shfl_xor(iw[c], 32, 64);
+          if (k < 2) {
+            const float d = dw * L.d[r * L.nb + sb];
+            float* t = L.term(m, r, sb, 16 * hh + jr);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) t[4 * k + c] = d * (float)iw[c];
+          }
         }
       }
     }
@@ -318,7 +346,7 @@ __device__ void dots_q6k(const GemvArgs& a, int tile, int rows, const ActLds<FMT
 // Q8_0 / Q5_0 (row-major planes, no row padding): lane l = output row l >> 1,
 // half h = l & 1 of each block.
 template <int FMT, int RB, int NW, int NM>
-__device__ void dots_q32(const GemvArgs& a, int tile, int rows, const ActLds<FMT, RB, NW>& L, float (&acc)[NM][RB][1]) {
+__device__ void dots_q32(const GemvArgs& a, int tile, int rows, const ActLds<FMT, RB, NW>& L) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int h = lane & 1;
   const int row = min(tile * 32 + (lane >> 1), a.n_out - 1);
@@ -377,7 +405,7 @@ __device__ void dots_q32(const GemvArgs& a, int tile, int rows, const ActLds<FMT
           sumi += __shfl_xor(sumi, 1, 64);
           sumi -= 16 * L.s[r * L.nb + b];
         }
-        acc[m][r][0] += (float)sumi * dw * L.d[r * L.nb + b];
+        if (h == 0) L.term(m, r, b, lane >> 1)[0] = (float)sumi * dw * L.d[r * L.nb + b];
       }
     }
   }
@@ -420,52 +448,40 @@ __device__ inline void prefetch_tile(const GemvArgs& a, bool second, int tile, i
   }
 }
 
-// One 32-row weight tile of a launch: block dots over the activations
-// already quantized in L, wave partials added in wave order, epilogue.
+// One 32-row weight tile of a launch: block terms over the activations
+// already quantized in L, then one lane per (row, output) adds them in block
+// order (GGML's scalar sums) and applies the epilogue.
 template <int FMT, int RB, int NW, int EPI>
 __device__ void q8_tile(const GemvArgs& a, int tile, int rows, const ActLds<FMT, RB, NW>& L) {
   constexpr int NM = EPI == EPI_SWIGLU ? 2 : 1;
-  constexpr int NI = FMT == FMT_Q6K ? 2 : 1;  // output rows per lane
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  float acc[NM][RB][NI];
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-#pragma unroll
-      for (int i = 0; i < NI; ++i) acc[m][r][i] = 0.0f;
-  if constexpr (FMT == FMT_Q4K) dots_q4k<RB, NW, NM>(a, tile, rows, L, acc);
-  else if constexpr (FMT == FMT_Q6K) dots_q6k<RB, NW, NM>(a, tile, rows, L, acc);
-  else dots_q32<FMT, RB, NW, NM>(a, tile, rows, L, acc);
-  // wave partials -> LDS [m][w][r][row] (over the activations: wait for every wave's dots)
+  if constexpr (FMT == FMT_Q4K) dots_q4k<RB, NW, NM>(a, tile, rows, L);
+  else if constexpr (FMT == FMT_Q6K) dots_q6k<RB, NW, NM>(a, tile, rows, L);
+  else dots_q32<FMT, RB, NW, NM>(a, tile, rows, L);
   __syncthreads();
-#pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      if (r >= rows) break;
-      float* red = L.red + ((m * NW + w) * RB + r) * 32;
-      if constexpr (FMT == FMT_Q6K) {
-        if ((lane >> 4) == 0) {
-          red[lane & 15] = acc[m][r][0];
-          red[16 + (lane & 15)] = acc[m][r][1];
-        }
-      } else if ((lane & 1) == 0) {
-        red[lane >> 1] = acc[m][r][0];
-      }
-    }
-  __syncthreads();
-  if (w != 0 || lane >= 32) return;
-  const int n = tile * 32 + lane;
-  if (n >= a.n_out) return;
-  for (int r = 0; r < rows; ++r) {
+  for (int t = threadIdx.x; t < rows * 32; t += blockDim.x) {
+    const int r = t >> 5, j = t & 31, n = tile * 32 + j;
+    if (n >= a.n_out) continue;
     float v[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const float* red = L.red + (m * NW * RB + r) * 32 + lane;
-      v[m] = red[0];
+      if constexpr (FMT == FMT_Q4K || FMT == FMT_Q6K) {
+        // vec_dot_q4_K_q8_K / vec_dot_q6_K_q8_K: sums[8] over the blocks, the
+        // min terms subtracted from sumf block by block, then sumf += sums[l]
+        float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, sumf = 0.0f;
+        for (int b = 0; b < L.nb; ++b) {
+          const float* tb = L.term(m, r, b, j);
 #pragma unroll
-      for (int ww = 1; ww < NW; ++ww) v[m] += red[ww * RB * 32];
+          for (int l = 0; l < 8; ++l) sums[l] += tb[l];
+          if constexpr (FMT == FMT_Q4K) sumf -= tb[8];
+        }
+#pragma unroll
+        for (int l = 0; l < 8; ++l) sumf += sums[l];
+        v[m] = sumf;
+      } else {
+        float sumf = 0.0f;
+        for (int b = 0; b < L.nb; ++b) sumf += L.term(m, r, b, j)[0];
+        v[m] = sumf;
+      }
     }
     const size_t o = (size_t)r * a.ldy + n;
     if constexpr (EPI == EPI_STORE) a.y[o] = v[0];
@@ -479,6 +495,12 @@ __device__ inline void keep(const GemvArgs& a, int rows, uint32_t sink) {
   if (rows < 0 && sink == 0x9e3779b9u) a.y[0] = 0.0f;
 }
 
+// K blocks of a row in units of 256 weights (4 Q8_0 / Q5_0 blocks)
+template <int FMT>
+__host__ __device__ inline int k_blocks(const GemvArgs& a) {
+  return (FMT == FMT_Q4K || FMT == FMT_Q6K) ? a.nsb : a.n_in / 128;
+}
+
 template <int FMT, int RB, int NW, int EPI>
 __global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(GemvArgs a, int rows) {
   extern __shared__ __attribute__((aligned(16))) char dsm[];
@@ -486,7 +508,7 @@ __global__ __launch_bounds__(64 * NW) void q8_gemv_kernel(GemvArgs a, int rows) 
   // the cache by the time the wave reaches them (measured: the 4864-wide down
   // projection 13.2 -> 11.0 us for Q6_K; tiles of one block per wave lost)
   uint32_t sink = 0;
-  if constexpr (NW == 16) {
+  if (NW == 8 && k_blocks<FMT>(a) > 8) {
     prefetch_tile<FMT>(a, false, blockIdx.x, 64 * NW, sink);
     if constexpr (EPI == EPI_SWIGLU) prefetch_tile<FMT>(a, true, blockIdx.x, 64 * NW, sink);
   }
@@ -508,7 +530,7 @@ __global__ __launch_bounds__(64 * NW) void q8_pair_kernel(GemvArgs a, GemvArgs b
   extern __shared__ __attribute__((aligned(16))) char dsm[];
   const bool first = (int)blockIdx.x < split;
   uint32_t sink = 0;
-  if constexpr (NW == 16) {
+  if (NW == 8 && k_blocks<FMT>(a) > 8) {
     if (first) prefetch_tile<FMT>(a, false, blockIdx.x, 64 * NW, sink);
     else prefetch_tile<FMT2>(b, false, blockIdx.x - split, 64 * NW, sink);
   }
@@ -547,21 +569,19 @@ void launch_q8(GemvArgs a, int nrows, hipStream_t s) {
   }
 }
 
-// waves per workgroup from the K blocks of a row (a shape property, so every
-// row count of one matrix sums in the same order)
+// waves per workgroup from the K blocks of a row (the sums do not depend on
+// it: every block's terms are added in block order by one lane)
 template <int FMT, int RB, int EPI>
 void launch_waves(const GemvArgs& a, int nrows, hipStream_t s) {
-  const int kb = (FMT == FMT_Q4K || FMT == FMT_Q6K) ? a.nsb : a.n_in / 128;  // in units of 4 Q8_0 blocks
-  if (kb <= 4) return launch_q8<FMT, RB, 4, EPI>(a, nrows, s);
-  if (kb <= 8) return launch_q8<FMT, RB, 8, EPI>(a, nrows, s);
-  launch_q8<FMT, RB, 16, EPI>(a, nrows, s);
+  if (k_blocks<FMT>(a) <= 4) return launch_q8<FMT, RB, 4, EPI>(a, nrows, s);
+  launch_q8<FMT, RB, 8, EPI>(a, nrows, s);
 }
 
 // LDS of one launch of RB rows: the quantized rows, or the wave partials of
 // the widest (16-wave) workgroup, whichever is larger
 template <int FMT, int RB>
 size_t lds_need(int n_in, int nm) {
-  return ActLds<FMT, RB, 16>::bytes(n_in, nm);
+  return ActLds<FMT, RB, 8>::bytes(n_in, nm);
 }
 
 // rows per launch: decode steps take 1..8; prefills 16 at a time (weights
@@ -617,12 +637,11 @@ void launch_pair_q8(GemvArgs a, GemvArgs b, int nrows, hipStream_t s) {
 // matrices: they have the same K)
 template <int FMT, int FMT2>
 void pair_rows(const GemvArgs& a, const GemvArgs& b, int nrows, hipStream_t s) {
-  const int kb = (FMT == FMT_Q4K || FMT == FMT_Q6K) ? a.nsb : a.n_in / 128;
+  const int kb = k_blocks<FMT>(a);
   auto go = [&](auto rb) {
     constexpr int RB = decltype(rb)::value;
     if (kb <= 4) return launch_pair_q8<FMT, FMT2, RB, 4>(a, b, nrows, s);
-    if (kb <= 8) return launch_pair_q8<FMT, FMT2, RB, 8>(a, b, nrows, s);
-    launch_pair_q8<FMT, FMT2, RB, 16>(a, b, nrows, s);
+    launch_pair_q8<FMT, FMT2, RB, 8>(a, b, nrows, s);
   };
   const size_t cap = 160 * 1024;
   auto fits = [&](auto rb) {

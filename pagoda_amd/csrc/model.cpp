@@ -687,7 +687,12 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
           attn_decode(w.D, w.F, nullptr, al, rm, ap, rows, st, &dst);
           post_in = qmat_gemv_a8_res_norm(L.o, act, w.x, H, L.post_norm, eps, w.act3, st);
         } else {
-          attn_decode(w.D, nullptr, w.E, al, rm, ap, rows, st);
+          // candle's CPU arithmetic: attention in the CPU path's order too, so
+          // the whole forward is bit-equal to the reference restatement (its
+          // LDS holds the block tables' capacity, a launch argument that
+          // changes only with max_blocks)
+          if (m.q8act) attn_exact(w.D, w.E, al, rm, rows, (int)max_blocks * c.kv_block, st);
+          else attn_decode(w.D, nullptr, w.E, al, rm, ap, rows, st);
           gemv(L.o, w.E, c.heads * c.head_dim, rows, w.x, H, w.x, H);
         }
       }

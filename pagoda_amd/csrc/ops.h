@@ -133,6 +133,12 @@ struct AttnPlan {
 void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, const int* block_tables,
                      int max_blocks, int block, int group, std::vector<int>& out);
 AttnPlan attn_plan_view(const int* host, const int* dev);
+// The same attention in the CPU path's exact operation order (sequential dot,
+// sum and weighted sum; exp correctly rounded): bit-equal to the CPU
+// restatement. out [rows, heads, head_dim]; max_len: the longest context of
+// the rows.
+void attn_exact(const float* q, float* out, const AttnLayout& L, const RowMeta& m, int rows, int max_len,
+                hipStream_t s);
 void attn_decode(const float* q, const float* gate, float* out, const AttnLayout& L, const RowMeta& m,
                  const AttnPlan& plan, int rows, hipStream_t s, const a8act::Dst* act = nullptr);
 

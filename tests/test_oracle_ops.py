@@ -150,3 +150,18 @@ def test_argmax_first_tie_rule():
     x = np.array([1.0, 3.0, np.nan, 3.0, np.inf, -1.0], np.float32)
     assert ora.argmax_first(x) == 1
     assert ora.argmax_first(np.array([np.nan, np.inf], np.float32)) == 0
+
+
+def test_exp_is_correctly_rounded_f32():
+    """The oracle's e^x (silu, sigmoid, softplus, decay, softmax) is the f32
+    nearest to the exact value: numpy's float64 exp rounded once to f32, on
+    values across the whole finite range (including the subnormal results
+    and the overflow edge)."""
+    from oracle import pyoracle as ora
+
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.uniform(-104, 89, 200000), rng.normal(0, 3, 200000), [0.0, -0.0, 1.0, -1.0, 88.72, -103.9]])
+    x = x.astype(np.float32)
+    got = ora.exp_f32(x)
+    ref = np.exp(x.astype(np.float64)).astype(np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))

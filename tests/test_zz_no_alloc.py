@@ -74,3 +74,46 @@ def test_noalloc_rejects_launch_beyond_fixed_scratch(dev):
     for p in (xd, act, y):
         dev.free(p)
     m.free()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dev):
+    """Two device handles (two HIP streams) take turns on the one fixed
+    scratch array without host synchronization: each call waits on the GPU
+    for the other stream's previous call, so every output equals the
+    allocating entry point's."""
+    import os
+
+    from pagoda_amd import Device, Matrix
+    from pagoda_amd.matrix import act_bytes, act_prep_dev
+
+    dev2 = Device(os.environ.get("PAGODA_DEVICE", "hip"))
+    n_out, n_in, r = 151936, 5120, 32  # stream-K: partial sums in scratch
+    ms = [Matrix.synth(d, 0, n_out, n_in, 3, 77, 0.02) for d in (dev, dev2)]
+    rng = np.random.default_rng(9)
+    acts, ys, refs = [], [], []
+    for k in range(4):
+        x = rng.normal(0, 1, (r, n_in)).astype(np.float32)
+        xd = dev.upload(x)
+        act = dev.alloc(act_bytes(r, n_in))
+        act_prep_dev(dev, xd, n_in, r, n_in, act)
+        dev.sync()
+        ref = dev.alloc(r * n_out * 4)
+        ms[0].gemv_act_dev(act, r, ref, n_out)
+        dev.sync()
+        refs.append(dev.download(ref, (r, n_out), np.float32))
+        dev.free(ref)
+        dev.free(xd)
+        acts.append(act)
+        ys.append(dev.alloc(r * n_out * 4))
+    for k in range(4):  # alternate streams, no host synchronization between calls
+        _noalloc(ms[k % 2], acts[k], r, ys[k], n_out)
+    dev.sync()
+    dev2.sync()
+    for k in range(4):
+        got = dev.download(ys[k], (r, n_out), np.float32)
+        np.testing.assert_array_equal(got.view(np.uint32), refs[k].view(np.uint32), err_msg=str(k))
+    for p in acts + ys:
+        dev.free(p)
+    for m in ms:
+        m.free()
+    dev2.close()
