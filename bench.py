@@ -390,7 +390,11 @@ def roofline(dev, cfg, batch):
     mfma = None
     mfile = ROOT / "profiles" / "mfma_busy.json"
     if mfile.exists():
-        mfma = json.loads(mfile.read_text())
+        pd = json.loads(mfile.read_text())["per_dispatch"]
+        pick = lambda prefix: next(v["mfma_busy"] for k, v in pd.items() if k.startswith(prefix))
+        mfma = {"a8_sk_kernel<2,2,2>": pick("a8_sk_kernel<2,2,2>"), "a8_mma_kernel_1row": pick("a8_mma_kernel"),
+                "prefill_a8_gemm_kernel<2>": pick("a8_gemm_kernel<2>"),
+                "source": "profiles/mfma_busy.json (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x CUs x 4)"}
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
             "copy_peak": copy["gbs"], "frac_of_copy": achieved / copy["gbs"], "copy_note": copy["note"],
