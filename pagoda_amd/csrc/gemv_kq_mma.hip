@@ -529,11 +529,27 @@ void q4k_launch_ks(const GemvArgs& a, int nb, hipStream_t s) {
 }
 
 template <bool XF16, int EPI>
+void q4k_launch_wide(const GemvArgs& a, int nb, hipStream_t s) {
+  if constexpr (EPI != EPI_SWIGLU) {
+    switch (q4k_split(a)) {
+      case 1: return q4k_launch<4, 1, XF16, EPI>(a, nb, s);
+      case 2: return q4k_launch<4, 2, XF16, EPI>(a, nb, s);
+      default: return q4k_launch<4, 4, XF16, EPI>(a, nb, s);
+    }
+  }
+}
+
+template <bool XF16, int EPI>
 void q4k_rows(GemvArgs a, int nrows, hipStream_t s) {
   const size_t xel = XF16 ? 2 : 4;
   while (nrows > 0) {
-    const int nb = nrows < 32 ? nrows : 32;
-    if (nb > 16) q4k_launch_ks<2, XF16, EPI>(a, nb, s);
+    // 33..64 rows as one launch of four 16-row batch tiles where the k split
+    // keeps them in registers (tall matrices: the weights stream once for all
+    // rows); a row's sums do not depend on the batch tiles
+    const bool wide = q4k_split(a) <= 4 && q4k_grid_split(a) == 1 && EPI != EPI_SWIGLU;
+    const int nb = nrows < (wide ? 64 : 32) ? nrows : (wide ? 64 : 32);
+    if (nb > 32) q4k_launch_wide<XF16, EPI>(a, nb, s);
+    else if (nb > 16) q4k_launch_ks<2, XF16, EPI>(a, nb, s);
     else q4k_launch_ks<1, XF16, EPI>(a, nb, s);
     PGD_HIP(hipGetLastError());
     nrows -= nb;
@@ -933,11 +949,31 @@ void q6k_launch_ks(const GemvArgs& a, int nb, hipStream_t s) {
 }
 
 template <bool XF16, int EPI>
+void q6k_launch_wide(const GemvArgs& a, int nb, hipStream_t s) {
+  if constexpr (EPI != EPI_SWIGLU) {
+    switch (q6k_split(a)) {
+      case 1: return q6k_launch<4, 1, XF16, EPI>(a, nb, s);
+      case 2: return q6k_launch<4, 2, XF16, EPI>(a, nb, s);
+      default: return q6k_launch<4, 4, XF16, EPI>(a, nb, s);
+    }
+  }
+}
+
+template <bool XF16, int EPI>
 void q6k_rows(GemvArgs a, int nrows, hipStream_t s) {
   const size_t xel = XF16 ? 2 : 4;
   while (nrows > 0) {
-    const int nb = nrows < 32 ? nrows : 32;
-    if (nb > 16) q6k_launch_ks<2, XF16, EPI>(a, nb, s);
+    // 33..64 rows as one launch of four 16-row batch tiles where the k split
+    // keeps them in registers (tall matrices: the weights stream once for all
+    // rows); a row's sums do not depend on the batch tiles
+    // (not the one-wave-per-tile form of very tall matrices: its four-tile
+    // registers measured slower than two 32-row launches)
+    const int ks6 = q6k_split(a);
+    const bool wide = ks6 >= 2 && ks6 <= 4 && grid_split((a.n_out + 31) / 32, a.n_in / 128, 16) == 1 &&
+                      EPI != EPI_SWIGLU;
+    const int nb = nrows < (wide ? 64 : 32) ? nrows : (wide ? 64 : 32);
+    if (nb > 32) q6k_launch_wide<XF16, EPI>(a, nb, s);
+    else if (nb > 16) q6k_launch_ks<2, XF16, EPI>(a, nb, s);
     else q6k_launch_ks<1, XF16, EPI>(a, nb, s);
     PGD_HIP(hipGetLastError());
     nrows -= nb;

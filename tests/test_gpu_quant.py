@@ -109,6 +109,26 @@ def test_batched_rows_bitwise_equal_serial(dev, fmt, n_out):
         np.testing.assert_array_equal(got.view(np.uint32), serial[:rows].view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt", [1, 2])
+@pytest.mark.parametrize("shape", [(4864, 896), (151936, 896)])
+def test_kquant_64_rows_one_launch_bitwise(dev, fmt, shape):
+    """Q4_K / Q6_K launches of 33..64 rows on tall matrices take four 16-row
+    batch tiles at once (the weights stream once): every row bitwise equal to
+    its single-row GEMV, the whole against fp64."""
+    n_out, n_in = shape
+    rng = np.random.default_rng(fmt + n_out)
+    from pagoda_amd import Matrix
+
+    m = Matrix.synth(dev, fmt, n_out, n_in, 5, 60 + fmt, 0.02)
+    x = rng.normal(0, 1, (64, n_in)).astype(np.float32)
+    full = m.gemv(x)
+    for r in (0, 17, 40, 63):
+        np.testing.assert_array_equal(full[r].view(np.uint32), m.gemv(x[r]).view(np.uint32))
+    np.testing.assert_array_equal(m.gemv(x[:45]).view(np.uint32), full[:45].view(np.uint32))
+    deq = m.dequant().astype(np.float64)
+    assert rel_err(full, x.astype(np.float64) @ deq.T) < GEMV_TOL
+
+
 def test_reference_gemv_patterns(dev):
     """qwen3_gemv.rs:1038-1112: closed-form A8 GEMVs."""
     from pagoda_amd import Matrix
