@@ -58,6 +58,11 @@ constexpr int kItemFields = 6;  // page_off, npages, row_off, first query, queri
 // DIRECT: every row of the launch has one chunk; the item normalizes and
 // writes the final output (gate, out / prepared operands) itself.
 constexpr int kSubsets = 4;
+// 16-query tiles per item of attn_split_kernel. More tiles share each loaded
+// K/V page, but their query and output slices cost registers: config 5's
+// 64-row decode measured 96.5 us per layer with 1 (110 VGPRs, 4 waves per
+// SIMD), 114.5 with 2 (150, 3 waves), 180 with 4 (226, 2 waves).
+constexpr int kSplitTiles = 1;
 constexpr int kXcds = 8;  // MI355X: accelerator complex dies, one L2 each
 
 template <int HD>
@@ -281,6 +286,218 @@ __global__ __launch_bounds__(256) void attn_item_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// head-dim split item kernel (head_dim 256)
+// ---------------------------------------------------------------------------
+// Workgroup (item, kv head), 4 waves; an item is up to kSplitTiles 16-query
+// tiles over the same chunk pages. Wave w owns head dims [64 w, 64 w + 64):
+// per page it loads that slice of K and V once for every tile, computes each
+// tile's partial scores over its dims (16 x v_mfma_f32_16x16x4_f32), and the
+// four partials meet in LDS, added in wave order, so every wave holds the
+// same scores; then each wave runs the same online-softmax update and
+// O += P V for its dims (16 MFMAs per tile). Every wave walks all pages of
+// the chunk in page order: a query's result depends only on its own row's
+// pages, never on the item it shares (batched rows equal single-row calls).
+// Registers hold a tile's query slice and output slice (16 + 16 per lane),
+// so one K/V page can feed several tiles (kSplitTiles).
+template <bool DIRECT>
+__global__ __launch_bounds__(256) void attn_split_kernel(const float* __restrict__ q, const float* __restrict__ gate,
+                                                         float* __restrict__ out, AttnLayout L, RowMeta m,
+                                                         AttnPlan plan, int G, float* __restrict__ part_o,
+                                                         float* __restrict__ part_ml, a8act::Dst act) {
+  constexpr int HD = 256, TQ = kSplitTiles;
+  constexpr int T = 16;  // QK k-steps per wave: lane (i, kq) holds d = 64 w + 16 kq + t
+  // PV n-tiles: lane (j, kq) holds d = 64 w + 4 j + nt, nt = 0..3
+  __shared__ __attribute__((aligned(16))) f4 xs[2][TQ][kSubsets][64];  // partial scores, by page parity
+  __shared__ __attribute__((aligned(16))) float tb[16][HD + 4];         // a tile's normalized outputs
+  const int total = gridDim.x, lin = blockIdx.x;
+  const int xcd = lin % kXcds, per = total / kXcds, rem = total % kXcds;
+  const int wi = xcd * per + min(xcd, rem) + lin / kXcds;
+  const int item = wi % plan.n_items, kvh = wi / plan.n_items;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, kq = lane >> 4;
+  const int* it = plan.items + (size_t)item * kItemFields;
+  const int page_off = it[0], npages = it[1], row_off = it[2], q0 = it[3], nq = it[4], chunk = it[5];
+  const int chunk_pos0 = chunk * kChunkPages * L.block;
+  const float inv_scale = 1.0f / sqrtf((float)HD);
+  const int d0 = 64 * wave;
+
+  float Q[TQ][T];
+  f4 O[TQ][4];
+  float mx[TQ], lsum[TQ];
+  int len[TQ];
+  bool qlive[TQ];
+  int lmax = 0;  // longest context of the item's live queries
+#pragma unroll
+  for (int t = 0; t < TQ; ++t) {
+    const int qi = 16 * t + j;
+    qlive[t] = qi < nq;
+    const int krow = qlive[t] ? (q0 + qi) / G : 0, g = qlive[t] ? (q0 + qi) % G : 0;
+    const int row = plan.item_rows[row_off + krow];
+    len[t] = qlive[t] ? m.pos_of_row[row] + 1 : 0;
+    lmax = max(lmax, len[t]);
+    const float* qp = q + ((size_t)row * L.heads + kvh * G + g) * HD + d0 + 16 * kq;
+#pragma unroll
+    for (int e = 0; e < T; e += 4) {
+      const float4 v = (16 * t < nq && qlive[t]) ? *reinterpret_cast<const float4*>(qp + e)
+                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      Q[t][e] = v.x;
+      Q[t][e + 1] = v.y;
+      Q[t][e + 2] = v.z;
+      Q[t][e + 3] = v.w;
+    }
+    mx[t] = -INFINITY;
+    lsum[t] = 0.0f;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) O[t][nt] = (f4){0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) lmax = max(lmax, __shfl_xor(lmax, o, 64));
+  lmax = max(lmax, 0);
+
+  float Kr[T], Vr[4][4];
+  auto page_base = [&](int k) {
+    const int page = plan.pages[page_off + min(k, npages - 1)];
+    return ((size_t)page * L.kv_heads + kvh) * L.block * HD;
+  };
+  auto load_k = [&](size_t base) {
+    const float* kp = L.k_pool + base + (size_t)j * HD + d0 + 16 * kq;
+#pragma unroll
+    for (int e = 0; e < T; e += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(kp + e);
+      Kr[e] = v.x;
+      Kr[e + 1] = v.y;
+      Kr[e + 2] = v.z;
+      Kr[e + 3] = v.w;
+    }
+  };
+  auto load_v = [&](size_t base) {
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const float4 v = *reinterpret_cast<const float4*>(L.v_pool + base + (size_t)(4 * kq + s2) * HD + d0 + 4 * j);
+      Vr[s2][0] = v.x;
+      Vr[s2][1] = v.y;
+      Vr[s2][2] = v.z;
+      Vr[s2][3] = v.w;
+    }
+  };
+  load_k(page_base(0));
+  load_v(page_base(0));
+  for (int k = 0; k < npages; ++k) {
+    const int par = k & 1;
+    // ---- partial scores over this wave's dims, every tile ----
+#pragma unroll
+    for (int t = 0; t < TQ; ++t) {
+      if (16 * t >= nq) break;
+      f4 Sa[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int e = 0; e < T; ++e) Sa[e & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(Kr[e], Q[t][e], Sa[e & 3], 0, 0, 0);
+      xs[par][t][wave][lane] = (Sa[0] + Sa[1]) + (Sa[2] + Sa[3]);
+    }
+    load_k(page_base(k + 1));
+    __syncthreads();
+    const int pos0 = chunk_pos0 + k * L.block + 4 * kq;  // lane (j, kq) holds positions 4 kq + r
+    if (pos0 - 4 * kq + L.block > lmax) {  // a page with unwritten slots: 0 * NaN is not 0
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2)
+        if (pos0 + s2 >= lmax)
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) Vr[s2][nt] = 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < TQ; ++t) {
+      if (16 * t >= nq) break;
+      const f4 S = ((xs[par][t][0][lane] + xs[par][t][1][lane]) + xs[par][t][2][lane]) + xs[par][t][3][lane];
+      float sc[4];
+      float pm = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[r] = pos0 + r < len[t] ? S[r] * inv_scale : -INFINITY;
+        pm = fmaxf(pm, sc[r]);
+      }
+      pm = fmaxf(pm, __shfl_xor(pm, 16, 64));
+      pm = fmaxf(pm, __shfl_xor(pm, 32, 64));
+      const float mn = fmaxf(mx[t], pm);
+      const float alpha = mn == -INFINITY ? 1.0f : expf(mx[t] - mn);
+      float ps = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[r] = (qlive[t] && sc[r] != -INFINITY) ? expf(sc[r] - mn) : 0.0f;
+        ps += sc[r];
+      }
+      ps += __shfl_xor(ps, 16, 64);
+      ps += __shfl_xor(ps, 32, 64);
+      lsum[t] = lsum[t] * alpha + ps;
+      mx[t] = mn;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float al = __shfl(alpha, 4 * kq + r, 64);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) O[t][nt][r] *= al;
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          O[t][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[s2], Vr[s2][nt], O[t][nt], 0, 0, 0);
+    }
+    load_v(page_base(k + 1));
+  }
+  // ---- outputs: lane (j, kq) holds O[query 4 kq + r][64 w + 4 j + nt] ----
+#pragma unroll
+  for (int t = 0; t < TQ; ++t) {
+    if (16 * t >= nq) break;
+    if constexpr (DIRECT) {
+      // normalize into LDS, then thread u = (query n, 16-dim slice) writes
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float lt = __shfl(lsum[t], 4 * kq + r, 64);
+        *reinterpret_cast<float4*>(&tb[4 * kq + r][d0 + 4 * j]) =
+            make_float4(O[t][0][r] / lt, O[t][1][r] / lt, O[t][2][r] / lt, O[t][3][r] / lt);
+      }
+      __syncthreads();
+      const int n = tid >> 4, s16 = (tid & 15) * 16;
+      const int qo = 16 * t + n;
+      const bool live = qo < nq;
+      const int qa = q0 + (live ? qo : 0);
+      const int orow = plan.item_rows[row_off + qa / G], head = kvh * G + qa % G;
+      const size_t oo = ((size_t)orow * L.heads + head) * HD + s16;
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        v[e] = tb[n][s16 + e];
+        if (gate && live) v[e] *= 1.0f / (1.0f + expf(-gate[oo + e]));
+      }
+      if (out && live) {
+#pragma unroll
+        for (int e = 0; e < 16; e += 4)
+          *reinterpret_cast<float4*>(out + oo + e) = make_float4(v[e], v[e + 1], v[e + 2], v[e + 3]);
+      }
+      if (act.XA) {
+        const int col = head * HD + s16;
+        a8act::emit_slice(act, orow, col >> 6, (col >> 4) & 3, v, live);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qo = 16 * t + 4 * kq + r;
+        if (qo >= nq) continue;
+        const int qa = q0 + qo;
+        const int slot = row_off + qa / G, go = qa % G;
+        float* po = part_o + (((size_t)slot * L.kv_heads + kvh) * G + go) * HD + d0 + 4 * j;
+        *reinterpret_cast<float4*>(po) = make_float4(O[t][0][r], O[t][1][r], O[t][2][r], O[t][3][r]);
+      }
+      if (wave == 0 && kq == 0 && 16 * t + j < nq) {
+        const int qa = q0 + 16 * t + j;
+        float* pml = part_ml + (((size_t)(row_off + qa / G) * L.kv_heads + kvh) * G + qa % G) * 2;
+        pml[0] = mx[t];
+        pml[1] = lsum[t];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // merge kernel: workgroup (row, kv head), 256 threads over the G x HD outputs
 // ---------------------------------------------------------------------------
 constexpr int kMergeMax = 1024;  // chunk slots per row, staged in LDS
@@ -349,14 +566,22 @@ void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L,
   const size_t ml_floats = (size_t)plan.n_slots * L.kv_heads * G * 2;
   // one chunk per row (n_slots == rows): the items finish the rows themselves
   if (plan.n_slots == rows) {
-    hipLaunchKernelGGL((attn_item_kernel<HD, true>), dim3(plan.n_items * L.kv_heads), dim3(256), 0, s, q, gate, out,
-                       L, m, plan, G, nullptr, nullptr, act);
+    if constexpr (HD == 256)
+      hipLaunchKernelGGL((attn_split_kernel<true>), dim3(plan.n_items * L.kv_heads), dim3(256), 0, s, q, gate, out,
+                         L, m, plan, G, nullptr, nullptr, act);
+    else
+      hipLaunchKernelGGL((attn_item_kernel<HD, true>), dim3(plan.n_items * L.kv_heads), dim3(256), 0, s, q, gate,
+                         out, L, m, plan, G, nullptr, nullptr, act);
     return;
   }
   PGD_CHECK(plan.max_row_slots <= kMergeMax, kErrShape, "attention context too long for the merge");
   float* ws = static_cast<float*>(gemv::gemv_scratch(s, (o_floats + ml_floats) * sizeof(float), 4));
-  hipLaunchKernelGGL((attn_item_kernel<HD, false>), dim3(plan.n_items * L.kv_heads), dim3(256), 0, s, q, gate, out,
-                     L, m, plan, G, ws, ws + o_floats, act);
+  if constexpr (HD == 256)
+    hipLaunchKernelGGL((attn_split_kernel<false>), dim3(plan.n_items * L.kv_heads), dim3(256), 0, s, q, gate, out,
+                       L, m, plan, G, ws, ws + o_floats, act);
+  else
+    hipLaunchKernelGGL((attn_item_kernel<HD, false>), dim3(plan.n_items * L.kv_heads), dim3(256), 0, s, q, gate,
+                       out, L, m, plan, G, ws, ws + o_floats, act);
   hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(rows, L.kv_heads, G), dim3(HD), 0, s,
                      gate, out, L, plan, G, ws, ws + o_floats, act);
 }
@@ -367,7 +592,10 @@ void attn_hd(const float* q, const float* gate, float* out, const AttnLayout& L,
 // host: plan
 // ---------------------------------------------------------------------------
 void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, const int* block_tables,
-                     int max_blocks, int block, int group, std::vector<int>& out) {
+                     int max_blocks, int block, int group, int head_dim, std::vector<int>& out) {
+  // queries per work item: one 16-query tile (head_dim 64, 128) or up to
+  // kSplitTiles tiles over the same pages (head_dim 256, attn_split_kernel)
+  const int qpi = head_dim == 256 ? 16 * kSplitTiles : 16;
   PGD_CHECK(group > 0 && group <= 64 && block == 16, kErrShape, "attention plan: group <= 64 heads, pages of 16");
   struct Key {
     int chunk;
@@ -421,9 +649,9 @@ void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, con
       item_rows.push_back(mem[k]);
     }
     const int nqs = (int)mem.size() * group;
-    for (int qs = 0; qs < nqs; qs += 16)
+    for (int qs = 0; qs < nqs; qs += qpi)
       items.insert(items.end(), {page_off, (int)keys[gi].pages.size(), base + qs / group, qs % group,
-                                 std::min(16, nqs - qs), keys[gi].chunk});
+                                 std::min(qpi, nqs - qs), keys[gi].chunk});
   }
   // row -> slots in chunk order
   std::vector<int> row_slot_off(rows + 1), row_slots;

@@ -373,7 +373,8 @@ int pgd_attn_decode_dev(pgd_dev* dev, int heads, int kv_heads, int head_dim, int
     std::vector<int> h_bt((size_t)nseq * max_blocks);
     PGD_HIP(hipMemcpy(h_bt.data(), block_tables, h_bt.size() * sizeof(int), hipMemcpyDeviceToHost));
     std::vector<int> plan;
-    build_attn_plan(h_seq.data(), h_pos.data(), rows, h_bt.data(), max_blocks, block, heads / kv_heads, plan);
+    build_attn_plan(h_seq.data(), h_pos.data(), rows, h_bt.data(), max_blocks, block, heads / kv_heads, head_dim,
+                    plan);
     DevBuf d_plan(plan.size() * sizeof(int));
     PGD_HIP(hipMemcpy(d_plan.p, plan.data(), plan.size() * sizeof(int), hipMemcpyHostToDevice));
     attn_decode(q, gate, out, L, m, attn_plan_view(plan.data(), d_plan.as<int>()), rows, dev->stream);

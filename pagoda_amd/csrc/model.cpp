@@ -482,7 +482,7 @@ void step(Model& m, Session* const* sess, const uint32_t* toks, const int* n, in
       }
     }
     build_attn_plan(p_seq.data(), p_pos.data(), rows, p_bt.data(), (int)max_blocks, c.kv_block, c.heads / c.kv_heads,
-                    plan);
+                    c.head_dim, plan);
   }
   // ---- host metadata, one upload ----
   size_t off_seq = 0;

@@ -131,7 +131,7 @@ struct AttnPlan {
 // Plan of one step as one int array (header + sections); the same array is
 // uploaded as is, and attn_plan_view maps the host header onto its device copy.
 void build_attn_plan(const int* seq_of_row, const int* pos_of_row, int rows, const int* block_tables,
-                     int max_blocks, int block, int group, std::vector<int>& out);
+                     int max_blocks, int block, int group, int head_dim, std::vector<int>& out);
 AttnPlan attn_plan_view(const int* host, const int* dev);
 // The same attention in the CPU path's exact operation order (sequential dot,
 // sum and weighted sum; exp correctly rounded): bit-equal to the CPU
