@@ -711,7 +711,7 @@ constexpr int kExactThreads = 256;
 constexpr int kExactChunkFloats = 8192;  // V rows staged per round: 32 KiB
 __global__ __launch_bounds__(kExactThreads) void attn_exact_kernel(const float* __restrict__ q,
                                                                    float* __restrict__ out, AttnLayout L, RowMeta m) {
-  extern __shared__ float sc[];  // [len] scores, then weights | V chunk [kExactChunkFloats / hd][hd]
+  extern __shared__ __attribute__((aligned(16))) float sc[];  // [len] scores, then weights | V chunk [kExactChunkFloats / hd][hd]
   __shared__ float qs[256];
   __shared__ float red[kExactThreads / 64];
   __shared__ float s_sum;
@@ -722,6 +722,16 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_kernel(const float* 
   float* vs = sc + m.max_blocks * L.block;
   const float* qh = q + ((size_t)r * L.heads + h) * hd;
   for (int i = tid; i < hd; i += kExactThreads) qs[i] = qh[i];
+  const int chunk = kExactChunkFloats / hd;
+  // V rows of the first chunk, staged while the scores are computed
+  auto stage_v = [&](int p0, int n) {
+    for (int e = tid * 4; e < n * hd; e += kExactThreads * 4) {
+      const int p = p0 + e / hd, i = e % hd;
+      const float* vr = L.v_pool + (((size_t)bt[p / L.block] * L.kv_heads + kvh) * L.block + (p % L.block)) * hd;
+      *reinterpret_cast<float4*>(vs + e) = *reinterpret_cast<const float4*>(vr + i);
+    }
+  };
+  stage_v(0, min(chunk, len));
   __syncthreads();
   const float scale = sqrtf((float)hd);
   float mx = -INFINITY;
@@ -747,26 +757,44 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_kernel(const float* 
   for (int p = tid; p < len; p += kExactThreads) sc[p] = exp_cr(sc[p] - mx);
   __syncthreads();
   if (tid == 0) {
+    // in position order; four at a time from LDS so the loads run ahead of
+    // the dependent additions
     float sum = 0.0f;
-    for (int p = 0; p < len; ++p) sum += sc[p];
+    int p = 0;
+    for (; p + 4 <= len; p += 4) {
+      const float4 e = *reinterpret_cast<const float4*>(sc + p);
+      sum += e.x;
+      sum += e.y;
+      sum += e.z;
+      sum += e.w;
+    }
+    for (; p < len; ++p) sum += sc[p];
     s_sum = sum;
   }
   __syncthreads();
   const float sum = s_sum;
   for (int p = tid; p < len; p += kExactThreads) sc[p] = sc[p] / sum;
   float acc = 0.0f;
-  const int chunk = kExactChunkFloats / hd;
   for (int p0 = 0; p0 < len; p0 += chunk) {
     const int n = min(chunk, len - p0);
-    __syncthreads();  // the weights are written / the previous chunk is consumed
-    for (int e = tid * 4; e < n * hd; e += kExactThreads * 4) {
-      const int p = p0 + e / hd, i = e % hd;
-      const float* vr = L.v_pool + (((size_t)bt[p / L.block] * L.kv_heads + kvh) * L.block + (p % L.block)) * hd;
-      *reinterpret_cast<float4*>(vs + e) = *reinterpret_cast<const float4*>(vr + i);
+    if (p0 > 0) {
+      __syncthreads();  // the previous chunk is consumed
+      stage_v(p0, n);
     }
-    __syncthreads();
-    if (tid < hd)
-      for (int t = 0; t < n; ++t) acc += sc[p0 + t] * vs[t * hd + tid];
+    __syncthreads();  // the weights are written, the chunk is staged
+    if (tid < hd) {
+      int t = 0;
+      for (; t + 4 <= n; t += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(sc + p0 + t);
+        const float v0 = vs[t * hd + tid], v1 = vs[(t + 1) * hd + tid];
+        const float v2 = vs[(t + 2) * hd + tid], v3 = vs[(t + 3) * hd + tid];
+        acc += w4.x * v0;
+        acc += w4.y * v1;
+        acc += w4.z * v2;
+        acc += w4.w * v3;
+      }
+      for (; t < n; ++t) acc += sc[p0 + t] * vs[t * hd + tid];
+    }
   }
   if (tid < hd) out[((size_t)r * L.heads + h) * hd + tid] = acc;
 }
