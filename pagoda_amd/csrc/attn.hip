@@ -706,49 +706,96 @@ AttnPlan attn_plan_view(const int* host, const int* dev) {
 // that order; used by the Qwen2 arithmetic that reproduces the reference CPU
 // path (candle's quantized matmul). Scores live in LDS: the context is at
 // most kExactMax positions.
-constexpr int kExactMax = 32256;
+constexpr int kExactMax = 30720;
 constexpr int kExactThreads = 256;
 constexpr int kExactChunkFloats = 8192;  // V rows staged per round: 32 KiB
+template <int HD>
 __global__ __launch_bounds__(kExactThreads) void attn_exact_kernel(const float* __restrict__ q,
                                                                    float* __restrict__ out, AttnLayout L, RowMeta m) {
-  extern __shared__ __attribute__((aligned(16))) float sc[];  // [len] scores, then weights | V chunk [kExactChunkFloats / hd][hd]
-  __shared__ float qs[256];
+  extern __shared__ __attribute__((aligned(16))) float sc[];  // [len] scores, then weights | V chunk [kExactChunkFloats / HD][HD] | page ids
+  __shared__ __attribute__((aligned(16))) float qs[HD];
   __shared__ float red[kExactThreads / 64];
   __shared__ float s_sum;
   const int r = blockIdx.y, h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int hd = L.head_dim, kvh = h / (L.heads / L.kv_heads);
+  const int kvh = h / (L.heads / L.kv_heads);
   const int seq = m.seq_of_row[r], len = m.pos_of_row[r] + 1;
-  const int* bt = m.block_tables + (size_t)seq * m.max_blocks;
   float* vs = sc + m.max_blocks * L.block;
-  const float* qh = q + ((size_t)r * L.heads + h) * hd;
-  for (int i = tid; i < hd; i += kExactThreads) qs[i] = qh[i];
-  const int chunk = kExactChunkFloats / hd;
-  // V rows of the first chunk, staged while the scores are computed
-  auto stage_v = [&](int p0, int n) {
-    for (int e = tid * 4; e < n * hd; e += kExactThreads * 4) {
-      const int p = p0 + e / hd, i = e % hd;
-      const float* vr = L.v_pool + (((size_t)bt[p / L.block] * L.kv_heads + kvh) * L.block + (p % L.block)) * hd;
-      *reinterpret_cast<float4*>(vs + e) = *reinterpret_cast<const float4*>(vr + i);
-    }
+  const float* qh = q + ((size_t)r * L.heads + h) * HD;
+  // the sequence's page ids go to LDS first, so every K / V row address after
+  // them is one LDS read away rather than a dependent global load
+  const int nblk = (len + L.block - 1) / L.block;
+  int* bt = reinterpret_cast<int*>(vs + kExactChunkFloats);
+  {
+    const int* src = m.block_tables + (size_t)seq * m.max_blocks;
+    for (int i = tid; i < nblk; i += kExactThreads) bt[i] = src[i];
+  }
+  for (int i = tid; i < HD; i += kExactThreads) qs[i] = qh[i];
+  constexpr int chunk = kExactChunkFloats / HD;
+  constexpr int KV = kExactChunkFloats / (kExactThreads * 4);
+  // V rows p0 .. p0 + n - 1: the thread's loads into registers (eight named
+  // float4, so they stay in registers), then (after other work if any) its
+  // stores into LDS. Every load is issued (past the end it re-reads row p0).
+  static_assert(KV == 8, "eight V loads per thread and chunk");
+  auto ldv = [&](int p0, int n, int k) -> float4 {
+    const int e = tid * 4 + k * kExactThreads * 4, ec = e < n * HD ? e : 0;
+    const int p = p0 + ec / HD, i = ec % HD;
+    const float* vr = L.v_pool + (((size_t)bt[p / L.block] * L.kv_heads + kvh) * L.block + (p % L.block)) * HD;
+    return *reinterpret_cast<const float4*>(vr + i);
   };
-  stage_v(0, min(chunk, len));
+  auto stv = [&](int n, int k, const float4& v) {
+    const int e = tid * 4 + k * kExactThreads * 4;
+    if (e < n * HD) *reinterpret_cast<float4*>(vs + e) = v;
+  };
+  float4 v0, v1, v2, v3, v4, v5, v6, v7;
+  auto load_v = [&](int p0, int n) {
+    v0 = ldv(p0, n, 0);
+    v1 = ldv(p0, n, 1);
+    v2 = ldv(p0, n, 2);
+    v3 = ldv(p0, n, 3);
+    v4 = ldv(p0, n, 4);
+    v5 = ldv(p0, n, 5);
+    v6 = ldv(p0, n, 6);
+    v7 = ldv(p0, n, 7);
+  };
+  auto store_v = [&](int n) {
+    stv(n, 0, v0);
+    stv(n, 1, v1);
+    stv(n, 2, v2);
+    stv(n, 3, v3);
+    stv(n, 4, v4);
+    stv(n, 5, v5);
+    stv(n, 6, v6);
+    stv(n, 7, v7);
+  };
   __syncthreads();
-  const float scale = sqrtf((float)hd);
+  // the first V chunk is in flight while the scores are computed
+  const int n0 = min(chunk, len);
+  load_v(0, n0);
+  const float scale = sqrtf((float)HD);
   float mx = -INFINITY;
   for (int p = tid; p < len; p += kExactThreads) {
-    const float* kr = L.k_pool + (((size_t)bt[p / L.block] * L.kv_heads + kvh) * L.block + (p % L.block)) * hd;
+    const float* kr = L.k_pool + (((size_t)bt[p / L.block] * L.kv_heads + kvh) * L.block + (p % L.block)) * HD;
     float dot = 0.0f;
-    for (int i = 0; i < hd; i += 4) {
-      const float4 k4 = *reinterpret_cast<const float4*>(kr + i);
-      dot += qs[i] * k4.x;
-      dot += qs[i + 1] * k4.y;
-      dot += qs[i + 2] * k4.z;
-      dot += qs[i + 3] * k4.w;
+    // the K row 64 values at a time, all of a part's loads in flight together
+#pragma unroll
+    for (int c = 0; c < HD; c += 64) {
+      float4 k4[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) k4[i] = *reinterpret_cast<const float4*>(kr + c + 4 * i);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float4 q4 = *reinterpret_cast<const float4*>(qs + c + 4 * i);
+        dot += q4.x * k4[i].x;
+        dot += q4.y * k4[i].y;
+        dot += q4.z * k4[i].z;
+        dot += q4.w * k4[i].w;
+      }
     }
     const float s = dot / scale;
     sc[p] = s;
     mx = fmaxf(mx, s);
   }
+  store_v(n0);
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
   if (lane == 0) red[wv] = mx;
   __syncthreads();
@@ -757,16 +804,21 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_kernel(const float* 
   for (int p = tid; p < len; p += kExactThreads) sc[p] = exp_cr(sc[p] - mx);
   __syncthreads();
   if (tid == 0) {
-    // in position order; four at a time from LDS so the loads run ahead of
+    // in position order; 16 at a time from LDS so the loads run ahead of
     // the dependent additions
     float sum = 0.0f;
     int p = 0;
-    for (; p + 4 <= len; p += 4) {
-      const float4 e = *reinterpret_cast<const float4*>(sc + p);
-      sum += e.x;
-      sum += e.y;
-      sum += e.z;
-      sum += e.w;
+    for (; p + 16 <= len; p += 16) {
+      float4 e[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) e[u] = *reinterpret_cast<const float4*>(sc + p + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        sum += e[u].x;
+        sum += e[u].y;
+        sum += e[u].z;
+        sum += e[u].w;
+      }
     }
     for (; p < len; ++p) sum += sc[p];
     s_sum = sum;
@@ -778,45 +830,65 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_kernel(const float* 
   for (int p0 = 0; p0 < len; p0 += chunk) {
     const int n = min(chunk, len - p0);
     if (p0 > 0) {
+      load_v(p0, n);
       __syncthreads();  // the previous chunk is consumed
-      stage_v(p0, n);
+      store_v(n);
     }
     __syncthreads();  // the weights are written, the chunk is staged
-    if (tid < hd) {
+    if (tid < HD) {
+      // 16 positions per round: all their LDS reads issued before the
+      // dependent additions (position order within and across rounds)
       int t = 0;
-      for (; t + 4 <= n; t += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(sc + p0 + t);
-        const float v0 = vs[t * hd + tid], v1 = vs[(t + 1) * hd + tid];
-        const float v2 = vs[(t + 2) * hd + tid], v3 = vs[(t + 3) * hd + tid];
-        acc += w4.x * v0;
-        acc += w4.y * v1;
-        acc += w4.z * v2;
-        acc += w4.w * v3;
+      for (; t + 16 <= n; t += 16) {
+        float4 w4[4];
+        float vv[16];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w4[u] = *reinterpret_cast<const float4*>(sc + p0 + t + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) vv[u] = vs[(t + u) * HD + tid];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          acc += w4[u].x * vv[4 * u];
+          acc += w4[u].y * vv[4 * u + 1];
+          acc += w4[u].z * vv[4 * u + 2];
+          acc += w4[u].w * vv[4 * u + 3];
+        }
       }
-      for (; t < n; ++t) acc += sc[p0 + t] * vs[t * hd + tid];
+      for (; t < n; ++t) acc += sc[p0 + t] * vs[t * HD + tid];
     }
   }
-  if (tid < hd) out[((size_t)r * L.heads + h) * hd + tid] = acc;
+  if (tid < HD) out[((size_t)r * L.heads + h) * HD + tid] = acc;
+}
+
+template <int HD>
+void launch_exact(const float* q, float* out, const AttnLayout& L, const RowMeta& m, int rows, int max_len,
+                  hipStream_t s) {
+  // scores | V chunk | page ids
+  const size_t lds = ((size_t)max_len + kExactChunkFloats + m.max_blocks) * sizeof(float);
+  if (lds > 64 * 1024) {
+    static bool set = false;
+    if (!set) {
+      PGD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_exact_kernel<HD>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024));
+      set = true;
+    }
+  }
+  hipLaunchKernelGGL(attn_exact_kernel<HD>, dim3(L.heads, rows), dim3(kExactThreads), lds, s, q, out, L, m);
 }
 
 void attn_exact(const float* q, float* out, const AttnLayout& L, const RowMeta& m, int rows, int max_len,
                 hipStream_t s) {
   PGD_CHECK(L.kv_heads > 0 && L.heads % L.kv_heads == 0, kErrShape, "heads must be a multiple of kv_heads");
-  PGD_CHECK(L.head_dim % 4 == 0 && L.head_dim <= 256, kErrShape, "exact-order attention: head_dim <= 256");
-  PGD_CHECK(max_len <= kExactMax && max_len == m.max_blocks * L.block, kErrShape,
-            "exact-order attention holds at most " + std::to_string(kExactMax) + " positions");
+  PGD_CHECK(L.head_dim == 64 || L.head_dim == 128 || L.head_dim == 256, kErrShape,
+            "exact-order attention: head_dim 64, 128 or 256");
+  PGD_CHECK(max_len <= kExactMax && max_len == m.max_blocks * L.block &&
+                (size_t)(max_len + kExactChunkFloats + m.max_blocks) * sizeof(float) <= 160 * 1024,
+            kErrShape, "exact-order attention holds at most " + std::to_string(kExactMax) + " positions");
   if (rows <= 0) return;
-  const size_t lds = ((size_t)max_len + kExactChunkFloats) * sizeof(float);
-  if (lds > 64 * 1024) {
-    static bool set = false;
-    if (!set) {
-      PGD_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_exact_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)((kExactMax + kExactChunkFloats) * sizeof(float))));
-      set = true;
-    }
-  }
-  hipLaunchKernelGGL(attn_exact_kernel, dim3(L.heads, rows), dim3(kExactThreads), lds, s, q, out, L, m);
+  if (L.head_dim == 64) launch_exact<64>(q, out, L, m, rows, max_len, s);
+  else if (L.head_dim == 128) launch_exact<128>(q, out, L, m, rows, max_len, s);
+  else launch_exact<256>(q, out, L, m, rows, max_len, s);
   PGD_HIP(hipGetLastError());
 }
 
