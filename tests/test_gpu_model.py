@@ -92,6 +92,35 @@ def test_prefill_then_greedy_decode_matches_oracle(which, request):
     np.testing.assert_array_equal(s.forward([]), got)
 
 
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_qwen2_cpu_arithmetic_bitwise_every_head_dim(dev, head_dim):
+    """The Qwen2 default arithmetic (candle's quantized matmul and the CPU
+    path's attention order, qwen2_gguf.rs:252-289) at every head size the
+    exact-order attention kernel takes: prompt and 12 greedy steps bit-equal
+    to the oracle's restatement on the same weights."""
+    from pagoda_amd.engine import ARITH_CPU_Q8, Model, argmax_first
+
+    cfg = small2(head_dim=head_dim, rotary_dim=head_dim, n_layers=2)
+    print(f"qwen2 cpu_q8 head_dim {head_dim}", flush=True)
+    m = Model.synth(dev, cfg, 21)
+    m.set_kquant_arith(ARITH_CPU_Q8)
+    o = oracle2(cfg, 21)
+    rng = np.random.default_rng(head_dim)
+    prompt = rng.integers(0, cfg.vocab, 37)
+    s = m.new_session()
+    oc = o.new_cache()
+    got = s.forward(prompt)
+    ref = o.forward(prompt, oc)
+    for step in range(12):
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32), err_msg=f"step {step}")
+        t = argmax_first(got)
+        assert t == ora.argmax_first(ref)
+        got = s.forward([t])
+        ref = o.forward([t], oc)
+    s.free()
+    m.free()
+
+
 @pytest.mark.parametrize("which", ["m35", "m2"])
 def test_ragged_batch_bitwise_equals_serial(which, request):
     """Batched step == per-session forwards (pagoda/tests/batch_tests.rs:217-242).
